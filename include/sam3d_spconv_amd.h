@@ -1,0 +1,198 @@
+/*
+ * sam3d_spconv_amd.h -- C ABI of the MI355X (gfx950) sparse-voxel
+ * convolution library (libsam3d_spconv_amd.so).
+ *
+ * Scope: the submanifold 3x3x3 and stride-2 SparseConv3d path of SAM 3D
+ * Objects -- kernel-map build, gather -> implicit GEMM -> store, stride-2
+ * downsample / subdivide maps, Q8_0 weights, scatter-mean.  Citations are
+ * relative to the reference repository (Asher-1/sam-3d-objects-ggml):
+ *   PATCH = cpp_ggml/third_party/ggml-patches/0001-sam3d-ggml-combined.patch
+ *   SRC   = cpp_ggml/src
+ *   SP    = sam3d_objects/model/backbone/tdfy_dit/modules/sparse
+ *
+ * Conventions
+ *   - Every buffer is caller-owned device memory (hipMalloc / torch).  The
+ *     library allocates nothing; scratch space comes from a caller-owned
+ *     workspace whose size the *_workspace_bytes queries return.
+ *   - Calls are asynchronous on `stream` (a hipStream_t; 0 = null stream)
+ *     unless documented as synchronising.  Calls on one stream are ordered;
+ *     separate workspaces make calls on different streams independent.
+ *   - Every entry point returns an spc_status; spc_last_error() describes
+ *     the most recent failure of the calling thread.
+ *   - Coordinates are int32 (b, x, y, z) rows.  The GPU key packing accepts
+ *     b in [0, 262144) and x, y, z in [0, 32768); anything else is
+ *     SPC_BAD_COORD (SparseTensor's contract is [0, 1023], SP/basic.py:33).
+ *   - Offsets o = kd*9 + kh*3 + kw with (dx,dy,dz) = (o/9-1, (o/3)%3-1,
+ *     o%3-1); centre tap o = 13 (SRC/sparse_ops.cpp:108).
+ */
+#ifndef SAM3D_SPCONV_AMD_H
+#define SAM3D_SPCONV_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* spc_stream_t; /* hipStream_t */
+
+typedef enum {
+    SPC_OK = 0,
+    SPC_BAD_SHAPE = 1,   /* sizes / channel counts the kernels do not support   */
+    SPC_BAD_COORD = 2,   /* coordinate outside the accepted range               */
+    SPC_DUP_COORD = 3,   /* duplicate coordinate where uniqueness is required   */
+    SPC_OOM = 4,         /* workspace too small                                 */
+    SPC_HIP_ERROR = 5,   /* a HIP runtime call failed                           */
+    SPC_BAD_ARG = 6      /* null pointer / unknown enum value                   */
+} spc_status;
+
+typedef enum { SPC_F32 = 0, SPC_F16 = 1, SPC_BF16 = 2, SPC_Q8_0 = 3 } spc_dtype;
+
+/* Map-build flags. */
+#define SPC_MAP_MESH 1u /* build_mesh_conv_table semantics: coords must lie in
+                           [0, resolution) and be unique (SRC/sparse_ops.cpp:312-329) */
+#define SPC_MAP_SYNC 2u /* synchronise `stream` and return the device-side status */
+
+/* Index-table layouts accepted by spc_sparse_conv. */
+#define SPC_IDX_TOKEN_MAJOR 0  /* [n_out, ntaps]; SRC/sparse_ops.cpp:102-116   */
+#define SPC_IDX_OFFSET_MAJOR 1 /* [ntaps, n_out]; SRC/sparse_ops.cpp:124-133   */
+
+const char* spc_last_error(void);
+const char* spc_status_string(int status);
+int spc_version(void);
+
+/* ------------------------------------------------------------------------
+ * Kernel map (submanifold 3x3x3 neighbour tables).
+ * Replaces SlatTables::build's conv tables (SRC/sparse_ops.cpp:93-155;
+ * declared SRC/sparse_ops.hpp:24-39,46-47) and build_mesh_conv_table
+ * (SRC/sparse_ops.cpp:312-346).  Bit-exact outputs:
+ *   token_major  [n*27]  row of coord+delta(o) in the same batch, else n
+ *   offset_major [27*n]  the same, offset-major, -1 when missing
+ *   mask_sorted  [n]     27-bit valid-tap masks in stable ascending order
+ *   argsort      [n]     std::stable_sort permutation of tokens by mask
+ *   mask_natural [n]     the masks in token order (not a reference table)
+ * Any output pointer may be NULL.  Duplicate coords without SPC_MAP_MESH
+ * follow std::map::emplace: the first row owns the key, later duplicates
+ * keep 27 sentinels and mask 0.  `resolution` is only read with
+ * SPC_MAP_MESH.  Device-side errors (BAD_COORD, DUP_COORD) are returned
+ * only with SPC_MAP_SYNC; otherwise read them with spc_read_status.
+ * ------------------------------------------------------------------------ */
+size_t spc_map_workspace_bytes(int64_t n);
+int spc_map_build(spc_stream_t stream, const int32_t* coords, int64_t n, int32_t resolution,
+                  uint32_t flags, int32_t* token_major, int32_t* offset_major,
+                  int32_t* mask_sorted, int32_t* argsort, int32_t* mask_natural,
+                  void* workspace, size_t workspace_bytes);
+
+/* Reads (and clears) the device status word of a map / downsample /
+ * subdivide workspace.  Synchronises `stream`. */
+int spc_read_status(spc_stream_t stream, void* workspace);
+
+/* ------------------------------------------------------------------------
+ * Stride-2 downsample map.  Replaces the coarse section of
+ * SlatTables::build (SRC/sparse_ops.cpp:27-81; fields SRC/sparse_ops.hpp:
+ * 15-23) and SparseDownsample's unique/inverse (SP/spatial.py:20-65).
+ * Coarse key (b, x/2, y/2, z/2); coarse rows in lexicographic key order.
+ *   fine_to_coarse [nf]          coarse row of each fine row
+ *   coarse_coords  [nc, 4]       int32 (b, x/2, y/2, z/2)
+ *   children       [8*nc]        fine rows, ascending, compacted, padded nf
+ *   counts         [nc] float    |children| + 1 (mean over the zero row too)
+ *   stride2_taps   [nc*8]        fine row at tap k = (x&1)*4+(y&1)*2+(z&1),
+ *                                nf if absent (input of the 2x2x2 stride-2
+ *                                conv; duplicates at one tap -> DUP_COORD)
+ * Output buffers are sized for the upper bound nc = nf; the call
+ * synchronises `stream` and writes nc to *nc_out (host).  Fine coords must
+ * satisfy 0 <= b < n_batch and 0 <= x,y,z < resolution (<= 32768).
+ * ------------------------------------------------------------------------ */
+size_t spc_downsample_workspace_bytes(int64_t nf);
+int spc_downsample_map(spc_stream_t stream, const int32_t* coords, int64_t nf, int64_t n_batch,
+                       int32_t resolution, int32_t* fine_to_coarse, int32_t* coarse_coords,
+                       int32_t* children, float* counts, int32_t* stride2_taps,
+                       int64_t* nc_out, void* workspace, size_t workspace_bytes);
+
+/* ------------------------------------------------------------------------
+ * Subdivide map.  Replaces subdivide_mesh_level (SRC/sparse_ops.cpp:
+ * 348-371) and SparseSubdivide's coordinates (SP/spatial.py:108-124).
+ * Child c = dx*4 + dy*2 + dz of parent p has coords (b, 2x+dx, 2y+dy, 2z+dz)
+ * and row p*8+c; with `keep` ([8n] bytes, nonzero = keep) survivors stay in
+ * parent-major order.  parent[m] = the parent row of each output row.
+ * Outputs sized for 8n rows; synchronises and writes m to *m_out.
+ * ------------------------------------------------------------------------ */
+size_t spc_subdivide_workspace_bytes(int64_t n);
+int spc_subdivide_map(spc_stream_t stream, const int32_t* coords, int64_t n, const uint8_t* keep,
+                      int32_t* out_coords, int32_t* parent, int64_t* m_out, void* workspace,
+                      size_t workspace_bytes);
+
+/* ------------------------------------------------------------------------
+ * Sparse convolution: gather -> implicit GEMM (MFMA) -> store.
+ * Same arithmetic as the ggml CPU op ggml_compute_forward_sam3d_sparse_
+ * conv_f16 (PATCH:217-265) -- F32 accumulation of bias + sum over valid
+ * taps and channels, one rounding to the output dtype -- and the same
+ * contract as the CUDA bridge sam3d_spconv_f16_forward (SPCONV bridge,
+ * cpp_ggml/third_party/sam3d-spconv/include/sam3d_spconv_bridge.cuh:10-21),
+ * generalised to any tap count (27 submanifold, 8 stride-2):
+ *   y[t, co] = bias[co] + sum_{o, s = idx(t,o) in [0,n_in)} sum_c
+ *              w[co, o, c] * x[s, c]
+ *   dtype    SPC_F32 / SPC_F16 / SPC_BF16: x, y, bias (and w unless Q8_0)
+ *   w_dtype  == dtype, or SPC_Q8_0 with dtype SPC_BF16: w = int8 quants
+ *            [cout, ntaps, cin], w_scale = fp16 scales [cout, ntaps, cin/32]
+ *            (spc_q8_0_repack makes both from ggml Q8_0 blocks)
+ *   idx      SPC_IDX_TOKEN_MAJOR [n_out, ntaps] or SPC_IDX_OFFSET_MAJOR
+ *            [ntaps, n_out]; entries outside [0, n_in) are skipped
+ *   row_perm optional [n_out]: processing order (e.g. the mask argsort);
+ *            processing row r computes and writes output row row_perm[r]
+ *   bias     may be NULL
+ * Each 128-row tile skips the taps none of its rows uses.
+ * Requires cin % 32 == 0 and cout % 32 == 0.
+ * ------------------------------------------------------------------------ */
+int spc_sparse_conv(spc_stream_t stream, int dtype, const void* x, int w_dtype, const void* w,
+                    const void* w_scale, const void* bias, void* y, const int32_t* idx,
+                    int idx_layout, const int32_t* row_perm, int64_t ntaps, int64_t n_out,
+                    int64_t n_in, int64_t cin, int64_t cout);
+
+/* Drop-in for the reference's spconv bridge (same name, arguments and
+ * layouts as cpp_ggml/third_party/sam3d-spconv/include/
+ * sam3d_spconv_bridge.cuh:10-21, called from PATCH:2033-2038): f16
+ * input [tokens, channels], weight [output_channels, 27, channels], bias
+ * [output_channels], output [tokens, output_channels]; indices offset-major
+ * [27, tokens] (-1 = missing), mask / mask_argsort the sorted masks and
+ * permutation of spc_map_build.  Accumulates in F32 (the reference kernel
+ * accumulates in f16).  Returns nothing, like the reference; failures are
+ * reported through spc_last_error(). */
+void sam3d_spconv_f16_forward(spc_stream_t stream, const void* input, const void* weight,
+                              const void* bias, void* output, const int32_t* indices,
+                              const uint32_t* mask, const int32_t* mask_argsort, int64_t tokens,
+                              int64_t channels, int64_t output_channels);
+
+/* Q8_0 weights.  ggml block = [fp16 d][int8 q[32]] (34 bytes), as written by
+ * quantize_q8_0 (cpp_ggml/scripts/gguf_schema.py:14-24).  Splits nblocks
+ * blocks into quants qs[nblocks*32] and scales d[nblocks] (16-byte
+ * aligned streams for the GEMM's in-register dequantisation). */
+int spc_q8_0_repack(spc_stream_t stream, const uint8_t* blocks, int64_t nblocks, int8_t* qs,
+                    uint16_t* d);
+
+/* ------------------------------------------------------------------------
+ * Scatter-mean.  Replaces ggml_sam3d_sparse_scatter_mean (PATCH:59-63,
+ * CPU semantics PATCH:151-215): out[r] = (sum over fine rows i with
+ * rows[i] == r, ascending i, partial sums rounded to the storage dtype
+ * after every add) / counts[r] in F32; rows outside [0, nc) skipped.
+ * Deterministic (the reference CUDA kernel uses atomics, PATCH:1847-1901).
+ * dtype SPC_F16 (the reference op), SPC_BF16 or SPC_F32.
+ * ------------------------------------------------------------------------ */
+size_t spc_scatter_mean_workspace_bytes(int64_t nf, int64_t nc);
+int spc_scatter_mean(spc_stream_t stream, int dtype, const void* features, const int32_t* rows,
+                     const float* counts, void* out, int64_t channels, int64_t nf, int64_t nc,
+                     void* workspace, size_t workspace_bytes);
+
+/* Row gather dst[i] = src[idx[i]] (zero row when idx[i] is outside
+ * [0, n_src)).  SparseUpsample's feats[idx] (SP/spatial.py:92; SRC/
+ * slat_flow_graph.cpp:244-247) and SparseSubdivide's parent broadcast
+ * (SP/spatial.py:123-128; SRC/mesh_decoder_graph.cpp:386-393). */
+int spc_gather_rows(spc_stream_t stream, int dtype, const void* src, const int32_t* idx,
+                    void* dst, int64_t n_out, int64_t n_src, int64_t channels);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SAM3D_SPCONV_AMD_H */

@@ -1,0 +1,303 @@
+"""ctypes binding of libsam3d_spconv_amd.so (the C ABI in include/).
+
+torch supplies device memory and the current HIP stream; every compute call
+goes to a hand-written HIP kernel in the library.  There is no CPU or
+PyTorch fallback: if the library is missing or the tensors are not on a GPU
+the call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from pathlib import Path
+
+import torch
+
+PKG = Path(__file__).resolve().parent
+LIB_PATH = PKG / "lib" / "libsam3d_spconv_amd.so"
+
+F32, F16, BF16, Q8_0 = 0, 1, 2, 3
+OK, BAD_SHAPE, BAD_COORD, DUP_COORD, OOM, HIP_ERROR, BAD_ARG = range(7)
+MAP_MESH, MAP_SYNC = 1, 2
+IDX_TOKEN_MAJOR, IDX_OFFSET_MAJOR = 0, 1
+
+_STATUS_NAMES = {BAD_SHAPE: "BAD_SHAPE", BAD_COORD: "BAD_COORD", DUP_COORD: "DUP_COORD",
+                 OOM: "OOM", HIP_ERROR: "HIP_ERROR", BAD_ARG: "BAD_ARG"}
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int32
+_U32 = ctypes.c_uint32
+_INT = ctypes.c_int
+_SZ = ctypes.c_size_t
+
+_lib = None
+
+
+class SparseConvError(RuntimeError):
+    """A library call returned a non-OK status."""
+
+    def __init__(self, fn: str, status: int, message: str):
+        super().__init__(f"{fn}: {_STATUS_NAMES.get(status, status)}: {message}")
+        self.status = status
+
+
+def lib() -> ctypes.CDLL:
+    """Loads the HIP library (after torch, so both share torch's HIP runtime)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(f"{LIB_PATH} is not built; run __graft_entry__.build()")
+    L = ctypes.CDLL(str(LIB_PATH))
+    L.spc_last_error.restype = ctypes.c_char_p
+    L.spc_status_string.restype = ctypes.c_char_p
+    L.spc_status_string.argtypes = [_INT]
+    L.spc_version.restype = _INT
+    L.spc_map_workspace_bytes.restype = _SZ
+    L.spc_map_workspace_bytes.argtypes = [_I64]
+    L.spc_map_build.argtypes = [_P, _P, _I64, _I32, _U32, _P, _P, _P, _P, _P, _P, _SZ]
+    L.spc_read_status.argtypes = [_P, _P]
+    L.spc_downsample_workspace_bytes.restype = _SZ
+    L.spc_downsample_workspace_bytes.argtypes = [_I64]
+    L.spc_downsample_map.argtypes = [_P, _P, _I64, _I64, _I32, _P, _P, _P, _P, _P, _P, _P, _SZ]
+    L.spc_subdivide_workspace_bytes.restype = _SZ
+    L.spc_subdivide_workspace_bytes.argtypes = [_I64]
+    L.spc_subdivide_map.argtypes = [_P, _P, _I64, _P, _P, _P, _P, _P, _SZ]
+    L.spc_sparse_conv.argtypes = [_P, _INT, _P, _INT, _P, _P, _P, _P, _P, _INT, _P, _I64, _I64,
+                                  _I64, _I64, _I64]
+    L.sam3d_spconv_f16_forward.argtypes = [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64]
+    L.sam3d_spconv_f16_forward.restype = None
+    L.spc_q8_0_repack.argtypes = [_P, _P, _I64, _P, _P]
+    L.spc_scatter_mean_workspace_bytes.restype = _SZ
+    L.spc_scatter_mean_workspace_bytes.argtypes = [_I64, _I64]
+    L.spc_scatter_mean.argtypes = [_P, _INT, _P, _P, _P, _P, _I64, _I64, _I64, _P, _SZ]
+    L.spc_gather_rows.argtypes = [_P, _INT, _P, _P, _P, _I64, _I64, _I64]
+    _lib = L
+    return L
+
+
+def _check(fn: str, status: int) -> None:
+    if status != OK:
+        raise SparseConvError(fn, status, lib().spc_last_error().decode(errors="replace"))
+
+
+def _stream(device: torch.device | None = None) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _ptr(t: torch.Tensor | None):
+    return None if t is None else t.data_ptr()
+
+
+def _need_gpu(*ts: torch.Tensor) -> None:
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError("sparse-conv kernels run on the GPU only; got a CPU tensor")
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.float32:
+        return F32
+    if dt == torch.float16:
+        return F16
+    if dt == torch.bfloat16:
+        return BF16
+    raise TypeError(f"unsupported feature dtype {dt}")
+
+
+def _workspace(nbytes: int, device) -> torch.Tensor:
+    return torch.empty(int(nbytes), dtype=torch.uint8, device=device)
+
+
+# ---------------------------------------------------------------------------
+# kernel maps
+# ---------------------------------------------------------------------------
+@dataclass
+class SubmMap:
+    """Submanifold 3x3x3 map of one coordinate set (all device tensors)."""
+
+    n: int
+    token_major: torch.Tensor   # [n*27] int32, sentinel n
+    offset_major: torch.Tensor  # [27*n] int32, -1 missing
+    mask_sorted: torch.Tensor   # [n] int32
+    argsort: torch.Tensor       # [n] int32
+    mask_natural: torch.Tensor  # [n] int32
+
+    @property
+    def pairs(self) -> int:
+        return int((self.token_major < self.n).sum().item())
+
+
+def map_build(coords: torch.Tensor, *, mesh_resolution: int | None = None,
+              outputs: str = "all", sync: bool = True, workspace: torch.Tensor | None = None):
+    """spc_map_build on int32 [N,4] device coords.  mesh_resolution selects the
+    build_mesh_conv_table semantics (range + uniqueness checks)."""
+    _need_gpu(coords)
+    coords = coords.contiguous()
+    if coords.dtype != torch.int32 or coords.dim() != 2 or coords.shape[1] != 4:
+        raise ValueError("coords must be int32 [N, 4]")
+    n = coords.shape[0]
+    dev = coords.device
+    L = lib()
+    ws = workspace if workspace is not None else _workspace(L.spc_map_workspace_bytes(n), dev)
+    e = lambda k: torch.empty(k, dtype=torch.int32, device=dev)  # noqa: E731
+    tm = e(27 * n)
+    om = e(27 * n) if outputs == "all" else None
+    ms, ar, mn = e(n), e(n), e(n)
+    flags = (MAP_MESH if mesh_resolution is not None else 0) | (MAP_SYNC if sync else 0)
+    st = L.spc_map_build(_stream(dev), _ptr(coords), n, int(mesh_resolution or 0), flags,
+                         _ptr(tm), _ptr(om), _ptr(ms), _ptr(ar), _ptr(mn), _ptr(ws), ws.numel())
+    _check("spc_map_build", st)
+    return SubmMap(n, tm, om, ms, ar, mn)
+
+
+@dataclass
+class DownsampleMap:
+    nf: int
+    nc: int
+    fine_to_coarse: torch.Tensor  # [nf]
+    coarse_coords: torch.Tensor   # [nc, 4]
+    children: torch.Tensor        # [8*nc]
+    counts: torch.Tensor          # [nc] float32
+    stride2_taps: torch.Tensor | None  # [nc*8]
+
+
+def downsample_map(coords: torch.Tensor, n_batch: int, resolution: int,
+                   with_taps: bool = True) -> DownsampleMap:
+    _need_gpu(coords)
+    coords = coords.contiguous()
+    nf = coords.shape[0]
+    dev = coords.device
+    L = lib()
+    ws = _workspace(L.spc_downsample_workspace_bytes(nf), dev)
+    f2c = torch.empty(nf, dtype=torch.int32, device=dev)
+    cc = torch.empty((nf, 4), dtype=torch.int32, device=dev)
+    ch = torch.empty(8 * nf, dtype=torch.int32, device=dev)
+    cnt = torch.empty(nf, dtype=torch.float32, device=dev)
+    taps = torch.empty(8 * nf, dtype=torch.int32, device=dev) if with_taps else None
+    nc = ctypes.c_int64(0)
+    st = L.spc_downsample_map(_stream(dev), _ptr(coords), nf, int(n_batch), int(resolution),
+                              _ptr(f2c), _ptr(cc), _ptr(ch), _ptr(cnt), _ptr(taps),
+                              ctypes.byref(nc), _ptr(ws), ws.numel())
+    _check("spc_downsample_map", st)
+    k = nc.value
+    return DownsampleMap(nf, k, f2c, cc[:k], ch[: 8 * k], cnt[:k],
+                         None if taps is None else taps[: 8 * k])
+
+
+def subdivide_map(coords: torch.Tensor, keep: torch.Tensor | None = None):
+    """Returns (child coords [m,4], parent [m]) in parent-major order."""
+    _need_gpu(coords, keep)
+    coords = coords.contiguous()
+    n = coords.shape[0]
+    dev = coords.device
+    L = lib()
+    ws = _workspace(L.spc_subdivide_workspace_bytes(n), dev)
+    oc = torch.empty((8 * n, 4), dtype=torch.int32, device=dev)
+    par = torch.empty(8 * n, dtype=torch.int32, device=dev)
+    if keep is not None:
+        keep = keep.to(torch.uint8).contiguous()
+        if keep.numel() != 8 * n:
+            raise ValueError("keep must have 8*n entries")
+    m = ctypes.c_int64(0)
+    st = L.spc_subdivide_map(_stream(dev), _ptr(coords), n, _ptr(keep), _ptr(oc), _ptr(par),
+                             ctypes.byref(m), _ptr(ws), ws.numel())
+    _check("spc_subdivide_map", st)
+    return oc[: m.value], par[: m.value]
+
+
+# ---------------------------------------------------------------------------
+# feature ops
+# ---------------------------------------------------------------------------
+def sparse_conv(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None,
+                idx: torch.Tensor, *, ntaps: int, n_out: int,
+                idx_layout: int = IDX_TOKEN_MAJOR, row_perm: torch.Tensor | None = None,
+                w_scale: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                cout: int | None = None) -> torch.Tensor:
+    """y = conv(x) through spc_sparse_conv.  weight [Cout, ntaps, Cin] in the
+    feature dtype, or int8 quants with w_scale (fp16 bits as int16/uint16 or
+    float16 tensor) for Q8_0."""
+    _need_gpu(x, weight, bias, idx, row_perm, w_scale)
+    x = x.contiguous()
+    weight = weight.contiguous()
+    dt = dtype_code(x.dtype)
+    if weight.dtype == torch.int8:
+        wdt = Q8_0
+        if w_scale is None:
+            raise ValueError("Q8_0 weights need w_scale")
+        w_scale = w_scale.contiguous()
+    else:
+        wdt = dtype_code(weight.dtype)
+    cin = x.shape[1]
+    if cout is None:
+        cout = weight.numel() // (ntaps * cin)
+    if bias is not None:
+        bias = bias.contiguous()
+    if out is None:
+        out = torch.empty((n_out, cout), dtype=x.dtype, device=x.device)
+    st = lib().spc_sparse_conv(_stream(x.device), dt, _ptr(x), wdt, _ptr(weight), _ptr(w_scale),
+                               _ptr(bias), _ptr(out), _ptr(idx), idx_layout, _ptr(row_perm),
+                               ntaps, n_out, x.shape[0], cin, cout)
+    _check("spc_sparse_conv", st)
+    return out
+
+
+def spconv_f16_forward(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor,
+                       indices: torch.Tensor, mask: torch.Tensor, argsort: torch.Tensor,
+                       out: torch.Tensor | None = None) -> torch.Tensor:
+    """The reference bridge signature sam3d_spconv_f16_forward."""
+    _need_gpu(x, weight, bias, indices, mask, argsort)
+    n, c = x.shape
+    cout = bias.shape[0]
+    if out is None:
+        out = torch.empty((n, cout), dtype=torch.float16, device=x.device)
+    L = lib()
+    L.sam3d_spconv_f16_forward(_stream(x.device), _ptr(x), _ptr(weight), _ptr(bias), _ptr(out),
+                               _ptr(indices), _ptr(mask), _ptr(argsort), n, c, cout)
+    msg = L.spc_last_error().decode(errors="replace")
+    return out, msg
+
+
+def q8_0_repack(blocks: torch.Tensor):
+    """ggml Q8_0 blocks (uint8, 34 bytes each) -> (int8 quants, fp16 scales)."""
+    _need_gpu(blocks)
+    blocks = blocks.contiguous()
+    nb = blocks.numel() // 34
+    qs = torch.empty(nb * 32, dtype=torch.int8, device=blocks.device)
+    d = torch.empty(nb, dtype=torch.float16, device=blocks.device)
+    st = lib().spc_q8_0_repack(_stream(blocks.device), _ptr(blocks), nb, _ptr(qs), _ptr(d))
+    _check("spc_q8_0_repack", st)
+    return qs, d
+
+
+def scatter_mean(features: torch.Tensor, rows: torch.Tensor, counts: torch.Tensor,
+                 nc: int) -> torch.Tensor:
+    _need_gpu(features, rows, counts)
+    features = features.contiguous()
+    rows = rows.to(torch.int32).contiguous()
+    counts = counts.to(torch.float32).contiguous()
+    nf, c = features.shape
+    dev = features.device
+    L = lib()
+    ws = _workspace(L.spc_scatter_mean_workspace_bytes(nf, nc), dev)
+    out = torch.empty((nc, c), dtype=features.dtype, device=dev)
+    st = L.spc_scatter_mean(_stream(dev), dtype_code(features.dtype), _ptr(features), _ptr(rows),
+                            _ptr(counts), _ptr(out), c, nf, nc, _ptr(ws), ws.numel())
+    _check("spc_scatter_mean", st)
+    return out
+
+
+def gather_rows(src: torch.Tensor, idx: torch.Tensor) -> torch.Tensor:
+    _need_gpu(src, idx)
+    src = src.contiguous()
+    idx = idx.to(torch.int32).contiguous()
+    n_src = src.shape[0]
+    channels = 1
+    for s in src.shape[1:]:
+        channels *= int(s)
+    out = torch.empty((idx.numel(),) + tuple(src.shape[1:]), dtype=src.dtype, device=src.device)
+    st = lib().spc_gather_rows(_stream(src.device), dtype_code(src.dtype), _ptr(src), _ptr(idx),
+                               _ptr(out), idx.numel(), n_src, channels)
+    _check("spc_gather_rows", st)
+    return out

@@ -1,0 +1,121 @@
+// common.h -- shared types and helpers of the sparse-conv HIP library (gfx950).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "sam3d_spconv_amd.h"
+
+namespace spc {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// 64-bit voxel key: b:18 | x:15 | y:15 | z:15 bits (63 bits; bit 63 clear).
+constexpr int kCoordBits = 15;
+constexpr int32_t kCoordLimit = 1 << kCoordBits;      // x, y, z in [0, 32768)
+constexpr int32_t kBatchLimit = 1 << 18;              // b in [0, 262144)
+constexpr unsigned long long kEmptyKey = ~0ull;
+
+__host__ __device__ inline unsigned long long pack_key(int32_t b, int32_t x, int32_t y,
+                                                       int32_t z) {
+    return ((unsigned long long)(uint32_t)b << 45) | ((unsigned long long)(uint32_t)x << 30) |
+           ((unsigned long long)(uint32_t)y << 15) | (unsigned long long)(uint32_t)z;
+}
+
+__device__ inline uint32_t hash_key(unsigned long long k) {
+    // 64-bit finaliser (splitmix64 constants), folded to 32 bits
+    k ^= k >> 30;
+    k *= 0xbf58476d1ce4e5b9ull;
+    k ^= k >> 27;
+    k *= 0x94d049bb133111ebull;
+    k ^= k >> 31;
+    return (uint32_t)k;
+}
+
+// Round-to-nearest-even float -> bf16 / f16 bits (device), from the formats'
+// definitions; NaN payloads are quieted.
+__device__ inline uint16_t f32_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+__device__ inline float bf16_bits_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+__device__ inline uint16_t f32_to_f16_bits(float f) {
+    _Float16 h = (_Float16)f;  // v_cvt_f16_f32: round to nearest even
+    return __builtin_bit_cast(uint16_t, h);
+}
+__device__ inline float f16_bits_to_f32(uint16_t h) {
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Carves aligned sub-buffers out of a caller-owned workspace.
+struct Carver {
+    char* base;
+    size_t cap;
+    size_t used = 0;
+    bool ok = true;
+    Carver(void* b, size_t c) : base(static_cast<char*>(b)), cap(c) {}
+    template <typename T>
+    T* take(size_t count) {
+        used = align_up(used, 256);
+        T* p = reinterpret_cast<T*>(base + used);
+        used += count * sizeof(T);
+        if (used > cap || (base == nullptr && count > 0)) ok = false;
+        return p;
+    }
+};
+
+// Byte counter mirroring Carver for workspace-size queries.
+struct Sizer {
+    size_t used = 0;
+    template <typename T>
+    T* take(size_t count) {
+        used = align_up(used, 256);
+        used += count * sizeof(T);
+        return nullptr;
+    }
+};
+
+// Device status word layout (first int of every workspace).
+constexpr int kStatusBytes = 256;
+
+void set_last_error(const char* fmt, ...);
+int hip_status(hipError_t e, const char* what);
+
+// Shared device utilities (maps.hip / sort.hip).
+hipError_t fill_i32(hipStream_t s, int32_t* p, int32_t v, int64_t n);
+hipError_t fill_u64(hipStream_t s, unsigned long long* p, unsigned long long v, int64_t n);
+hipError_t iota_i32(hipStream_t s, int32_t* p, int64_t n);
+
+// Stable LSD radix sort of (key, value) pairs over key bits [0, end_bit).
+// vals_in may be null (values = 0..n-1).  keys_out / vals_out may alias
+// nothing else.  Workspace from radix_sort_ws_bytes.
+size_t radix_sort_ws_bytes(int64_t n, int key_bytes);
+hipError_t radix_sort_u32(hipStream_t s, const uint32_t* keys_in, const int32_t* vals_in,
+                          uint32_t* keys_out, int32_t* vals_out, int64_t n, int end_bit, void* ws,
+                          size_t ws_bytes);
+hipError_t radix_sort_u64(hipStream_t s, const unsigned long long* keys_in,
+                          const int32_t* vals_in, unsigned long long* keys_out, int32_t* vals_out,
+                          int64_t n, int end_bit, void* ws, size_t ws_bytes);
+
+// Exclusive prefix sum of int32 (n elements) with total written to *total.
+size_t scan_ws_bytes(int64_t n);
+hipError_t exclusive_scan_i32(hipStream_t s, const int32_t* in, int32_t* out, int32_t* total,
+                              int64_t n, void* ws, size_t ws_bytes);
+
+}  // namespace spc
+
+#define SPC_HIP(call)                                             \
+    do {                                                          \
+        hipError_t e_ = (call);                                   \
+        if (e_ != hipSuccess) return spc::hip_status(e_, #call);  \
+    } while (0)

@@ -1,0 +1,507 @@
+// maps.hip -- kernel-map construction on the GPU.
+//
+//   spc_map_build       : submanifold 3x3x3 neighbour tables (SlatTables::
+//                         build's conv tables, SRC/sparse_ops.cpp:93-155, and
+//                         build_mesh_conv_table, SRC/sparse_ops.cpp:312-346)
+//   spc_downsample_map  : stride-2 coarse map (SRC/sparse_ops.cpp:27-81)
+//   spc_subdivide_map   : 2x subdivision (SRC/sparse_ops.cpp:348-371)
+//
+// Design: an open-addressing hash table in HBM (power-of-two capacity >= 2N,
+// 64-bit packed (b,x,y,z) keys, linear probing, atomicCAS insert, atomicMin
+// of the row id so the first occurrence of a duplicate owns the key exactly
+// like std::map::emplace).  The 27-offset query runs one workgroup per 64
+// tokens: 27x64 probes land in LDS, then the token-major table, the
+// offset-major table (27 coalesced 256-byte rows) and the masks are written
+// from LDS with unit-stride stores.  The stable mask argsort is the radix
+// sort of sort.hip.
+#include <climits>
+
+#include "common.h"
+
+namespace spc {
+
+namespace {
+
+enum : int32_t { kErrBadCoord = 1, kErrDup = 2, kErrOom = 4 };
+
+__device__ inline bool coord_ok(int4 c, int32_t lim) {
+    return c.x >= 0 && c.x < kBatchLimit && c.y >= 0 && c.y < lim && c.z >= 0 && c.z < lim &&
+           c.w >= 0 && c.w < lim;
+}
+
+__global__ void map_init_kernel(unsigned long long* hkeys, int32_t* hvals, int64_t cap,
+                                int32_t* status) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < cap) {
+        hkeys[i] = kEmptyKey;
+        hvals[i] = INT_MAX;
+    }
+    if (i == 0) *status = 0;
+}
+
+__global__ __launch_bounds__(256) void hash_insert_kernel(const int4* __restrict__ coords,
+                                                          int64_t n, int32_t lim,
+                                                          unsigned long long* hkeys,
+                                                          int32_t* hvals, uint32_t cap_mask,
+                                                          int32_t* status) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int4 c = coords[i];
+    if (!coord_ok(c, lim)) {
+        atomicOr(status, kErrBadCoord);
+        return;
+    }
+    const unsigned long long key = pack_key(c.x, c.y, c.z, c.w);
+    uint32_t h = hash_key(key) & cap_mask;
+    for (uint32_t it = 0; it <= cap_mask; ++it) {
+        const unsigned long long prev = atomicCAS(&hkeys[h], kEmptyKey, key);
+        if (prev == kEmptyKey || prev == key) {
+            atomicMin(&hvals[h], (int32_t)i);
+            return;
+        }
+        h = (h + 1) & cap_mask;
+    }
+    atomicOr(status, kErrOom);
+}
+
+__device__ inline int32_t hash_find(const unsigned long long* __restrict__ hkeys,
+                                    const int32_t* __restrict__ hvals, uint32_t cap_mask,
+                                    unsigned long long key) {
+    uint32_t h = hash_key(key) & cap_mask;
+    for (uint32_t it = 0; it <= cap_mask; ++it) {
+        const unsigned long long k = hkeys[h];
+        if (k == key) return hvals[h];
+        if (k == kEmptyKey) return -1;
+        h = (h + 1) & cap_mask;
+    }
+    return -1;
+}
+
+constexpr int kNbrTokens = 64;
+
+// MESH: duplicates are an error (build_mesh_conv_table); otherwise the
+// SlatTables rule applies (only the owning row gets its neighbours).
+template <bool MESH>
+__global__ __launch_bounds__(256) void neighbor_kernel(
+    const int4* __restrict__ coords, int64_t n, const unsigned long long* __restrict__ hkeys,
+    const int32_t* __restrict__ hvals, uint32_t cap_mask, int32_t* __restrict__ token_major,
+    int32_t* __restrict__ offset_major, int32_t* __restrict__ mask_nat, int32_t* status) {
+    __shared__ int32_t nb[27][kNbrTokens + 1];
+    __shared__ int32_t owner[kNbrTokens];
+    const int tid = threadIdx.x;
+    const int64_t t0 = (int64_t)blockIdx.x * kNbrTokens;
+    for (int e = tid; e < 27 * kNbrTokens; e += 256) {
+        const int o = e / kNbrTokens;
+        const int tl = e % kNbrTokens;
+        const int64_t t = t0 + tl;
+        int32_t res = -1;
+        if (t < n) {
+            const int4 c = coords[t];
+            const int32_t x = c.y + (o / 9 - 1);
+            const int32_t y = c.z + ((o / 3) % 3 - 1);
+            const int32_t z = c.w + (o % 3 - 1);
+            if (c.x >= 0 && c.x < kBatchLimit && x >= 0 && x < kCoordLimit && y >= 0 &&
+                y < kCoordLimit && z >= 0 && z < kCoordLimit)
+                res = hash_find(hkeys, hvals, cap_mask, pack_key(c.x, x, y, z));
+        }
+        nb[o][tl] = res;
+    }
+    __syncthreads();
+    if (tid < kNbrTokens) {
+        const int64_t t = t0 + tid;
+        int own = 0;
+        if (t < n) {
+            own = nb[13][tid] == (int32_t)t;
+            if (MESH && !own) atomicOr(status, kErrDup);
+        }
+        owner[tid] = own;
+    }
+    __syncthreads();
+    const int64_t valid_tokens = n - t0 < kNbrTokens ? n - t0 : kNbrTokens;
+    if (token_major) {
+        for (int e = tid; e < 27 * valid_tokens; e += 256) {
+            const int tl = e / 27;
+            const int o = e % 27;
+            const int32_t v = owner[tl] ? nb[o][tl] : -1;
+            token_major[t0 * 27 + e] = v >= 0 ? v : (int32_t)n;
+        }
+    }
+    if (offset_major) {
+        for (int e = tid; e < 27 * kNbrTokens; e += 256) {
+            const int o = e / kNbrTokens;
+            const int tl = e % kNbrTokens;
+            if (tl < valid_tokens) {
+                const int32_t v = owner[tl] ? nb[o][tl] : -1;
+                offset_major[(int64_t)o * n + t0 + tl] = v;
+            }
+        }
+    }
+    if (mask_nat && tid < valid_tokens) {
+        int32_t m = 0;
+        if (owner[tid]) {
+#pragma unroll
+            for (int o = 0; o < 27; ++o) m |= (nb[o][tid] >= 0 ? 1 : 0) << o;
+        }
+        mask_nat[t0 + tid] = m;
+    }
+}
+
+int status_to_code(int32_t bits) {
+    if (bits & kErrBadCoord) return SPC_BAD_COORD;
+    if (bits & kErrDup) return SPC_DUP_COORD;
+    if (bits & kErrOom) return SPC_OOM;
+    return SPC_OK;
+}
+
+int read_status_word(hipStream_t s, int32_t* dev) {
+    int32_t bits = 0;
+    SPC_HIP(hipMemcpyAsync(&bits, dev, sizeof(int32_t), hipMemcpyDeviceToHost, s));
+    SPC_HIP(hipStreamSynchronize(s));
+    const int code = status_to_code(bits);
+    if (code != SPC_OK) set_last_error("device reported: %s", spc_status_string(code));
+    return code;
+}
+
+int64_t hash_capacity(int64_t n) {
+    int64_t cap = 256;
+    while (cap < 2 * n) cap <<= 1;
+    return cap;
+}
+
+struct MapWs {
+    int32_t* status;
+    unsigned long long* hkeys;
+    int32_t* hvals;
+    int32_t* mask_nat;
+    uint32_t* mask_sorted;
+    int32_t* argsort;
+    void* sort_ws;
+    size_t sort_bytes;
+};
+
+template <typename C>
+void carve_map_ws(C& c, int64_t n, MapWs* w) {
+    const int64_t cap = hash_capacity(n);
+    auto* st = c.template take<int32_t>(kStatusBytes / 4);
+    auto* hk = c.template take<unsigned long long>(cap);
+    auto* hv = c.template take<int32_t>(cap);
+    auto* mn = c.template take<int32_t>(n);
+    auto* ms = c.template take<uint32_t>(n);
+    auto* ar = c.template take<int32_t>(n);
+    const size_t sb = radix_sort_ws_bytes(n, 4);
+    auto* sw = c.template take<char>(sb);
+    if (w) *w = MapWs{st, hk, hv, mn, ms, ar, sw, sb};
+}
+
+// ---- downsample ---------------------------------------------------------
+
+__global__ void coarse_key_kernel(const int4* __restrict__ coords, int64_t nf, int64_t n_batch,
+                                  int32_t res, int cbits, unsigned long long* __restrict__ keys,
+                                  int32_t* status) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nf) return;
+    const int4 c = coords[i];
+    if (c.x < 0 || c.x >= n_batch || c.y < 0 || c.y >= res || c.z < 0 || c.z >= res || c.w < 0 ||
+        c.w >= res) {
+        atomicOr(status, kErrBadCoord);
+        keys[i] = 0;
+        return;
+    }
+    // (b, x/2, y/2, z/2), most significant first: lexicographic order
+    keys[i] = ((unsigned long long)c.x << (3 * cbits)) |
+              ((unsigned long long)(c.y >> 1) << (2 * cbits)) |
+              ((unsigned long long)(c.z >> 1) << cbits) | (unsigned long long)(c.w >> 1);
+}
+
+__global__ void head_flag_kernel(const unsigned long long* __restrict__ sk, int64_t n,
+                                 int32_t* __restrict__ flag) {
+    const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (p < n) flag[p] = (p == 0 || sk[p] != sk[p - 1]) ? 1 : 0;
+}
+
+__global__ void downsample_assign_kernel(const unsigned long long* __restrict__ sk,
+                                         const int32_t* __restrict__ sv,
+                                         const int32_t* __restrict__ flag,
+                                         const int32_t* __restrict__ excl, int64_t nf, int cbits,
+                                         int32_t* __restrict__ fine_to_coarse,
+                                         int32_t* __restrict__ head_pos,
+                                         int4* __restrict__ coarse_coords) {
+    const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= nf) return;
+    const int32_t id = excl[p] + flag[p] - 1;
+    fine_to_coarse[sv[p]] = id;
+    if (flag[p]) {
+        head_pos[id] = (int32_t)p;
+        const unsigned long long k = sk[p];
+        const unsigned long long m = (1ull << cbits) - 1ull;
+        coarse_coords[id] = make_int4((int32_t)(k >> (3 * cbits)), (int32_t)((k >> (2 * cbits)) & m),
+                                      (int32_t)((k >> cbits) & m), (int32_t)(k & m));
+    }
+    if (p == nf - 1) head_pos[id + 1] = (int32_t)nf;
+}
+
+__global__ void downsample_children_kernel(const int32_t* __restrict__ sv,
+                                           const int32_t* __restrict__ head_pos,
+                                           const int32_t* __restrict__ nc_dev,
+                                           const int4* __restrict__ coords, int64_t nf,
+                                           int32_t* __restrict__ children,
+                                           float* __restrict__ counts,
+                                           int32_t* __restrict__ taps, int32_t* status) {
+    const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= *nc_dev) return;
+    const int32_t h = head_pos[id];
+    const int32_t run = head_pos[id + 1] - h;
+    for (int j = 0; j < 8; ++j) children[id * 8 + j] = j < run ? sv[h + j] : (int32_t)nf;
+    counts[id] = (float)(run + 1);
+    if (taps) {
+        int32_t t[8];
+        for (int j = 0; j < 8; ++j) t[j] = (int32_t)nf;
+        bool dup = false;
+        for (int j = 0; j < run; ++j) {
+            const int32_t f = sv[h + j];
+            const int4 c = coords[f];
+            const int k = (c.y & 1) * 4 + (c.z & 1) * 2 + (c.w & 1);
+            if (t[k] != (int32_t)nf) dup = true;
+            t[k] = f;
+        }
+        if (dup) atomicOr(status, kErrDup);
+        for (int j = 0; j < 8; ++j) taps[id * 8 + j] = t[j];
+    }
+}
+
+int bits_for(int64_t v) {  // bits needed to hold values in [0, v)
+    int b = 0;
+    while (b < 62 && (1ll << b) < v) ++b;
+    return b;
+}
+
+// ---- subdivide ------------------------------------------------------------
+
+__global__ void subdivide_flag_kernel(const uint8_t* __restrict__ keep, int64_t m8,
+                                      int32_t* __restrict__ flag) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < m8) flag[i] = keep[i] ? 1 : 0;
+}
+
+__global__ void subdivide_kernel(const int4* __restrict__ coords, int64_t n,
+                                 const uint8_t* __restrict__ keep,
+                                 const int32_t* __restrict__ pos, int4* __restrict__ out_coords,
+                                 int32_t* __restrict__ parent, int32_t* status) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n * 8) return;
+    if (keep && !keep[i]) return;
+    const int64_t p = i >> 3;
+    const int c = (int)(i & 7);
+    const int4 s = coords[p];
+    if (s.x < 0 || s.x >= kBatchLimit || s.y < 0 || s.z < 0 || s.w < 0 ||
+        s.y >= kCoordLimit / 2 || s.z >= kCoordLimit / 2 || s.w >= kCoordLimit / 2)
+        atomicOr(status, kErrBadCoord);
+    const int64_t dst = keep ? pos[i] : i;
+    out_coords[dst] = make_int4(s.x, s.y * 2 + c / 4, s.z * 2 + (c / 2) % 2, s.w * 2 + c % 2);
+    parent[dst] = (int32_t)p;
+}
+
+inline unsigned grid_for(int64_t n, int threads) { return (unsigned)((n + threads - 1) / threads); }
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace
+}  // namespace spc
+
+using namespace spc;
+
+extern "C" {
+
+size_t spc_map_workspace_bytes(int64_t n) {
+    Sizer z;
+    carve_map_ws(z, n > 0 ? n : 1, nullptr);
+    return z.used + 256;
+}
+
+int spc_map_build(spc_stream_t stream, const int32_t* coords, int64_t n, int32_t resolution,
+                  uint32_t flags, int32_t* token_major, int32_t* offset_major,
+                  int32_t* mask_sorted, int32_t* argsort, int32_t* mask_natural,
+                  void* workspace, size_t workspace_bytes) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (n <= 0 || n > INT32_MAX / 27) {
+        set_last_error("spc_map_build: n = %lld out of range", (long long)n);
+        return SPC_BAD_SHAPE;
+    }
+    if (!coords || !workspace || !aligned16(coords)) {
+        set_last_error("spc_map_build: null or misaligned coords / workspace");
+        return SPC_BAD_ARG;
+    }
+    const bool mesh = flags & SPC_MAP_MESH;
+    if (mesh && (resolution <= 0 || resolution > kCoordLimit)) {
+        set_last_error("spc_map_build: resolution %d outside (0, %d]", resolution, kCoordLimit);
+        return SPC_BAD_ARG;
+    }
+    Carver c(workspace, workspace_bytes);
+    MapWs w;
+    carve_map_ws(c, n, &w);
+    if (!c.ok) {
+        set_last_error("spc_map_build: workspace of %zu bytes < %zu", workspace_bytes,
+                       spc_map_workspace_bytes(n));
+        return SPC_OOM;
+    }
+    const int64_t cap = hash_capacity(n);
+    const uint32_t cap_mask = (uint32_t)(cap - 1);
+    const int4* c4 = reinterpret_cast<const int4*>(coords);
+    int32_t* mnat = mask_natural ? mask_natural : w.mask_nat;
+    map_init_kernel<<<grid_for(cap, 256), 256, 0, s>>>(w.hkeys, w.hvals, cap, w.status);
+    hash_insert_kernel<<<grid_for(n, 256), 256, 0, s>>>(c4, n, mesh ? resolution : kCoordLimit,
+                                                        w.hkeys, w.hvals, cap_mask, w.status);
+    const unsigned nb = grid_for(n, kNbrTokens);
+    if (mesh)
+        neighbor_kernel<true><<<nb, 256, 0, s>>>(c4, n, w.hkeys, w.hvals, cap_mask, token_major,
+                                                 offset_major, mnat, w.status);
+    else
+        neighbor_kernel<false><<<nb, 256, 0, s>>>(c4, n, w.hkeys, w.hvals, cap_mask, token_major,
+                                                  offset_major, mnat, w.status);
+    SPC_HIP(hipGetLastError());
+    if (mask_sorted || argsort) {
+        uint32_t* ms = mask_sorted ? reinterpret_cast<uint32_t*>(mask_sorted) : w.mask_sorted;
+        int32_t* ar = argsort ? argsort : w.argsort;
+        SPC_HIP(radix_sort_u32(s, reinterpret_cast<const uint32_t*>(mnat), nullptr, ms, ar, n, 27,
+                               w.sort_ws, w.sort_bytes));
+    }
+    if (flags & SPC_MAP_SYNC) return read_status_word(s, w.status);
+    return SPC_OK;
+}
+
+int spc_read_status(spc_stream_t stream, void* workspace) {
+    if (!workspace) return SPC_BAD_ARG;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    int32_t* st = static_cast<int32_t*>(workspace);
+    const int code = read_status_word(s, st);
+    SPC_HIP(fill_i32(s, st, 0, 1));
+    return code;
+}
+
+size_t spc_downsample_workspace_bytes(int64_t nf) {
+    const int64_t n = nf > 0 ? nf : 1;
+    Sizer z;
+    z.take<int32_t>(kStatusBytes / 4);
+    z.take<unsigned long long>(n);  // keys
+    z.take<unsigned long long>(n);  // sorted keys
+    z.take<int32_t>(n);             // sorted values
+    z.take<int32_t>(n);             // head flags
+    z.take<int32_t>(n);             // exclusive scan
+    z.take<int32_t>(n + 1);         // head positions
+    z.take<int32_t>(1);             // nc
+    z.take<char>(radix_sort_ws_bytes(n, 8));
+    z.take<char>(scan_ws_bytes(n));
+    return z.used + 256;
+}
+
+int spc_downsample_map(spc_stream_t stream, const int32_t* coords, int64_t nf, int64_t n_batch,
+                       int32_t resolution, int32_t* fine_to_coarse, int32_t* coarse_coords,
+                       int32_t* children, float* counts, int32_t* stride2_taps,
+                       int64_t* nc_out, void* workspace, size_t workspace_bytes) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (nf <= 0 || nf > INT32_MAX / 8) {
+        set_last_error("spc_downsample_map: nf = %lld out of range", (long long)nf);
+        return SPC_BAD_SHAPE;
+    }
+    if (!coords || !fine_to_coarse || !coarse_coords || !children || !counts || !nc_out ||
+        !workspace || !aligned16(coords) || !aligned16(coarse_coords)) {
+        set_last_error("spc_downsample_map: null or misaligned argument");
+        return SPC_BAD_ARG;
+    }
+    if (n_batch <= 0 || n_batch > kBatchLimit || resolution <= 0 || resolution > kCoordLimit) {
+        set_last_error("spc_downsample_map: n_batch %lld / resolution %d out of range",
+                       (long long)n_batch, resolution);
+        return SPC_BAD_ARG;
+    }
+    const int64_t n = nf;
+    Carver c(workspace, workspace_bytes);
+    int32_t* status = c.take<int32_t>(kStatusBytes / 4);
+    auto* keys = c.take<unsigned long long>(n);
+    auto* sk = c.take<unsigned long long>(n);
+    int32_t* sv = c.take<int32_t>(n);
+    int32_t* flag = c.take<int32_t>(n);
+    int32_t* excl = c.take<int32_t>(n);
+    int32_t* head = c.take<int32_t>(n + 1);
+    int32_t* nc_dev = c.take<int32_t>(1);
+    const size_t sort_bytes = radix_sort_ws_bytes(n, 8);
+    char* sort_ws = c.take<char>(sort_bytes);
+    const size_t scan_bytes = scan_ws_bytes(n);
+    char* scan_ws = c.take<char>(scan_bytes);
+    if (!c.ok) {
+        set_last_error("spc_downsample_map: workspace too small");
+        return SPC_OOM;
+    }
+    const int cbits = bits_for((resolution + 1) / 2);
+    const int end_bit = 3 * cbits + bits_for(n_batch);
+    const int4* c4 = reinterpret_cast<const int4*>(coords);
+    SPC_HIP(fill_i32(s, status, 0, 1));
+    coarse_key_kernel<<<grid_for(n, 256), 256, 0, s>>>(c4, n, n_batch, resolution, cbits, keys,
+                                                       status);
+    SPC_HIP(radix_sort_u64(s, keys, nullptr, sk, sv, n, end_bit, sort_ws, sort_bytes));
+    head_flag_kernel<<<grid_for(n, 256), 256, 0, s>>>(sk, n, flag);
+    SPC_HIP(exclusive_scan_i32(s, flag, excl, nc_dev, n, scan_ws, scan_bytes));
+    downsample_assign_kernel<<<grid_for(n, 256), 256, 0, s>>>(
+        sk, sv, flag, excl, n, cbits, fine_to_coarse, head, reinterpret_cast<int4*>(coarse_coords));
+    downsample_children_kernel<<<grid_for(n, 256), 256, 0, s>>>(
+        sv, head, nc_dev, c4, n, children, counts, stride2_taps, status);
+    SPC_HIP(hipGetLastError());
+    int32_t nc_host = 0;
+    SPC_HIP(hipMemcpyAsync(&nc_host, nc_dev, sizeof(int32_t), hipMemcpyDeviceToHost, s));
+    const int code = read_status_word(s, status);  // synchronises
+    *nc_out = nc_host;
+    return code;
+}
+
+size_t spc_subdivide_workspace_bytes(int64_t n) {
+    const int64_t m8 = (n > 0 ? n : 1) * 8;
+    Sizer z;
+    z.take<int32_t>(kStatusBytes / 4);
+    z.take<int32_t>(m8);  // flags
+    z.take<int32_t>(m8);  // positions
+    z.take<int32_t>(1);   // total
+    z.take<char>(scan_ws_bytes(m8));
+    return z.used + 256;
+}
+
+int spc_subdivide_map(spc_stream_t stream, const int32_t* coords, int64_t n, const uint8_t* keep,
+                      int32_t* out_coords, int32_t* parent, int64_t* m_out, void* workspace,
+                      size_t workspace_bytes) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (n <= 0 || n > INT32_MAX / 8) {
+        set_last_error("spc_subdivide_map: n = %lld out of range", (long long)n);
+        return SPC_BAD_SHAPE;
+    }
+    if (!coords || !out_coords || !parent || !m_out || !workspace || !aligned16(coords) ||
+        !aligned16(out_coords)) {
+        set_last_error("spc_subdivide_map: null or misaligned argument");
+        return SPC_BAD_ARG;
+    }
+    const int64_t m8 = n * 8;
+    Carver c(workspace, workspace_bytes);
+    int32_t* status = c.take<int32_t>(kStatusBytes / 4);
+    int32_t* flag = c.take<int32_t>(m8);
+    int32_t* pos = c.take<int32_t>(m8);
+    int32_t* total = c.take<int32_t>(1);
+    const size_t scan_bytes = scan_ws_bytes(m8);
+    char* scan_ws = c.take<char>(scan_bytes);
+    if (!c.ok) {
+        set_last_error("spc_subdivide_map: workspace too small");
+        return SPC_OOM;
+    }
+    SPC_HIP(fill_i32(s, status, 0, 1));
+    if (keep) {
+        subdivide_flag_kernel<<<grid_for(m8, 256), 256, 0, s>>>(keep, m8, flag);
+        SPC_HIP(exclusive_scan_i32(s, flag, pos, total, m8, scan_ws, scan_bytes));
+    }
+    subdivide_kernel<<<grid_for(m8, 256), 256, 0, s>>>(
+        reinterpret_cast<const int4*>(coords), n, keep, pos, reinterpret_cast<int4*>(out_coords),
+        parent, status);
+    SPC_HIP(hipGetLastError());
+    int32_t m = (int32_t)m8;
+    if (keep) SPC_HIP(hipMemcpyAsync(&m, total, sizeof(int32_t), hipMemcpyDeviceToHost, s));
+    const int code = read_status_word(s, status);
+    *m_out = m;
+    return code;
+}
+
+}  // extern "C"

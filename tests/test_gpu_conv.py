@@ -1,0 +1,205 @@
+"""GPU sparse-conv parity against the oracle (the ggml CPU op's F32-accumulate
+arithmetic, PATCH:217-265).  Tolerances: bf16 / f16 / Q8_0 max-rel
+(max|a-b| / max|b|) <= 2e-2; fp32 |a-b| <= 1e-5 + 1e-4 |b|."""
+import numpy as np
+import pytest
+
+from helpers import bf16_bits, from_dev, max_rel, row_subset, to_dev_bf16
+
+pytestmark = pytest.mark.gpu
+
+MAXREL = 2e-2
+F32_RTOL, F32_ATOL = 1e-4, 1e-5
+
+
+def _case(name):
+    print(f"[case] {name}", flush=True)
+
+
+def _bf16_inputs(spc, orc, n, cin, cout, ntaps=27, seed=0):
+    wl = spc.workloads
+    x = bf16_bits(orc, wl.normal((n, cin), 1.0, seed=seed + 1))
+    w = bf16_bits(orc, wl.normal((cout, ntaps, cin), 0.02, seed=seed + 2))
+    b = bf16_bits(orc, wl.normal((cout,), 0.01, seed=seed + 3))
+    return x, w, b
+
+
+def _oracle_bf16(orc, x, w, b, idx_tm, rows, ntaps, n_in):
+    import oracle
+
+    sub = row_subset(idx_tm, n_in, rows, ntaps)
+    return orc.sparse_conv(x, w, b, sub, ntaps=ntaps, n_out=len(rows), idx_layout=1,
+                           out_dtype=oracle.F32, x_dtype=oracle.BF16, w_dtype=oracle.BF16,
+                           b_dtype=oracle.BF16)
+
+
+def _sample_rows(n, k=512, seed=0):
+    rng = np.random.default_rng(seed)
+    if n <= k:
+        return np.arange(n)
+    rows = np.concatenate([[0, n - 1], rng.choice(n, k - 2, replace=False)])
+    return np.sort(rows)
+
+
+@pytest.mark.parametrize("cin,cout", [(32, 32), (64, 64), (128, 128), (32, 64), (64, 128),
+                                      (128, 256), (96, 160)])
+def test_bf16_channels(spc, orc, dev, cin, cout):
+    import torch
+
+    nat = spc._native
+    coords = spc.workloads.random_voxels(2500, 20, batches=2, seed=cin + cout)
+    n = coords.shape[0]
+    _case(f"bf16 subm N={n} cin={cin} cout={cout}")
+    x, w, b = _bf16_inputs(spc, orc, n, cin, cout, seed=cin)
+    m = nat.map_build(torch.from_numpy(coords).to(dev))
+    y = nat.sparse_conv(to_dev_bf16(x, dev), to_dev_bf16(w, dev), to_dev_bf16(b, dev),
+                        m.token_major, ntaps=27, n_out=n)
+    torch.cuda.synchronize()
+    tm = m.token_major.cpu().numpy()
+    rows = np.arange(n)
+    ref = _oracle_bf16(orc, x, w, b, tm, rows, 27, n)
+    assert max_rel(from_dev(y), ref) <= MAXREL
+
+
+def test_bf16_config2_ellipsoids(spc, orc, dev):
+    """4 ellipsoid shells, C=128, bf16, fp32 accumulate."""
+    import torch
+
+    nat = spc._native
+    coords = spc.workloads.ellipsoid_batch()
+    n = coords.shape[0]
+    _case(f"bf16 config2 N={n}")
+    x, w, b = _bf16_inputs(spc, orc, n, 128, 128, seed=20)
+    m = nat.map_build(torch.from_numpy(coords).to(dev))
+    xd, wd, bd = to_dev_bf16(x, dev), to_dev_bf16(w, dev), to_dev_bf16(b, dev)
+    y = nat.sparse_conv(xd, wd, bd, m.token_major, ntaps=27, n_out=n)
+    # the same conv in mask-argsort processing order (offset-major indices)
+    y2 = nat.sparse_conv(xd, wd, bd, m.offset_major, ntaps=27, n_out=n,
+                         idx_layout=nat.IDX_OFFSET_MAJOR, row_perm=m.argsort)
+    torch.cuda.synchronize()
+    tm = m.token_major.cpu().numpy()
+    rows = _sample_rows(n, 768, seed=2)
+    ref = _oracle_bf16(orc, x, w, b, tm, rows, 27, n)
+    y = from_dev(y)
+    assert max_rel(y[rows], ref) <= MAXREL
+    assert max_rel(from_dev(y2)[rows], ref) <= MAXREL
+    assert np.isfinite(y).all()
+
+
+def test_f32_config1_sphere(spc, orc, dev):
+    """BASELINE config 1 on the GPU: sphere shell, C=64, fp32, zero bias."""
+    import oracle
+    import torch
+
+    nat = spc._native
+    wl = spc.workloads
+    coords = wl.sphere_shell()
+    n = coords.shape[0]
+    _case(f"f32 config1 N={n}")
+    x = wl.normal((n, 64), 1.0, seed=31)
+    w = wl.normal((64, 27, 64), 0.02, seed=32)
+    b = np.zeros(64, np.float32)
+    m = nat.map_build(torch.from_numpy(coords).to(dev))
+    y = nat.sparse_conv(torch.from_numpy(x).to(dev), torch.from_numpy(w).to(dev),
+                        torch.from_numpy(b).to(dev), m.token_major, ntaps=27, n_out=n)
+    torch.cuda.synchronize()
+    rows = _sample_rows(n, 2048, seed=3)
+    sub = row_subset(m.token_major.cpu().numpy(), n, rows)
+    ref = orc.sparse_conv(x, w, b, sub, ntaps=27, n_out=len(rows), idx_layout=1,
+                          out_dtype=oracle.F32)
+    got = y.cpu().numpy()[rows]
+    assert np.all(np.abs(got - ref) <= F32_ATOL + F32_RTOL * np.abs(ref))
+
+
+def test_f16_spconv_bridge(spc, orc, dev):
+    """sam3d_spconv_f16_forward: offset-major indices + mask argsort."""
+    import oracle
+    import torch
+
+    nat = spc._native
+    wl = spc.workloads
+    coords = wl.random_voxels(3000, 22, batches=2, seed=41)
+    n = coords.shape[0]
+    _case(f"f16 bridge N={n}")
+    x = wl.normal((n, 64), 1.0, seed=42).astype(np.float16)
+    w = wl.normal((128, 27, 64), 0.02, seed=43).astype(np.float16)
+    b = wl.normal((128,), 0.01, seed=44).astype(np.float16)
+    m = nat.map_build(torch.from_numpy(coords).to(dev))
+    y, msg = nat.spconv_f16_forward(torch.from_numpy(x).to(dev), torch.from_numpy(w).to(dev),
+                                    torch.from_numpy(b).to(dev), m.offset_major, m.mask_sorted,
+                                    m.argsort)
+    torch.cuda.synchronize()
+    ref = orc.sparse_conv(x, w, b, m.offset_major.cpu().numpy(), ntaps=27, n_out=n,
+                          idx_layout=0, out_dtype=oracle.F32)
+    assert max_rel(y.float().cpu().numpy(), ref) <= MAXREL
+
+
+def test_q8_0_config5_sphere(spc, orc, dev):
+    """Q8_0 weights (C=768) dequantised inside the GEMM,
+    against the reference's f16(f32(d)*q) GEMM input."""
+    import oracle
+    import torch
+
+    nat = spc._native
+    wl = spc.workloads
+    coords = wl.sphere_shell()
+    n = coords.shape[0]
+    c = 768
+    _case(f"q8_0 config5 N={n} C={c}")
+    x = bf16_bits(orc, wl.normal((n, c), 1.0, seed=51))
+    wf = wl.normal((c, 27, c), 0.02, seed=52)
+    b = bf16_bits(orc, wl.normal((c,), 0.01, seed=53))
+    blocks = orc.q8_0_quantize(wf)
+    qs, d = nat.q8_0_repack(torch.from_numpy(blocks).to(dev))
+    m = nat.map_build(torch.from_numpy(coords).to(dev))
+    y = nat.sparse_conv(to_dev_bf16(x, dev), qs, to_dev_bf16(b, dev), m.token_major, ntaps=27,
+                        n_out=n, w_scale=d, cout=c)
+    torch.cuda.synchronize()
+    w16 = orc.q8_0_dequant(blocks, oracle.F16)
+    rows = _sample_rows(n, 64, seed=5)
+    sub = row_subset(m.token_major.cpu().numpy(), n, rows)
+    ref = orc.sparse_conv(x, w16, b, sub, ntaps=27, n_out=len(rows), idx_layout=1,
+                          out_dtype=oracle.F32, x_dtype=oracle.BF16, w_dtype=oracle.F16,
+                          b_dtype=oracle.BF16)
+    assert max_rel(from_dev(y)[rows], ref) <= MAXREL
+
+
+def test_stride2_conv(spc, orc, dev):
+    """BASELINE config 3 first stage: 2x2x2 stride-2 conv 64^3 -> 32^3."""
+    import torch
+
+    nat = spc._native
+    coords = spc.workloads.ellipsoid_batch()
+    nf = coords.shape[0]
+    _case(f"stride2 conv nf={nf}")
+    d = nat.downsample_map(torch.from_numpy(coords).to(dev), 4, 64)
+    x, w, b = _bf16_inputs(spc, orc, nf, 128, 128, ntaps=8, seed=60)
+    y = nat.sparse_conv(to_dev_bf16(x, dev), to_dev_bf16(w, dev), to_dev_bf16(b, dev),
+                        d.stride2_taps, ntaps=8, n_out=d.nc)
+    torch.cuda.synchronize()
+    taps = d.stride2_taps.cpu().numpy()
+    rows = _sample_rows(d.nc, 1024, seed=6)
+    ref = _oracle_bf16(orc, x, w, b, taps, rows, 8, nf)
+    assert max_rel(from_dev(y)[rows], ref) <= MAXREL
+
+
+def test_empty_and_missing(spc, orc, dev):
+    """n_out = 0 is a no-op; an all-missing row yields exactly the bias."""
+    import torch
+
+    nat = spc._native
+    _case("empty and isolated rows")
+    x = torch.zeros((0, 32), dtype=torch.bfloat16, device=dev)
+    w = torch.zeros((32, 27, 32), dtype=torch.bfloat16, device=dev)
+    idx = torch.zeros(0, dtype=torch.int32, device=dev)
+    y = nat.sparse_conv(x, w, None, idx, ntaps=27, n_out=0)
+    assert y.shape == (0, 32)
+    # rows whose every tap is the sentinel: output = bias
+    n = 5
+    xb = torch.randn((n, 32), device=dev).to(torch.bfloat16)
+    wb = torch.randn((32, 27, 32), device=dev).to(torch.bfloat16)
+    bb = torch.randn(32, device=dev).to(torch.bfloat16)
+    idx = torch.full((n * 27,), n, dtype=torch.int32, device=dev)
+    y = nat.sparse_conv(xb, wb, bb, idx, ntaps=27, n_out=n)
+    torch.cuda.synchronize()
+    assert torch.equal(y, bb.unsqueeze(0).expand(n, 32))

@@ -1,0 +1,130 @@
+"""GPU kernel-map parity: every table bit-exact with the oracle (which is
+itself pinned to the reference's compiled SlatTables / MeshTables in
+tests/test_oracle_maps.py and to the golden fixtures)."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(name):
+    print(f"[case] {name}", flush=True)
+
+
+def _coord_sets(spc):
+    wl = spc.workloads
+    return {
+        "sphere64": wl.sphere_shell(),
+        "ellipsoids4": wl.ellipsoid_batch(),
+        "random_dups_unsorted": np.ascontiguousarray(
+            np.concatenate([wl.random_voxels(900, 10, batches=3, seed=5, sort=False),
+                            wl.random_voxels(300, 10, batches=3, seed=5, sort=False)[:150]])),
+        "single": np.array([[0, 5, 5, 5]], np.int32),
+        "ragged_193": wl.random_voxels(193, 7, batches=2, seed=9),
+    }
+
+
+@pytest.mark.parametrize("name", ["sphere64", "ellipsoids4", "random_dups_unsorted", "single",
+                                  "ragged_193"])
+def test_map_build_matches_oracle(spc, orc, dev, name):
+    import torch
+
+    coords = _coord_sets(spc)[name]
+    _case(f"map_build {name} N={coords.shape[0]}")
+    n = coords.shape[0]
+    tm_ref = orc.conv_table_slat(coords)
+    om_ref, ms_ref, ar_ref = orc.spconv_tables(tm_ref, n)
+    m = spc._native.map_build(torch.from_numpy(coords).to(dev))
+    assert np.array_equal(m.token_major.cpu().numpy(), tm_ref)
+    assert np.array_equal(m.offset_major.cpu().numpy(), om_ref)
+    assert np.array_equal(m.mask_sorted.cpu().numpy(), ms_ref)
+    assert np.array_equal(m.argsort.cpu().numpy(), ar_ref)
+    mn = m.mask_natural.cpu().numpy()
+    assert np.array_equal(mn[ar_ref], ms_ref)
+
+
+def test_map_kat_sparse_tables_test(spc, dev):
+    """KAT of the reference's sparse_tables_test.cpp:11-27."""
+    import torch
+
+    _case("map_build KAT sparse_tables_test")
+    coords = np.array([[0, 0, 0, 0], [0, 1, 0, 0], [0, 3, 0, 0]], np.int32)
+    m = spc._native.map_build(torch.from_numpy(coords).to(dev))
+    assert m.mask_sorted.cpu().tolist() == [1 << 13, (1 << 4) | (1 << 13), (1 << 13) | (1 << 22)]
+    assert m.argsort.cpu().tolist() == [2, 1, 0]
+
+
+def test_map_mesh_errors(spc, dev):
+    import torch
+
+    nat = spc._native
+    _case("map_build mesh errors")
+    ok = np.array([[0, 1, 2, 3], [0, 1, 2, 4]], np.int32)
+    m = nat.map_build(torch.from_numpy(ok).to(dev), mesh_resolution=8)
+    assert m.token_major.cpu().numpy().reshape(2, 27)[0, 14] == 1
+    dup = np.array([[0, 1, 2, 3], [0, 1, 2, 3]], np.int32)
+    with pytest.raises(nat.SparseConvError) as e:
+        nat.map_build(torch.from_numpy(dup).to(dev), mesh_resolution=8)
+    assert e.value.status == nat.DUP_COORD
+    oor = np.array([[0, 1, 2, 8]], np.int32)
+    with pytest.raises(nat.SparseConvError) as e:
+        nat.map_build(torch.from_numpy(oor).to(dev), mesh_resolution=8)
+    assert e.value.status == nat.BAD_COORD
+    neg = np.array([[0, -1, 2, 3]], np.int32)
+    with pytest.raises(nat.SparseConvError) as e:
+        nat.map_build(torch.from_numpy(neg).to(dev))
+    assert e.value.status == nat.BAD_COORD
+
+
+def test_mesh_levels_match_oracle(spc, orc, dev):
+    """Config-4 subdivision (seeded 50% pruning) and the mesh conv tables."""
+    import torch
+
+    wl = spc.workloads
+    nat = spc._native
+    c0 = wl.sphere_shell()
+    keeps = wl.prune_masks(c0.shape[0])
+    coords, res = c0, 64
+    for lvl, keep in enumerate(keeps, start=1):
+        _case(f"subdivide level {lvl} from N={coords.shape[0]}")
+        ref_c, ref_p = orc.subdivide(coords, keep)
+        oc, par = nat.subdivide_map(torch.from_numpy(coords).to(dev),
+                                    torch.from_numpy(keep).to(dev))
+        assert np.array_equal(oc.cpu().numpy(), ref_c)
+        assert np.array_equal(par.cpu().numpy(), ref_p)
+        res *= 2
+        st, tm_ref = orc.conv_table_mesh(ref_c, res)
+        assert st == 0
+        m = nat.map_build(oc, mesh_resolution=res)
+        assert np.array_equal(m.token_major.cpu().numpy(), tm_ref)
+        coords = ref_c
+    assert coords.shape[0] == 347860
+
+
+def test_subdivide_unpruned(spc, orc, dev):
+    import torch
+
+    _case("subdivide unpruned")
+    c = spc.workloads.random_voxels(500, 16, batches=2, seed=3)
+    ref_c, ref_p = orc.subdivide(c)
+    oc, par = spc._native.subdivide_map(torch.from_numpy(c).to(dev))
+    assert np.array_equal(oc.cpu().numpy(), ref_c)
+    assert np.array_equal(par.cpu().numpy(), ref_p)
+
+
+@pytest.mark.parametrize("name", ["sphere64", "ellipsoids4", "ragged_193"])
+def test_downsample_map_matches_oracle(spc, orc, dev, name):
+    import torch
+
+    coords = _coord_sets(spc)[name]
+    _case(f"downsample_map {name}")
+    ref = orc.downsample_map(coords)
+    taps_ref = orc.stride2_taps(coords, ref["fine_to_coarse"], ref["nc"])
+    nb = int(coords[:, 0].max()) + 1
+    d = spc._native.downsample_map(torch.from_numpy(coords).to(dev), nb, 64)
+    assert d.nc == ref["nc"]
+    assert np.array_equal(d.fine_to_coarse.cpu().numpy(), ref["fine_to_coarse"])
+    assert np.array_equal(d.coarse_coords.cpu().numpy(), ref["coarse_coords"])
+    assert np.array_equal(d.children.cpu().numpy(), ref["children"])
+    assert np.array_equal(d.counts.cpu().numpy(), ref["counts"])
+    assert np.array_equal(d.stride2_taps.cpu().numpy(), taps_ref)
