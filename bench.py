@@ -1,0 +1,347 @@
+#!/usr/bin/env python3
+"""One-GPU sparse-conv benchmark (MI355X).
+
+Default workload: submanifold 3x3x3 sparse conv, bf16 features and weights
+with F32 accumulation, C_in = C_out = 128, batch of 4 ellipsoid shells in a
+64^3 grid (semi-axes U(16,28), Haar rotations, seed 2024; N = 62,710 voxels,
+1,306,542 valid taps).  A step is one conv forward over the whole batch with
+the kernel map already built and every input resident in HBM -- the SLAT IO
+block loop reuses one map for every conv of every sampling step.
+
+Reported:
+  value          Mvoxel/s = N / t_step
+  tflops         algorithmic TFLOP/s = 2 * pairs * C_in * C_out / t_step
+  roofline       the conv kernel against the dense bf16 MFMA peak (2.5 PFLOP/s)
+  map_build_ms   GPU neighbour-map build (hash + 27-offset query + stable mask
+                 argsort) for the same coordinates
+  cpu_baseline   the oracle's restatement of the ggml CPU op (F32 accumulate,
+                 token partition) on the host cores, over a bounded sample of
+                 output rows
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--config 2]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "sparse-conv Mvoxel/s + TFLOP/s (% bf16 MFMA peak), 64³ shell N≈20k C=128"
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_F32_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5],
+                    help="2 = the headline workload; others print diagnostic lines")
+    ap.add_argument("--order", choices=["natural", "mask"], default="natural",
+                    help="row processing order of the conv kernel")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=8.0,
+                    help="target duration of the all-core CPU baseline sample")
+    return ap.parse_args()
+
+
+def bf16_dev(orc, a, dev):
+    import torch
+
+    bits = orc.f32_to_bf16(np.ascontiguousarray(a, dtype=np.float32))
+    return torch.from_numpy(bits.view(np.int16)).to(dev).view(torch.bfloat16), bits
+
+
+class ConvCall:
+    """Pre-extracted arguments of one spc_sparse_conv launch (keeps Python
+    overhead per step at a single ctypes call)."""
+
+    def __init__(self, nat, x, w, bias, y, idx, *, ntaps, n_out, layout, perm=None,
+                 w_scale=None, wdt=None):
+        import torch
+
+        self.fn = nat.lib().spc_sparse_conv
+        self.stream = torch.cuda.current_stream().cuda_stream
+        dt = nat.dtype_code(x.dtype)
+        wd = wdt if wdt is not None else dt
+        self.args = (self.stream, dt, x.data_ptr(), wd, w.data_ptr(),
+                     None if w_scale is None else w_scale.data_ptr(),
+                     None if bias is None else bias.data_ptr(), y.data_ptr(), idx.data_ptr(),
+                     layout, None if perm is None else perm.data_ptr(), ntaps, n_out,
+                     x.shape[0], x.shape[1], y.shape[1])
+        self.nat = nat
+
+    def __call__(self):
+        st = self.fn(*self.args)
+        if st != 0:
+            self.nat._check("spc_sparse_conv", st)
+
+
+def time_gpu(fn, steps, warmup):
+    """Warm-up, then K steps between events recorded on the launch stream."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(steps):
+        fn()
+    stop.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return start.elapsed_time(stop) / steps, wall
+
+
+def traffic_from_profile(name: str):
+    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE +
+    WRITE_SIZE, calibrated against a copy kernel), if the summary exists."""
+    p = ROOT / "profiles" / f"{name}_pmc.md"
+    if not p.exists():
+        return None
+    m = re.search(r"traffic_bytes_per_launch\s*=\s*([0-9.eE+]+)", p.read_text())
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(orc, x_bits, w_bits, b_bits, tm, n, cin, cout, target_s, ntaps=27,
+                 x_dt=None, w_dt=None):
+    """Times the oracle conv (ggml CPU op restatement) on the host over the first
+    S output rows, S chosen so the all-core run lasts about target_s."""
+    import oracle
+
+    x_dt = oracle.BF16 if x_dt is None else x_dt
+    w_dt = oracle.BF16 if w_dt is None else w_dt
+    threads = min(oracle.cpu_threads(), 16)
+    tmr = tm.reshape(n, ntaps)
+
+    def run(rows, th):
+        sub = np.ascontiguousarray(tmr[:rows]).reshape(-1)
+        t0 = time.perf_counter()
+        orc.sparse_conv(x_bits, w_bits, b_bits, sub, ntaps=ntaps, n_out=rows, idx_layout=1,
+                        out_dtype=oracle.F32, x_dtype=x_dt, w_dtype=w_dt, b_dtype=x_dt,
+                        nthreads=th)
+        return time.perf_counter() - t0
+
+    probe = min(n, 64 * threads)
+    t = run(probe, threads)
+    rows = int(min(n, max(probe, probe * target_s / max(t, 1e-6))))
+    times = [run(rows, threads) for _ in range(2)]
+    t_all = min(times)
+    rows1 = max(64, rows // (2 * threads))
+    t_one = run(rows1, 1)
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            m = re.search(r"model name\s*:\s*(.*)", f.read())
+            model = m.group(1).strip() if m else ""
+    except OSError:
+        pass
+    return {
+        "value": rows / t_all / 1e6, "unit": "Mvoxel/s", "cores": threads, "kind": "port",
+        "sample": f"first {rows} of {n} output rows, {threads} threads (ggml op token "
+                  f"partition), best of 2; host '{model}'",
+        "single_thread": {"value": rows1 / t_one / 1e6, "unit": "Mvoxel/s", "cores": 1,
+                          "sample": f"first {rows1} rows, 1 thread"},
+    }
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE "
+              f"{world}); every box here has one GPU and this build has no multi-GPU path. "
+              "Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import __graft_entry__
+
+    spc = __graft_entry__.load()
+    nat = spc._native
+    wl = spc.workloads
+    import oracle
+
+    orc = oracle.orc()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    cfg = args.config
+    if cfg == 2:
+        coords = wl.ellipsoid_batch()
+        cin = cout = 128
+        batch = 4
+        workload = "subm3x3x3 bf16 C=128, 4 ellipsoid shells 64^3 (N=62,710)"
+    elif cfg == 1:
+        coords = wl.sphere_shell()
+        cin = cout = 64
+        batch = 1
+        workload = "subm3x3x3 fp32 C=64, sphere shell r=24 in 64^3 (N=21,766)"
+    elif cfg == 5:
+        coords = wl.sphere_shell()
+        cin = cout = 768
+        batch = 1
+        workload = "subm3x3x3 Q8_0 weights, bf16 activations, C=768, sphere shell 64^3"
+    elif cfg == 3:
+        coords = wl.ellipsoid_batch()
+        cin, cout = 128, 1024
+        batch = 4
+        workload = "stride-2 2x2x2 conv 128->128 then subm3x3x3 128->1024 at 32^3 (bf16)"
+    else:
+        coords = wl.sphere_shell()
+        cin = cout = 64
+        batch = 1
+        workload = "subdivide x2 (50% pruning) + subm3x3x3 bf16 C=64 @128^3, C=32 @256^3"
+
+    n = coords.shape[0]
+    c_dev = torch.from_numpy(coords).to(dev)
+
+    # ---- map build (timed separately; maps are reused by every conv) ----
+    ws = torch.empty(nat.lib().spc_map_workspace_bytes(n), dtype=torch.uint8, device=dev)
+    m = nat.map_build(c_dev, workspace=ws)
+    map_ms, _ = time_gpu(lambda: nat.map_build(c_dev, sync=False, workspace=ws), 50, 5)
+    tm_host = m.token_major.cpu().numpy()
+    pairs = int((tm_host < n).sum())
+    map_bytes = 16 * n + 108 * n + 8 * n
+
+    result = {}
+    if cfg in (2, 1, 5):
+        torch.manual_seed(0)
+        xf = wl.normal((n, cin), 1.0, seed=101)
+        wf = wl.normal((cout, 27, cin), 0.02, seed=102)
+        bf = wl.normal((cout,), 0.01, seed=103) if cfg != 1 else np.zeros(cout, np.float32)
+        y = torch.empty((n, cout), dtype=torch.float32 if cfg == 1 else torch.bfloat16,
+                        device=dev)
+        perm = m.argsort if args.order == "mask" else None
+        idx = m.offset_major if args.order == "mask" else m.token_major
+        layout = nat.IDX_OFFSET_MAJOR if args.order == "mask" else nat.IDX_TOKEN_MAJOR
+        if cfg == 1:
+            x = torch.from_numpy(xf).to(dev)
+            w = torch.from_numpy(wf).to(dev)
+            b = torch.from_numpy(bf).to(dev)
+            call = ConvCall(nat, x, w, b, y, idx, ntaps=27, n_out=n, layout=layout, perm=perm)
+            dtype = "f32"
+            peak = PEAK_F32_TFLOPS
+            xb, wb, bb = xf, wf, bf
+            cpu_dt = (oracle.F32, oracle.F32)
+            w_bytes = wf.nbytes
+            es = 4
+        elif cfg == 2:
+            x, xb = bf16_dev(orc, xf, dev)
+            w, wb = bf16_dev(orc, wf, dev)
+            b, bb = bf16_dev(orc, bf, dev)
+            call = ConvCall(nat, x, w, b, y, idx, ntaps=27, n_out=n, layout=layout, perm=perm)
+            dtype = "bf16"
+            peak = PEAK_BF16_TFLOPS
+            cpu_dt = (oracle.BF16, oracle.BF16)
+            w_bytes = wb.nbytes
+            es = 2
+        else:
+            x, xb = bf16_dev(orc, xf, dev)
+            b, bb = bf16_dev(orc, bf, dev)
+            blocks = orc.q8_0_quantize(wf)
+            qs, dsc = nat.q8_0_repack(torch.from_numpy(blocks).to(dev))
+            call = ConvCall(nat, x, qs, b, y, idx, ntaps=27, n_out=n, layout=layout, perm=perm,
+                            w_scale=dsc, wdt=nat.Q8_0)
+            dtype = "bf16 x Q8_0"
+            peak = PEAK_BF16_TFLOPS
+            wb = orc.q8_0_dequant(blocks, oracle.F16)
+            cpu_dt = (oracle.BF16, oracle.F16)
+            w_bytes = blocks.nbytes
+            es = 2
+        ms, wall = time_gpu(call, args.steps, args.warmup)
+        t = ms / 1e3
+        flops = 2.0 * pairs * cin * cout
+        tflops = flops / t / 1e12
+        comp_bytes = n * cin * es + n * cout * es + w_bytes + 108 * n
+        traffic = traffic_from_profile({2: "conv_bf16_ellipsoids4_c128", 1: "conv_f32_sphere_c64",
+                                        5: "conv_q8_0_sphere_c768"}[cfg])
+        result = {
+            "metric": METRIC if cfg == 2 else f"config {cfg}: {workload}",
+            "value": n / t / 1e6, "unit": "Mvoxel/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": dtype, "data": "synthetic",
+            "config": {"workload": workload, "n_voxels": n, "pairs": pairs, "cin": cin,
+                       "cout": cout, "batch": batch, "ntaps": 27, "row_order": args.order,
+                       "shell_rule": "|dist to surface| <= 1.5 voxel"},
+            "tflops": tflops, "pct_peak": 100.0 * tflops / peak,
+            "dense_equiv_tflops": 2.0 * 27 * n * cin * cout / t / 1e12,
+            "wall_s": wall, "map_build_ms": map_ms,
+            "map_build_gbs": map_bytes / (map_ms / 1e3) / 1e9,
+            "compulsory_gbs": comp_bytes / t / 1e9,
+            "roofline": {"bound": "mfma", "achieved": tflops, "peak": peak, "unit": "TFLOP/s",
+                         "frac": tflops / peak, "traffic": traffic,
+                         "kernel": "conv_kernel (gather -> MFMA implicit GEMM -> store)",
+                         "algorithmic_flops_per_launch": flops},
+        }
+        if not args.no_cpu:
+            result["cpu_baseline"] = cpu_baseline(orc, xb, wb, bb, tm_host, n, cin, cout,
+                                                  args.cpu_seconds, x_dt=cpu_dt[0],
+                                                  w_dt=cpu_dt[1])
+    elif cfg == 3:
+        d = nat.downsample_map(c_dev, 4, 64)
+        nc = d.nc
+        mc = nat.map_build(d.coarse_coords)
+        pairs_c = int((mc.token_major < nc).sum().item())
+        x, _ = bf16_dev(orc, wl.normal((n, cin), 1.0, seed=301), dev)
+        w1, _ = bf16_dev(orc, wl.normal((128, 8, cin), 0.02, seed=302), dev)
+        w2, _ = bf16_dev(orc, wl.normal((cout, 27, 128), 0.02, seed=303), dev)
+        h = torch.empty((nc, 128), dtype=torch.bfloat16, device=dev)
+        y = torch.empty((nc, cout), dtype=torch.bfloat16, device=dev)
+        c1 = ConvCall(nat, x, w1, None, h, d.stride2_taps, ntaps=8, n_out=nc,
+                      layout=nat.IDX_TOKEN_MAJOR)
+        c2 = ConvCall(nat, h, w2, None, y, mc.token_major, ntaps=27, n_out=nc,
+                      layout=nat.IDX_TOKEN_MAJOR)
+        ms1, _ = time_gpu(c1, args.steps, args.warmup)
+        ms2, _ = time_gpu(c2, args.steps, args.warmup)
+        f1 = 2.0 * n * cin * 128
+        f2 = 2.0 * pairs_c * 128 * cout
+        ms = ms1 + ms2
+        result = {"metric": f"config 3: {workload}", "value": nc / (ms / 1e3) / 1e6,
+                  "unit": "Mvoxel/s", "ms_per_step": ms, "dtype": "bf16",
+                  "config": {"workload": workload, "nf": n, "nc": nc, "pairs_coarse": pairs_c},
+                  "stride2_ms": ms1, "stride2_tflops": f1 / (ms1 / 1e3) / 1e12,
+                  "subm_ms": ms2, "subm_tflops": f2 / (ms2 / 1e3) / 1e12,
+                  "pct_peak_subm": 100 * f2 / (ms2 / 1e3) / 1e12 / PEAK_BF16_TFLOPS}
+    else:
+        keeps = wl.prune_masks(n)
+        lv = []
+        cc = c_dev
+        for keep, ch in zip(keeps, (64, 32)):
+            oc, par = nat.subdivide_map(cc, torch.from_numpy(keep).to(dev))
+            res = 128 if ch == 64 else 256
+            ml = nat.map_build(oc, mesh_resolution=res)
+            nl = oc.shape[0]
+            pl = int((ml.token_major < nl).sum().item())
+            x, _ = bf16_dev(orc, wl.normal((nl, ch), 1.0, seed=400 + ch), dev)
+            w, _ = bf16_dev(orc, wl.normal((ch, 27, ch), 0.02, seed=401 + ch), dev)
+            y = torch.empty((nl, ch), dtype=torch.bfloat16, device=dev)
+            call = ConvCall(nat, x, w, None, y, ml.token_major, ntaps=27, n_out=nl,
+                            layout=nat.IDX_TOKEN_MAJOR)
+            msl, _ = time_gpu(call, args.steps, args.warmup)
+            tl = msl / 1e3
+            byt = nl * ch * 2 * 2 + w.numel() * 2 + 108 * nl
+            lv.append({"resolution": res, "n": nl, "pairs": pl, "c": ch, "ms": msl,
+                       "mvoxel_s": nl / tl / 1e6, "tflops": 2.0 * pl * ch * ch / tl / 1e12,
+                       "compulsory_gbs": byt / tl / 1e9})
+            cc = oc
+        result = {"metric": f"config 4: {workload}", "levels": lv, "dtype": "bf16"}
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

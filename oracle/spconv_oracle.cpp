@@ -147,6 +147,75 @@ void run_partitioned(int64_t items, int nthreads, F&& body) {
     for (auto& t : pool) t.join();
 }
 
+struct ConvProblem {
+    const void* x;
+    const void* w;
+    int w_layout;
+    int b_dtype;
+    const void* bias;
+    int y_dtype;
+    void* y;
+    const int32_t* idx;
+    int idx_layout;
+    int64_t ntaps, n_out, n_in, channels, out_channels;
+};
+
+struct LoadF32 {
+    typedef float T;
+    static float f(float v) { return v; }
+};
+struct LoadF16 {
+    typedef uint16_t T;
+    static float f(uint16_t v) { return h2f(v); }
+};
+struct LoadBF16 {
+    typedef uint16_t T;
+    static float f(uint16_t v) { return b2f(v); }
+};
+
+// Rows [begin, end) of the F32-accumulate conv.  The element loads are
+// resolved at compile time; the arithmetic is the op's: acc = bias, then
+// acc += w * x for offsets ascending and channels ascending, each multiply
+// and add rounded separately (-ffp-contract=off).
+template <typename LX, typename LW>
+void conv_rows(const ConvProblem& p, int64_t begin, int64_t end) {
+    const auto* x = static_cast<const typename LX::T*>(p.x);
+    const auto* w = static_cast<const typename LW::T*>(p.w);
+    const int64_t C = p.channels;
+    for (int64_t t = begin; t < end; ++t) {
+        for (int64_t out = 0; out < p.out_channels; ++out) {
+            float acc = p.bias ? load_as_f32(p.b_dtype, p.bias, out) : 0.0f;
+            for (int64_t o = 0; o < p.ntaps; ++o) {
+                const int32_t s = p.idx_layout == 0 ? p.idx[o * p.n_out + t] : p.idx[t * p.ntaps + o];
+                if (s < 0 || s >= p.n_in) continue;
+                const int64_t wbase = p.w_layout == 0 ? (out * p.ntaps + o) * C
+                                                      : (o * p.out_channels + out) * C;
+                const auto* wr = w + wbase;
+                const auto* xr = x + (int64_t)s * C;
+                for (int64_t c = 0; c < C; ++c) acc += LW::f(wr[c]) * LX::f(xr[c]);
+            }
+            store_from_f32(p.y_dtype, p.y, t * p.out_channels + out, acc);
+        }
+    }
+}
+
+template <typename LX>
+void conv_rows_w(int w_dtype, const ConvProblem& p, int64_t b, int64_t e) {
+    switch (w_dtype) {
+        case ORC_F16: conv_rows<LX, LoadF16>(p, b, e); break;
+        case ORC_BF16: conv_rows<LX, LoadBF16>(p, b, e); break;
+        default: conv_rows<LX, LoadF32>(p, b, e); break;
+    }
+}
+
+void conv_rows_dispatch(int x_dtype, int w_dtype, const ConvProblem& p, int64_t b, int64_t e) {
+    switch (x_dtype) {
+        case ORC_F16: conv_rows_w<LoadF16>(w_dtype, p, b, e); break;
+        case ORC_BF16: conv_rows_w<LoadBF16>(w_dtype, p, b, e); break;
+        default: conv_rows_w<LoadF32>(w_dtype, p, b, e); break;
+    }
+}
+
 }  // namespace
 
 extern "C" {
@@ -343,27 +412,13 @@ int orc_sparse_conv(int x_dtype, const void* x, int w_dtype, const void* w, int 
                     int64_t channels, int64_t out_channels, int nthreads) {
     if (ntaps <= 0 || n_out < 0 || n_in < 0 || channels <= 0 || out_channels <= 0)
         return ORC_BAD_SHAPE;
+    ConvProblem p{x, w, w_layout, b_dtype, bias, y_dtype, y, idx, idx_layout, ntaps, n_out,
+                  n_in, channels, out_channels};
     auto body = [&](int ith, int nth) {
         const int64_t per = (n_out + nth - 1) / nth;
         const int64_t begin = std::min(n_out, (int64_t)ith * per);
         const int64_t end = std::min(n_out, begin + per);
-        for (int64_t t = begin; t < end; ++t) {
-            for (int64_t out = 0; out < out_channels; ++out) {
-                float acc = bias ? load_as_f32(b_dtype, bias, out) : 0.0f;
-                for (int64_t o = 0; o < ntaps; ++o) {
-                    const int32_t s = idx_layout == 0 ? idx[o * n_out + t] : idx[t * ntaps + o];
-                    if (s < 0 || s >= n_in) continue;
-                    const int64_t wbase = w_layout == 0 ? (out * ntaps + o) * channels
-                                                        : (o * out_channels + out) * channels;
-                    for (int64_t c = 0; c < channels; ++c) {
-                        const float wv = load_as_f32(w_dtype, w, wbase + c);
-                        const float xv = load_as_f32(x_dtype, x, (int64_t)s * channels + c);
-                        acc += wv * xv;
-                    }
-                }
-                store_from_f32(y_dtype, y, t * out_channels + out, acc);
-            }
-        }
+        conv_rows_dispatch(x_dtype, w_dtype, p, begin, end);
     };
     run_partitioned(n_out, nthreads, body);
     return ORC_OK;
