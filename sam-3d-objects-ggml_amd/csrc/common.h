@@ -13,6 +13,8 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // 64-bit voxel key: b:18 | x:15 | y:15 | z:15 bits (63 bits; bit 63 clear).
 constexpr int kCoordBits = 15;
@@ -34,6 +36,17 @@ __device__ inline uint32_t hash_key(unsigned long long k) {
     k *= 0x94d049bb133111ebull;
     k ^= k >> 31;
     return (uint32_t)k;
+}
+
+// Workgroup barrier that orders LDS traffic only.  __syncthreads() also
+// fences global memory, which makes the compiler wait for every outstanding
+// global load (s_waitcnt vmcnt(0)) -- including register prefetches meant to
+// stay in flight across the barrier.  The kernels' barriers protect LDS
+// stages only, so an LDS-scoped fence is sufficient.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 // Round-to-nearest-even float -> bf16 / f16 bits (device), from the formats'
