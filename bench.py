@@ -73,9 +73,13 @@ class ConvCall:
         self.fn = nat.lib().spc_sparse_conv
         self.stream = torch.cuda.current_stream().cuda_stream
         dt = nat.dtype_code(x.dtype)
-        wd = wdt if wdt is not None else dt
-        self.args = (self.stream, dt, x.data_ptr(), wd, w.data_ptr(),
-                     None if w_scale is None else w_scale.data_ptr(),
+        if isinstance(w, nat.PackedWeights):
+            wd, layout_w, wptr, sptr = w.w_dtype, nat.W_PACKED, w.data.data_ptr(), None
+        else:
+            wd = wdt if wdt is not None else dt
+            layout_w, wptr = nat.W_KRSC, w.data_ptr()
+            sptr = None if w_scale is None else w_scale.data_ptr()
+        self.args = (self.stream, dt, x.data_ptr(), wd, layout_w, wptr, sptr,
                      None if bias is None else bias.data_ptr(), y.data_ptr(), idx.data_ptr(),
                      layout, None if perm is None else perm.data_ptr(), ntaps, n_out,
                      x.shape[0], x.shape[1], y.shape[1])
@@ -233,7 +237,8 @@ def main():
             x = torch.from_numpy(xf).to(dev)
             w = torch.from_numpy(wf).to(dev)
             b = torch.from_numpy(bf).to(dev)
-            call = ConvCall(nat, x, w, b, y, idx, ntaps=27, n_out=n, layout=layout, perm=perm)
+            call = ConvCall(nat, x, nat.pack_weights(w), b, y, idx, ntaps=27, n_out=n,
+                            layout=layout, perm=perm)
             dtype = "f32"
             peak = PEAK_F32_TFLOPS
             xb, wb, bb = xf, wf, bf
@@ -244,7 +249,8 @@ def main():
             x, xb = bf16_dev(orc, xf, dev)
             w, wb = bf16_dev(orc, wf, dev)
             b, bb = bf16_dev(orc, bf, dev)
-            call = ConvCall(nat, x, w, b, y, idx, ntaps=27, n_out=n, layout=layout, perm=perm)
+            call = ConvCall(nat, x, nat.pack_weights(w), b, y, idx, ntaps=27, n_out=n,
+                            layout=layout, perm=perm)
             dtype = "bf16"
             peak = PEAK_BF16_TFLOPS
             cpu_dt = (oracle.BF16, oracle.BF16)
@@ -255,8 +261,8 @@ def main():
             b, bb = bf16_dev(orc, bf, dev)
             blocks = orc.q8_0_quantize(wf)
             qs, dsc = nat.q8_0_repack(torch.from_numpy(blocks).to(dev))
-            call = ConvCall(nat, x, qs, b, y, idx, ntaps=27, n_out=n, layout=layout, perm=perm,
-                            w_scale=dsc, wdt=nat.Q8_0)
+            call = ConvCall(nat, x, nat.pack_weights(qs, dsc, cin=cin, cout=cout), b, y, idx,
+                            ntaps=27, n_out=n, layout=layout, perm=perm)
             dtype = "bf16 x Q8_0"
             peak = PEAK_BF16_TFLOPS
             wb = orc.q8_0_dequant(blocks, oracle.F16)
@@ -302,9 +308,9 @@ def main():
         w2, _ = bf16_dev(orc, wl.normal((cout, 27, 128), 0.02, seed=303), dev)
         h = torch.empty((nc, 128), dtype=torch.bfloat16, device=dev)
         y = torch.empty((nc, cout), dtype=torch.bfloat16, device=dev)
-        c1 = ConvCall(nat, x, w1, None, h, d.stride2_taps, ntaps=8, n_out=nc,
+        c1 = ConvCall(nat, x, nat.pack_weights(w1), None, h, d.stride2_taps, ntaps=8, n_out=nc,
                       layout=nat.IDX_TOKEN_MAJOR)
-        c2 = ConvCall(nat, h, w2, None, y, mc.token_major, ntaps=27, n_out=nc,
+        c2 = ConvCall(nat, h, nat.pack_weights(w2), None, y, mc.token_major, ntaps=27, n_out=nc,
                       layout=nat.IDX_TOKEN_MAJOR)
         ms1, _ = time_gpu(c1, args.steps, args.warmup)
         ms2, _ = time_gpu(c2, args.steps, args.warmup)
@@ -330,8 +336,8 @@ def main():
             x, _ = bf16_dev(orc, wl.normal((nl, ch), 1.0, seed=400 + ch), dev)
             w, _ = bf16_dev(orc, wl.normal((ch, 27, ch), 0.02, seed=401 + ch), dev)
             y = torch.empty((nl, ch), dtype=torch.bfloat16, device=dev)
-            call = ConvCall(nat, x, w, None, y, ml.token_major, ntaps=27, n_out=nl,
-                            layout=nat.IDX_TOKEN_MAJOR)
+            call = ConvCall(nat, x, nat.pack_weights(w), None, y, ml.token_major, ntaps=27,
+                            n_out=nl, layout=nat.IDX_TOKEN_MAJOR)
             msl, _ = time_gpu(call, args.steps, args.warmup)
             tl = msl / 1e3
             byt = nl * ch * 2 * 2 + w.numel() * 2 + 108 * nl

@@ -58,6 +58,10 @@ typedef enum { SPC_F32 = 0, SPC_F16 = 1, SPC_BF16 = 2, SPC_Q8_0 = 3 } spc_dtype;
 #define SPC_IDX_TOKEN_MAJOR 0  /* [n_out, ntaps]; SRC/sparse_ops.cpp:102-116   */
 #define SPC_IDX_OFFSET_MAJOR 1 /* [ntaps, n_out]; SRC/sparse_ops.cpp:124-133   */
 
+/* Weight layouts accepted by spc_sparse_conv. */
+#define SPC_W_KRSC 0   /* [cout, ntaps, cin]: spconv KRSC = ggml op row format      */
+#define SPC_W_PACKED 1 /* MFMA fragment order, made by spc_conv_pack_weights        */
+
 const char* spc_last_error(void);
 const char* spc_status_string(int status);
 int spc_version(void);
@@ -130,25 +134,36 @@ int spc_subdivide_map(spc_stream_t stream, const int32_t* coords, int64_t n, con
  * taps and channels, one rounding to the output dtype -- and the same
  * contract as the CUDA bridge sam3d_spconv_f16_forward (SPCONV bridge,
  * cpp_ggml/third_party/sam3d-spconv/include/sam3d_spconv_bridge.cuh:10-21),
- * generalised to any tap count (27 submanifold, 8 stride-2):
+ * for 27 taps (submanifold 3x3x3) and 8 taps (2x2x2 stride 2):
  *   y[t, co] = bias[co] + sum_{o, s = idx(t,o) in [0,n_in)} sum_c
  *              w[co, o, c] * x[s, c]
  *   dtype    SPC_F32 / SPC_F16 / SPC_BF16: x, y, bias (and w unless Q8_0)
- *   w_dtype  == dtype, or SPC_Q8_0 with dtype SPC_BF16: w = int8 quants
- *            [cout, ntaps, cin], w_scale = fp16 scales [cout, ntaps, cin/32]
- *            (spc_q8_0_repack makes both from ggml Q8_0 blocks)
+ *   w_dtype  == dtype, or SPC_Q8_0 with dtype SPC_BF16
+ *   w_layout SPC_W_KRSC: w is [cout, ntaps, cin] (Q8_0: int8 quants with
+ *            w_scale = fp16 block scales [cout, ntaps, cin/32], as
+ *            spc_q8_0_repack makes them from ggml blocks);
+ *            SPC_W_PACKED: w from spc_conv_pack_weights (w_scale unused) --
+ *            the fast path, each MFMA operand one contiguous load
  *   idx      SPC_IDX_TOKEN_MAJOR [n_out, ntaps] or SPC_IDX_OFFSET_MAJOR
  *            [ntaps, n_out]; entries outside [0, n_in) are skipped
- *   row_perm optional [n_out]: processing order (e.g. the mask argsort);
- *            processing row r computes and writes output row row_perm[r]
+ *   row_perm optional [n_out]: processing order; processing row r computes
+ *            and writes output row row_perm[r].  Rows in lexicographic
+ *            (natural) order are fastest: the kernel deduplicates the
+ *            gathered rows of each 256-row tile.
  *   bias     may be NULL
- * Each 128-row tile skips the taps none of its rows uses.
- * Requires cin % 32 == 0 and cout % 32 == 0.
+ * Requires ntaps 27 or 8, cin % 32 == 0, cout % 32 == 0.
  * ------------------------------------------------------------------------ */
-int spc_sparse_conv(spc_stream_t stream, int dtype, const void* x, int w_dtype, const void* w,
-                    const void* w_scale, const void* bias, void* y, const int32_t* idx,
-                    int idx_layout, const int32_t* row_perm, int64_t ntaps, int64_t n_out,
-                    int64_t n_in, int64_t cin, int64_t cout);
+int spc_sparse_conv(spc_stream_t stream, int dtype, const void* x, int w_dtype, int w_layout,
+                    const void* w, const void* w_scale, const void* bias, void* y,
+                    const int32_t* idx, int idx_layout, const int32_t* row_perm, int64_t ntaps,
+                    int64_t n_out, int64_t n_in, int64_t cin, int64_t cout);
+
+/* Bytes of the SPC_W_PACKED form of [cout, ntaps, cin] weights of w_dtype
+ * (Q8_0: quants then f32 scales), and the packer.  No reference
+ * counterpart: the packed form is this library's operand layout. */
+size_t spc_conv_packed_bytes(int w_dtype, int64_t ntaps, int64_t cin, int64_t cout);
+int spc_conv_pack_weights(spc_stream_t stream, int w_dtype, const void* w, const void* w_scale,
+                          int64_t ntaps, int64_t cin, int64_t cout, void* packed);
 
 /* Drop-in for the reference's spconv bridge (same name, arguments and
  * layouts as cpp_ggml/third_party/sam3d-spconv/include/

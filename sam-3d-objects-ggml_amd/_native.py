@@ -20,6 +20,7 @@ F32, F16, BF16, Q8_0 = 0, 1, 2, 3
 OK, BAD_SHAPE, BAD_COORD, DUP_COORD, OOM, HIP_ERROR, BAD_ARG = range(7)
 MAP_MESH, MAP_SYNC = 1, 2
 IDX_TOKEN_MAJOR, IDX_OFFSET_MAJOR = 0, 1
+W_KRSC, W_PACKED = 0, 1
 
 _STATUS_NAMES = {BAD_SHAPE: "BAD_SHAPE", BAD_COORD: "BAD_COORD", DUP_COORD: "DUP_COORD",
                  OOM: "OOM", HIP_ERROR: "HIP_ERROR", BAD_ARG: "BAD_ARG"}
@@ -64,8 +65,11 @@ def lib() -> ctypes.CDLL:
     L.spc_subdivide_workspace_bytes.restype = _SZ
     L.spc_subdivide_workspace_bytes.argtypes = [_I64]
     L.spc_subdivide_map.argtypes = [_P, _P, _I64, _P, _P, _P, _P, _P, _SZ]
-    L.spc_sparse_conv.argtypes = [_P, _INT, _P, _INT, _P, _P, _P, _P, _P, _INT, _P, _I64, _I64,
-                                  _I64, _I64, _I64]
+    L.spc_sparse_conv.argtypes = [_P, _INT, _P, _INT, _INT, _P, _P, _P, _P, _P, _INT, _P, _I64,
+                                  _I64, _I64, _I64, _I64]
+    L.spc_conv_packed_bytes.restype = _SZ
+    L.spc_conv_packed_bytes.argtypes = [_INT, _I64, _I64, _I64]
+    L.spc_conv_pack_weights.argtypes = [_P, _INT, _P, _P, _I64, _I64, _I64, _P]
     L.sam3d_spconv_f16_forward.argtypes = [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64]
     L.sam3d_spconv_f16_forward.restype = None
     L.spc_q8_0_repack.argtypes = [_P, _P, _I64, _P, _P]
@@ -210,33 +214,82 @@ def subdivide_map(coords: torch.Tensor, keep: torch.Tensor | None = None):
 # ---------------------------------------------------------------------------
 # feature ops
 # ---------------------------------------------------------------------------
-def sparse_conv(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None,
-                idx: torch.Tensor, *, ntaps: int, n_out: int,
-                idx_layout: int = IDX_TOKEN_MAJOR, row_perm: torch.Tensor | None = None,
-                w_scale: torch.Tensor | None = None, out: torch.Tensor | None = None,
-                cout: int | None = None) -> torch.Tensor:
-    """y = conv(x) through spc_sparse_conv.  weight [Cout, ntaps, Cin] in the
-    feature dtype, or int8 quants with w_scale (fp16 bits as int16/uint16 or
-    float16 tensor) for Q8_0."""
-    _need_gpu(x, weight, bias, idx, row_perm, w_scale)
-    x = x.contiguous()
+@dataclass
+class PackedWeights:
+    """Weights in the kernel's MFMA fragment order (spc_conv_pack_weights)."""
+
+    data: torch.Tensor  # uint8
+    w_dtype: int
+    ntaps: int
+    cin: int
+    cout: int
+
+
+def pack_weights(weight: torch.Tensor, w_scale: torch.Tensor | None = None, *,
+                 cin: int | None = None, cout: int | None = None) -> PackedWeights:
+    """[Cout, ntaps, Cin] weights (or int8 Q8_0 quants + fp16 block scales)
+    -> packed operand layout."""
+    _need_gpu(weight, w_scale)
     weight = weight.contiguous()
-    dt = dtype_code(x.dtype)
     if weight.dtype == torch.int8:
         wdt = Q8_0
         if w_scale is None:
             raise ValueError("Q8_0 weights need w_scale")
         w_scale = w_scale.contiguous()
+        if weight.dim() != 3 and (cin is None or cout is None):
+            raise ValueError("flat Q8_0 quants need cin and cout")
     else:
         wdt = dtype_code(weight.dtype)
+    if weight.dim() == 3:
+        cout, ntaps, cin = weight.shape
+    else:
+        ntaps = weight.numel() // (cin * cout)
+    L = lib()
+    nbytes = L.spc_conv_packed_bytes(wdt, ntaps, cin, cout)
+    out = torch.empty(nbytes, dtype=torch.uint8, device=weight.device)
+    st = L.spc_conv_pack_weights(_stream(weight.device), wdt, _ptr(weight), _ptr(w_scale), ntaps,
+                                 cin, cout, _ptr(out))
+    _check("spc_conv_pack_weights", st)
+    return PackedWeights(out, wdt, ntaps, cin, cout)
+
+
+def sparse_conv(x: torch.Tensor, weight, bias: torch.Tensor | None,
+                idx: torch.Tensor, *, ntaps: int, n_out: int,
+                idx_layout: int = IDX_TOKEN_MAJOR, row_perm: torch.Tensor | None = None,
+                w_scale: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                cout: int | None = None) -> torch.Tensor:
+    """y = conv(x) through spc_sparse_conv.  `weight` is a PackedWeights, a
+    [Cout, ntaps, Cin] tensor in the feature dtype, or int8 Q8_0 quants with
+    w_scale (fp16 block scales)."""
+    _need_gpu(x, bias, idx, row_perm, w_scale)
+    x = x.contiguous()
+    dt = dtype_code(x.dtype)
     cin = x.shape[1]
-    if cout is None:
-        cout = weight.numel() // (ntaps * cin)
+    if isinstance(weight, PackedWeights):
+        _need_gpu(weight.data)
+        wdt, layout, wptr, sptr = weight.w_dtype, W_PACKED, _ptr(weight.data), None
+        cout = weight.cout
+        if weight.ntaps != ntaps or weight.cin != cin:
+            raise ValueError("packed weights do not match ntaps / cin")
+    else:
+        _need_gpu(weight)
+        weight = weight.contiguous()
+        layout = W_KRSC
+        if weight.dtype == torch.int8:
+            wdt = Q8_0
+            if w_scale is None:
+                raise ValueError("Q8_0 weights need w_scale")
+            w_scale = w_scale.contiguous()
+        else:
+            wdt = dtype_code(weight.dtype)
+        wptr, sptr = _ptr(weight), _ptr(w_scale)
+        if cout is None:
+            cout = weight.numel() // (ntaps * cin)
     if bias is not None:
         bias = bias.contiguous()
     if out is None:
         out = torch.empty((n_out, cout), dtype=x.dtype, device=x.device)
-    st = lib().spc_sparse_conv(_stream(x.device), dt, _ptr(x), wdt, _ptr(weight), _ptr(w_scale),
+    st = lib().spc_sparse_conv(_stream(x.device), dt, _ptr(x), wdt, layout, wptr, sptr,
                                _ptr(bias), _ptr(out), _ptr(idx), idx_layout, _ptr(row_perm),
                                ntaps, n_out, x.shape[0], cin, cout)
     _check("spc_sparse_conv", st)

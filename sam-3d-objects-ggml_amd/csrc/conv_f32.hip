@@ -1,0 +1,9 @@
+// conv_f32.hip -- instantiations of the sparse-conv kernel (conv_kernel.h)
+// for one operand type, compiled as a separate unit to parallelise the build.
+#include "conv_kernel.h"
+
+namespace spc {
+
+hipError_t conv_f32(hipStream_t s, const ConvArgs& a) { return dispatch_conv<float, false>(s, a); }
+
+}  // namespace spc

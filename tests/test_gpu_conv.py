@@ -52,13 +52,18 @@ def test_bf16_channels(spc, orc, dev, cin, cout):
     _case(f"bf16 subm N={n} cin={cin} cout={cout}")
     x, w, b = _bf16_inputs(spc, orc, n, cin, cout, seed=cin)
     m = nat.map_build(torch.from_numpy(coords).to(dev))
-    y = nat.sparse_conv(to_dev_bf16(x, dev), to_dev_bf16(w, dev), to_dev_bf16(b, dev),
-                        m.token_major, ntaps=27, n_out=n)
+    wd = to_dev_bf16(w, dev)
+    y = nat.sparse_conv(to_dev_bf16(x, dev), wd, to_dev_bf16(b, dev), m.token_major, ntaps=27,
+                        n_out=n)
+    yp = nat.sparse_conv(to_dev_bf16(x, dev), nat.pack_weights(wd), to_dev_bf16(b, dev),
+                         m.token_major, ntaps=27, n_out=n)
     torch.cuda.synchronize()
     tm = m.token_major.cpu().numpy()
     rows = np.arange(n)
     ref = _oracle_bf16(orc, x, w, b, tm, rows, 27, n)
     assert max_rel(from_dev(y), ref) <= MAXREL
+    # both weight layouts feed identical operands in identical order
+    assert torch.equal(y, yp)
 
 
 def test_bf16_config2_ellipsoids(spc, orc, dev):
@@ -72,7 +77,7 @@ def test_bf16_config2_ellipsoids(spc, orc, dev):
     x, w, b = _bf16_inputs(spc, orc, n, 128, 128, seed=20)
     m = nat.map_build(torch.from_numpy(coords).to(dev))
     xd, wd, bd = to_dev_bf16(x, dev), to_dev_bf16(w, dev), to_dev_bf16(b, dev)
-    y = nat.sparse_conv(xd, wd, bd, m.token_major, ntaps=27, n_out=n)
+    y = nat.sparse_conv(xd, nat.pack_weights(wd), bd, m.token_major, ntaps=27, n_out=n)
     # the same conv in mask-argsort processing order (offset-major indices)
     y2 = nat.sparse_conv(xd, wd, bd, m.offset_major, ntaps=27, n_out=n,
                          idx_layout=nat.IDX_OFFSET_MAJOR, row_perm=m.argsort)
@@ -100,8 +105,12 @@ def test_f32_config1_sphere(spc, orc, dev):
     w = wl.normal((64, 27, 64), 0.02, seed=32)
     b = np.zeros(64, np.float32)
     m = nat.map_build(torch.from_numpy(coords).to(dev))
-    y = nat.sparse_conv(torch.from_numpy(x).to(dev), torch.from_numpy(w).to(dev),
+    wd = torch.from_numpy(w).to(dev)
+    y = nat.sparse_conv(torch.from_numpy(x).to(dev), nat.pack_weights(wd),
                         torch.from_numpy(b).to(dev), m.token_major, ntaps=27, n_out=n)
+    y_raw = nat.sparse_conv(torch.from_numpy(x).to(dev), wd, torch.from_numpy(b).to(dev),
+                            m.token_major, ntaps=27, n_out=n)
+    assert torch.equal(y, y_raw)
     torch.cuda.synchronize()
     rows = _sample_rows(n, 2048, seed=3)
     sub = row_subset(m.token_major.cpu().numpy(), n, rows)
@@ -154,7 +163,11 @@ def test_q8_0_config5_sphere(spc, orc, dev):
     m = nat.map_build(torch.from_numpy(coords).to(dev))
     y = nat.sparse_conv(to_dev_bf16(x, dev), qs, to_dev_bf16(b, dev), m.token_major, ntaps=27,
                         n_out=n, w_scale=d, cout=c)
+    pw = nat.pack_weights(qs, d, cin=c, cout=c)
+    yp = nat.sparse_conv(to_dev_bf16(x, dev), pw, to_dev_bf16(b, dev), m.token_major, ntaps=27,
+                         n_out=n)
     torch.cuda.synchronize()
+    assert torch.equal(y, yp)
     w16 = orc.q8_0_dequant(blocks, oracle.F16)
     rows = _sample_rows(n, 64, seed=5)
     sub = row_subset(m.token_major.cpu().numpy(), n, rows)
@@ -174,8 +187,12 @@ def test_stride2_conv(spc, orc, dev):
     _case(f"stride2 conv nf={nf}")
     d = nat.downsample_map(torch.from_numpy(coords).to(dev), 4, 64)
     x, w, b = _bf16_inputs(spc, orc, nf, 128, 128, ntaps=8, seed=60)
-    y = nat.sparse_conv(to_dev_bf16(x, dev), to_dev_bf16(w, dev), to_dev_bf16(b, dev),
+    wd = to_dev_bf16(w, dev)
+    y = nat.sparse_conv(to_dev_bf16(x, dev), nat.pack_weights(wd), to_dev_bf16(b, dev),
                         d.stride2_taps, ntaps=8, n_out=d.nc)
+    y_raw = nat.sparse_conv(to_dev_bf16(x, dev), wd, to_dev_bf16(b, dev), d.stride2_taps,
+                            ntaps=8, n_out=d.nc)
+    assert torch.equal(y, y_raw)
     torch.cuda.synchronize()
     taps = d.stride2_taps.cpu().numpy()
     rows = _sample_rows(d.nc, 1024, seed=6)
