@@ -470,39 +470,73 @@ __global__ __launch_bounds__(kThreads, 1) void conv_kernel(ConvArgs a) {
     // Weight ring: the operands of step m are loaded into ring[m % kPD]
     // during step m - kPD; the step body is instantiated once per ring
     // position so every slot index is a compile-time constant.
+    // A operands of one step: union slots of the wave's rows for a tap, and
+    // the fragments read from them.  Slots depend only on the tap, so they
+    // are read two steps ahead; fragments one step ahead (within a chunk),
+    // overlapping the LDS latency with the current step's MFMAs.
+    typedef typename M::frag AFrag[P::KS][FM];
+    auto read_slots = [&](int o, int* sl) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            const int rl = wm * WTM + i * 32 + (lane & 31);
+            sl[i] = fast ? sidx[o * TM + rl] : rl;
+        }
+    };
+    auto read_frags = [&](const int* sl, AFrag& f) __attribute__((always_inline)) {
+#pragma unroll
+        for (int ks = 0; ks < P::KS; ++ks) {
+            const int kof = ks * M::KSUB + (lane >> 5) * M::EPL;
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+                f[ks][i] = *reinterpret_cast<const typename M::frag*>(&Au[sl[i] * PITCH + kof]);
+        }
+    };
+    AFrag afc;         // fragments of the current step
+    int slot_n[FM];    // slots of the next step
+
     auto step = [&](int s, auto u_const) __attribute__((always_inline)) {
         constexpr int u = decltype(u_const)::value;
         const int o = __ffs(cc.m) - 1;
+        const Cursor nc = advance(cc);  // step s+1
         if (fast ? cc.m == tile_mask : true) {  // first tap of a chunk, or every step
             if (s > 0) lds_barrier();           // every wave is done reading Au
             stage_a(o, cc.kc);
             lds_barrier();
+            int sl[FM];
+            read_slots(o, sl);
+            read_frags(sl, afc);
+            if (s + 1 < nsteps) read_slots(__ffs(nc.m) - 1, slot_n);
         }
-        int slot[FM];
-#pragma unroll
-        for (int i = 0; i < FM; ++i) {
-            const int rl = wm * WTM + i * 32 + (lane & 31);
-            slot[i] = fast ? sidx[o * TM + rl] : rl;
-        }
+        // prefetch: fragments of step s+1 (same chunk) and slots of step s+2
+        const bool next_same_chunk = fast && s + 1 < nsteps && nc.kc == cc.kc;
+        AFrag afn;
+        if (next_same_chunk) read_frags(slot_n, afn);
+        int slot_nn[FM];
+        if (s + 2 < nsteps) read_slots(__ffs(advance(nc).m) - 1, slot_nn);
 #pragma unroll
         for (int ks = 0; ks < P::KS; ++ks) {
-            typename M::frag af[FM];
-            const int kof = ks * M::KSUB + (lane >> 5) * M::EPL;
-#pragma unroll
-            for (int i = 0; i < FM; ++i)
-                af[i] = *reinterpret_cast<const typename M::frag*>(&Au[slot[i] * PITCH + kof]);
 #pragma unroll
             for (int j = 0; j < FN; ++j) {
                 const typename M::frag bf = b_frag(ring[u], j, ks);
 #pragma unroll
-                for (int i = 0; i < FM; ++i) acc[i][j] = M::mma(af[i], bf, acc[i][j]);
+                for (int i = 0; i < FM; ++i) acc[i][j] = M::mma(afc[ks][i], bf, acc[i][j]);
             }
+        }
+        if (next_same_chunk) {
+#pragma unroll
+            for (int ks = 0; ks < P::KS; ++ks)
+#pragma unroll
+                for (int i = 0; i < FM; ++i) afc[ks][i] = afn[ks][i];
+        }
+        if (s + 2 < nsteps) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i) slot_n[i] = slot_nn[i];
         }
         if (s + kPD < nsteps) {
             load_b(pc, ring[u]);
             pc = advance(pc);
         }
-        cc = advance(cc);
+        cc = nc;
     };
 
     static_assert(kPD == 3, "the prologue and the unrolled loop assume a 3-deep ring");
