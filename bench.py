@@ -50,8 +50,10 @@ def parse():
     ap.add_argument("--order", choices=["natural", "mask"], default="natural",
                     help="row processing order of the conv kernel")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--cpu-seconds", type=float, default=8.0,
-                    help="target duration of the all-core CPU baseline sample")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="target duration of the all-core CPU baseline sample (5 runs)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only time a 256 MiB device copy (PMC traffic calibration)")
     return ap.parse_args()
 
 
@@ -120,10 +122,28 @@ def traffic_from_profile(name: str):
     return float(m.group(1)) if m else None
 
 
-def cpu_baseline(orc, x_bits, w_bits, b_bits, tm, n, cin, cout, target_s, ntaps=27,
+def _host_cpu():
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            m = re.search(r"model name\s*:\s*(.*)", f.read())
+            model = m.group(1).strip() if m else ""
+    except OSError:
+        pass
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    return model, avail
+
+
+def cpu_baseline(orc, x_bits, w_bits, b_bits, tm, coords, n, cin, cout, target_s, ntaps=27,
                  x_dt=None, w_dt=None):
-    """Times the oracle conv (ggml CPU op restatement) on the host over the first
-    S output rows, S chosen so the all-core run lasts about target_s."""
+    """Times the oracle conv (the ggml CPU op's F32-accumulate loop, token
+    partition across threads) on the host over the first S output rows, S
+    sized so one run lasts about target_s / 5: 1 warm-up, median of 5.  Also
+    one thread (the op's likely n_tasks = 1) and the std::map neighbour-map
+    build on one thread."""
     import oracle
 
     x_dt = oracle.BF16 if x_dt is None else x_dt
@@ -139,27 +159,51 @@ def cpu_baseline(orc, x_bits, w_bits, b_bits, tm, n, cin, cout, target_s, ntaps=
                         nthreads=th)
         return time.perf_counter() - t0
 
+    def median_of(k, fn):
+        fn()  # warm-up
+        return float(np.median([fn() for _ in range(k)]))
+
     probe = min(n, 64 * threads)
     t = run(probe, threads)
-    rows = int(min(n, max(probe, probe * target_s / max(t, 1e-6))))
-    times = [run(rows, threads) for _ in range(2)]
-    t_all = min(times)
-    rows1 = max(64, rows // (2 * threads))
-    t_one = run(rows1, 1)
-    model = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            m = re.search(r"model name\s*:\s*(.*)", f.read())
-            model = m.group(1).strip() if m else ""
-    except OSError:
-        pass
+    rows = int(min(n, max(probe, probe * (target_s / 5) / max(t, 1e-6))))
+    t_all = median_of(5, lambda: run(rows, threads))
+    t1 = run(64, 1)
+    rows1 = int(min(n, max(64, 64 * (target_s / 10) / max(t1, 1e-6))))
+    t_one = median_of(3, lambda: run(rows1, 1))
+
+    def build_map():
+        t0 = time.perf_counter()
+        tm_c = orc.conv_table_slat(coords)
+        orc.spconv_tables(tm_c, n)
+        return time.perf_counter() - t0
+
+    t_map = median_of(5, build_map)
+    model, avail = _host_cpu()
     return {
         "value": rows / t_all / 1e6, "unit": "Mvoxel/s", "cores": threads, "kind": "port",
-        "sample": f"first {rows} of {n} output rows, {threads} threads (ggml op token "
-                  f"partition), best of 2; host '{model}'",
+        "sample": f"first {rows} of {n} output rows, {threads} threads (the op's token "
+                  f"partition), 1 warm-up + median of 5; host '{model}', {avail} CPUs "
+                  "available",
         "single_thread": {"value": rows1 / t_one / 1e6, "unit": "Mvoxel/s", "cores": 1,
-                          "sample": f"first {rows1} rows, 1 thread"},
+                          "sample": f"first {rows1} rows, 1 thread, median of 3"},
+        "map_build_1thread_ms": {"value": t_map * 1e3, "cores": 1,
+                                 "sample": f"std::map 27-offset table + stable mask argsort, "
+                                           f"all {n} voxels, median of 5"},
     }
+
+
+def copy_calibration(steps: int):
+    """Plain device-to-device copies of a known size: the FETCH_SIZE /
+    WRITE_SIZE scale factors for the conv kernel's PMC traffic."""
+    import torch
+
+    nbytes = 256 << 20
+    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda:0").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    ms, _ = time_gpu(lambda: dst.copy_(src), steps, 3)
+    print(json.dumps({"copy_bytes_read": nbytes, "copy_bytes_written": nbytes,
+                      "ms_per_copy": ms, "gbs": 2 * nbytes / (ms / 1e3) / 1e9}))
 
 
 def main():
@@ -172,6 +216,10 @@ def main():
         sys.exit(2)
 
     import torch
+
+    if args.copy_calibration:
+        copy_calibration(args.steps)
+        return
 
     import __graft_entry__
 
@@ -295,8 +343,8 @@ def main():
                          "algorithmic_flops_per_launch": flops},
         }
         if not args.no_cpu:
-            result["cpu_baseline"] = cpu_baseline(orc, xb, wb, bb, tm_host, n, cin, cout,
-                                                  args.cpu_seconds, x_dt=cpu_dt[0],
+            result["cpu_baseline"] = cpu_baseline(orc, xb, wb, bb, tm_host, coords, n, cin,
+                                                  cout, args.cpu_seconds, x_dt=cpu_dt[0],
                                                   w_dt=cpu_dt[1])
     elif cfg == 3:
         d = nat.downsample_map(c_dev, 4, 64)

@@ -58,9 +58,17 @@ typedef enum { SPC_F32 = 0, SPC_F16 = 1, SPC_BF16 = 2, SPC_Q8_0 = 3 } spc_dtype;
 #define SPC_IDX_TOKEN_MAJOR 0  /* [n_out, ntaps]; SRC/sparse_ops.cpp:102-116   */
 #define SPC_IDX_OFFSET_MAJOR 1 /* [ntaps, n_out]; SRC/sparse_ops.cpp:124-133   */
 
-/* Weight layouts accepted by spc_sparse_conv. */
-#define SPC_W_KRSC 0   /* [cout, ntaps, cin]: spconv KRSC = ggml op row format      */
+/* Weight layouts.  spc_sparse_conv takes SPC_W_KRSC or SPC_W_PACKED;
+ * spc_conv_pack_weights reads SPC_W_KRSC, SPC_W_TCK or SPC_W_TKC. */
+#define SPC_W_KRSC 0   /* [cout, ntaps, cin]: spconv KRSC = ggml op row format
+                          (PATCH:241-243; cpp_ggml/scripts/gguf_schema.py:330-338) */
 #define SPC_W_PACKED 1 /* MFMA fragment order, made by spc_conv_pack_weights        */
+#define SPC_W_TCK 2    /* [ntaps, cout, cin]: mesh-decoder GGUF rows, one (Cout,Cin)
+                          matrix per offset (cpp_ggml/scripts/convert_sam3d_to_gguf.py:
+                          508-511; SRC/mesh_decoder_graph.cpp:285-289,334-337)      */
+#define SPC_W_TKC 3    /* [ntaps, cin, cout]: w[o][ci][co].  With ntaps = 1 this is the
+                          1x1x1 skip conv's raw view of its saved [cout,1,1,1,cin]
+                          buffer as (cin, cout) (SRC/mesh_decoder_graph.cpp:349-376) */
 
 const char* spc_last_error(void);
 const char* spc_status_string(int status);
@@ -114,6 +122,15 @@ int spc_downsample_map(spc_stream_t stream, const int32_t* coords, int64_t nf, i
                        int32_t* children, float* counts, int32_t* stride2_taps,
                        int64_t* nc_out, void* workspace, size_t workspace_bytes);
 
+/* Map of the transposed 2x2x2 stride-2 conv (SparseInverseConv3d after a
+ * stride-2 SparseConv3d, SP/conv/conv_spconv.py:92-139): taps [nf*8] with
+ * taps[f*8 + k(f)] = fine_to_coarse[f] for the fine row's own tap k(f) =
+ * (x&1)*4 + (y&1)*2 + (z&1), every other entry nc.  Used as the token-major
+ * index table of spc_sparse_conv with ntaps 8, n_out nf, n_in nc. */
+int spc_stride2_inverse_taps(spc_stream_t stream, const int32_t* coords,
+                             const int32_t* fine_to_coarse, int64_t nf, int64_t nc,
+                             int32_t* taps);
+
 /* ------------------------------------------------------------------------
  * Subdivide map.  Replaces subdivide_mesh_level (SRC/sparse_ops.cpp:
  * 348-371) and SparseSubdivide's coordinates (SP/spatial.py:108-124).
@@ -151,19 +168,27 @@ int spc_subdivide_map(spc_stream_t stream, const int32_t* coords, int64_t n, con
  *            (natural) order are fastest: the kernel deduplicates the
  *            gathered rows of each 256-row tile.
  *   bias     may be NULL
- * Requires ntaps 27 or 8, cin % 32 == 0, cout % 32 == 0.
+ * Requires ntaps 27, 8 or 1, cin % 32 == 0, cout % 32 == 0.  With ntaps 1
+ * and idx NULL the map is the identity (n_in == n_out): the dense 1x1x1
+ * conv y = x W^T + b of sparse_conv_1x1 (SRC/mesh_decoder_graph.cpp:349-384).
  * ------------------------------------------------------------------------ */
 int spc_sparse_conv(spc_stream_t stream, int dtype, const void* x, int w_dtype, int w_layout,
                     const void* w, const void* w_scale, const void* bias, void* y,
                     const int32_t* idx, int idx_layout, const int32_t* row_perm, int64_t ntaps,
                     int64_t n_out, int64_t n_in, int64_t cin, int64_t cout);
 
-/* Bytes of the SPC_W_PACKED form of [cout, ntaps, cin] weights of w_dtype
- * (Q8_0: quants then f32 scales), and the packer.  No reference
- * counterpart: the packed form is this library's operand layout. */
+/* Bytes of the SPC_W_PACKED form of ntaps x cout x cin weights of w_dtype
+ * (Q8_0: quants then f32 scales), and the packer.  w_layout (SPC_W_KRSC,
+ * SPC_W_TCK or SPC_W_TKC) says how w is stored.  Q8_0 quants (int8) come
+ * with fp16 block scales w_scale, one per 32 consecutive stored channels,
+ * which must run along cin: SPC_W_KRSC or SPC_W_TCK (SPC_W_TKC Q8_0 weights
+ * are dequantised first, as the reference does, SRC/mesh_decoder_graph.cpp:
+ * 370-372).  No reference counterpart: the packed form is this library's
+ * operand layout. */
 size_t spc_conv_packed_bytes(int w_dtype, int64_t ntaps, int64_t cin, int64_t cout);
-int spc_conv_pack_weights(spc_stream_t stream, int w_dtype, const void* w, const void* w_scale,
-                          int64_t ntaps, int64_t cin, int64_t cout, void* packed);
+int spc_conv_pack_weights(spc_stream_t stream, int w_dtype, int w_layout, const void* w,
+                          const void* w_scale, int64_t ntaps, int64_t cin, int64_t cout,
+                          void* packed);
 
 /* Drop-in for the reference's spconv bridge (same name, arguments and
  * layouts as cpp_ggml/third_party/sam3d-spconv/include/
@@ -185,6 +210,18 @@ void sam3d_spconv_f16_forward(spc_stream_t stream, const void* input, const void
  * aligned streams for the GEMM's in-register dequantisation). */
 int spc_q8_0_repack(spc_stream_t stream, const uint8_t* blocks, int64_t nblocks, int8_t* qs,
                     uint16_t* d);
+
+/* quantize_q8_0 (cpp_ggml/scripts/gguf_schema.py:14-24) on the GPU: n
+ * floats (n % 32 == 0) -> n/32 blocks of 34 bytes.  Per block d =
+ * fp16(amax / 127) (amax 0 -> 1e-12), q = clip(rint(w / f32(d)), -127, 127)
+ * with rint rounding half to even.  Bit-exact with the converter. */
+int spc_q8_0_quantize(spc_stream_t stream, const float* w, int64_t n, uint8_t* blocks);
+
+/* Q8_0 blocks -> f32(d) * q in out_dtype (SPC_F32, SPC_F16 or SPC_BF16):
+ * the reference's as_f32 / as_f16 dequantisation (SRC/slat_flow_graph.cpp:
+ * 24-27; SRC/mesh_decoder_graph.cpp:309-312). */
+int spc_q8_0_dequant(spc_stream_t stream, const uint8_t* blocks, int64_t nblocks, int out_dtype,
+                     void* out);
 
 /* ------------------------------------------------------------------------
  * Scatter-mean.  Replaces ggml_sam3d_sparse_scatter_mean (PATCH:59-63,

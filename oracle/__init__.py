@@ -77,6 +77,8 @@ class _Oracle:
         lib.orc_scatter_mean.argtypes = [_INT, _P, _P, _P, _P, _I64, _I64, _I64, _INT]
         lib.orc_q8_0_quantize.argtypes = [_P, _I64, _P]
         lib.orc_q8_0_dequant.argtypes = [_P, _I64, _INT, _P]
+        lib.orc_scatter_case.argtypes = [_I64, _I64, _I64, _I32, _P, _P, _P]
+        lib.orc_scatter_case.restype = None
         for f in ("orc_f32_to_f16", "orc_f16_to_f32", "orc_f32_to_bf16"):
             getattr(lib, f).argtypes = [_P, _P, _I64]
             getattr(lib, f).restype = None
@@ -179,6 +181,15 @@ class _Oracle:
         if st != OK:
             raise ValueError(f"orc_scatter_mean status {st}")
         return out
+
+    def scatter_case(self, channels: int, nf: int, nc: int, seed: int):
+        """Inputs of the reference scatter-mean test case (channels, nf, nc,
+        seed): (f16 features [nf, channels] as uint16 bits, rows, counts)."""
+        f = np.empty((nf, channels), np.uint16)
+        r = np.empty(nf, np.int32)
+        c = np.empty(nc, np.float32)
+        self.lib.orc_scatter_case(channels, nf, nc, seed, _ptr(f), _ptr(r), _ptr(c))
+        return f, r, c
 
     def q8_0_quantize(self, w: np.ndarray) -> np.ndarray:
         w = np.ascontiguousarray(w, dtype=np.float32).reshape(-1)

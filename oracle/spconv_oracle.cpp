@@ -39,6 +39,7 @@
 #include <cstdint>
 #include <cstring>
 #include <map>
+#include <random>
 #include <thread>
 #include <tuple>
 #include <vector>
@@ -509,6 +510,31 @@ int orc_q8_0_dequant(const uint8_t* blocks, int64_t nblocks, int out_dtype, void
         }
     }
     return ORC_OK;
+}
+
+// Inputs of one case of the reference's scatter-mean regression test
+// (SRC/scatter_mean_backend_test.cpp:35-75), drawn with the same engine and
+// distributions in the same order: f16 features uniform in [-4, 4); the
+// first min(nc, nf) fine rows hit coarse rows 0.. in order; every later row
+// draws rng() % 16 -- 15 -> -1, 14 -> nc (both skipped), else a uniform
+// coarse row; counts = hits per coarse row.
+void orc_scatter_case(int64_t channels, int64_t nf, int64_t nc, int32_t seed,
+                      uint16_t* features, int32_t* rows, float* counts) {
+    std::mt19937 rng((uint32_t)seed);
+    std::uniform_real_distribution<float> uniform(-4.0f, 4.0f);
+    for (int64_t i = 0; i < channels * nf; ++i) features[i] = f2h(uniform(rng));
+    std::uniform_int_distribution<int32_t> pick(0, (int32_t)nc - 1);
+    const int64_t pinned = std::min(nc, nf);
+    for (int64_t i = 0; i < pinned; ++i) rows[i] = (int32_t)i;
+    for (int64_t i = pinned; i < nf; ++i) {
+        const uint32_t draw = rng() % 16;
+        if (draw == 15) rows[i] = -1;
+        else if (draw == 14) rows[i] = (int32_t)nc;
+        else rows[i] = pick(rng);
+    }
+    for (int64_t r = 0; r < nc; ++r) counts[r] = 0.0f;
+    for (int64_t i = 0; i < nf; ++i)
+        if (rows[i] >= 0 && rows[i] < nc) counts[rows[i]] += 1.0f;
 }
 
 // Scalar conversions exposed for tests.

@@ -20,7 +20,7 @@ F32, F16, BF16, Q8_0 = 0, 1, 2, 3
 OK, BAD_SHAPE, BAD_COORD, DUP_COORD, OOM, HIP_ERROR, BAD_ARG = range(7)
 MAP_MESH, MAP_SYNC = 1, 2
 IDX_TOKEN_MAJOR, IDX_OFFSET_MAJOR = 0, 1
-W_KRSC, W_PACKED = 0, 1
+W_KRSC, W_PACKED, W_TCK, W_TKC = 0, 1, 2, 3
 
 _STATUS_NAMES = {BAD_SHAPE: "BAD_SHAPE", BAD_COORD: "BAD_COORD", DUP_COORD: "DUP_COORD",
                  OOM: "OOM", HIP_ERROR: "HIP_ERROR", BAD_ARG: "BAD_ARG"}
@@ -62,6 +62,7 @@ def lib() -> ctypes.CDLL:
     L.spc_downsample_workspace_bytes.restype = _SZ
     L.spc_downsample_workspace_bytes.argtypes = [_I64]
     L.spc_downsample_map.argtypes = [_P, _P, _I64, _I64, _I32, _P, _P, _P, _P, _P, _P, _P, _SZ]
+    L.spc_stride2_inverse_taps.argtypes = [_P, _P, _P, _I64, _I64, _P]
     L.spc_subdivide_workspace_bytes.restype = _SZ
     L.spc_subdivide_workspace_bytes.argtypes = [_I64]
     L.spc_subdivide_map.argtypes = [_P, _P, _I64, _P, _P, _P, _P, _P, _SZ]
@@ -69,10 +70,12 @@ def lib() -> ctypes.CDLL:
                                   _I64, _I64, _I64, _I64]
     L.spc_conv_packed_bytes.restype = _SZ
     L.spc_conv_packed_bytes.argtypes = [_INT, _I64, _I64, _I64]
-    L.spc_conv_pack_weights.argtypes = [_P, _INT, _P, _P, _I64, _I64, _I64, _P]
+    L.spc_conv_pack_weights.argtypes = [_P, _INT, _INT, _P, _P, _I64, _I64, _I64, _P]
     L.sam3d_spconv_f16_forward.argtypes = [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64]
     L.sam3d_spconv_f16_forward.restype = None
     L.spc_q8_0_repack.argtypes = [_P, _P, _I64, _P, _P]
+    L.spc_q8_0_quantize.argtypes = [_P, _P, _I64, _P]
+    L.spc_q8_0_dequant.argtypes = [_P, _P, _I64, _INT, _P]
     L.spc_scatter_mean_workspace_bytes.restype = _SZ
     L.spc_scatter_mean_workspace_bytes.argtypes = [_I64, _I64]
     L.spc_scatter_mean.argtypes = [_P, _INT, _P, _P, _P, _P, _I64, _I64, _I64, _P, _SZ]
@@ -190,6 +193,20 @@ def downsample_map(coords: torch.Tensor, n_batch: int, resolution: int,
                          None if taps is None else taps[: 8 * k])
 
 
+def stride2_inverse_taps(fine_coords: torch.Tensor, fine_to_coarse: torch.Tensor,
+                         nc: int) -> torch.Tensor:
+    """Token-major [nf*8] map of the transposed stride-2 conv (coarse -> fine)."""
+    _need_gpu(fine_coords, fine_to_coarse)
+    fine_coords = fine_coords.contiguous()
+    f2c = fine_to_coarse.to(torch.int32).contiguous()
+    nf = fine_coords.shape[0]
+    taps = torch.empty(8 * nf, dtype=torch.int32, device=fine_coords.device)
+    st = lib().spc_stride2_inverse_taps(_stream(fine_coords.device), _ptr(fine_coords), _ptr(f2c),
+                                        nf, int(nc), _ptr(taps))
+    _check("spc_stride2_inverse_taps", st)
+    return taps
+
+
 def subdivide_map(coords: torch.Tensor, keep: torch.Tensor | None = None):
     """Returns (child coords [m,4], parent [m]) in parent-major order."""
     _need_gpu(coords, keep)
@@ -226,9 +243,12 @@ class PackedWeights:
 
 
 def pack_weights(weight: torch.Tensor, w_scale: torch.Tensor | None = None, *,
-                 cin: int | None = None, cout: int | None = None) -> PackedWeights:
-    """[Cout, ntaps, Cin] weights (or int8 Q8_0 quants + fp16 block scales)
-    -> packed operand layout."""
+                 cin: int | None = None, cout: int | None = None, ntaps: int | None = None,
+                 layout: int = W_KRSC) -> PackedWeights:
+    """Weights -> the kernel's packed operand layout.  `layout` says how
+    `weight` is stored: W_KRSC [Cout, ntaps, Cin], W_TCK [ntaps, Cout, Cin]
+    or W_TKC [ntaps, Cin, Cout].  int8 weights are Q8_0 quants with fp16
+    block scales `w_scale` (blocks along Cin)."""
     _need_gpu(weight, w_scale)
     weight = weight.contiguous()
     if weight.dtype == torch.int8:
@@ -236,31 +256,48 @@ def pack_weights(weight: torch.Tensor, w_scale: torch.Tensor | None = None, *,
         if w_scale is None:
             raise ValueError("Q8_0 weights need w_scale")
         w_scale = w_scale.contiguous()
-        if weight.dim() != 3 and (cin is None or cout is None):
-            raise ValueError("flat Q8_0 quants need cin and cout")
     else:
         wdt = dtype_code(weight.dtype)
     if weight.dim() == 3:
-        cout, ntaps, cin = weight.shape
+        a, b, c = weight.shape
+        if layout == W_KRSC:
+            cout, ntaps, cin = a, b, c
+        elif layout == W_TCK:
+            ntaps, cout, cin = a, b, c
+        elif layout == W_TKC:
+            ntaps, cin, cout = a, b, c
+        else:
+            raise ValueError(f"unknown weight layout {layout}")
     else:
-        ntaps = weight.numel() // (cin * cout)
+        known = [v for v in (cin, cout, ntaps) if v is not None]
+        if len(known) < 2:
+            raise ValueError("a flat weight needs two of cin, cout, ntaps")
+        if ntaps is None:
+            ntaps = weight.numel() // (cin * cout)
+        elif cin is None:
+            cin = weight.numel() // (ntaps * cout)
+        elif cout is None:
+            cout = weight.numel() // (ntaps * cin)
+        if ntaps * cin * cout != weight.numel():
+            raise ValueError("weight size does not match ntaps * cin * cout")
     L = lib()
     nbytes = L.spc_conv_packed_bytes(wdt, ntaps, cin, cout)
     out = torch.empty(nbytes, dtype=torch.uint8, device=weight.device)
-    st = L.spc_conv_pack_weights(_stream(weight.device), wdt, _ptr(weight), _ptr(w_scale), ntaps,
-                                 cin, cout, _ptr(out))
+    st = L.spc_conv_pack_weights(_stream(weight.device), wdt, int(layout), _ptr(weight),
+                                 _ptr(w_scale), ntaps, cin, cout, _ptr(out))
     _check("spc_conv_pack_weights", st)
     return PackedWeights(out, wdt, ntaps, cin, cout)
 
 
 def sparse_conv(x: torch.Tensor, weight, bias: torch.Tensor | None,
-                idx: torch.Tensor, *, ntaps: int, n_out: int,
+                idx: torch.Tensor | None, *, ntaps: int, n_out: int,
                 idx_layout: int = IDX_TOKEN_MAJOR, row_perm: torch.Tensor | None = None,
                 w_scale: torch.Tensor | None = None, out: torch.Tensor | None = None,
                 cout: int | None = None) -> torch.Tensor:
     """y = conv(x) through spc_sparse_conv.  `weight` is a PackedWeights, a
     [Cout, ntaps, Cin] tensor in the feature dtype, or int8 Q8_0 quants with
-    w_scale (fp16 block scales)."""
+    w_scale (fp16 block scales).  idx None with ntaps 1 is the identity map
+    (the dense 1x1x1 conv)."""
     _need_gpu(x, bias, idx, row_perm, w_scale)
     x = x.contiguous()
     dt = dtype_code(x.dtype)
@@ -322,6 +359,30 @@ def q8_0_repack(blocks: torch.Tensor):
     st = lib().spc_q8_0_repack(_stream(blocks.device), _ptr(blocks), nb, _ptr(qs), _ptr(d))
     _check("spc_q8_0_repack", st)
     return qs, d
+
+
+def q8_0_quantize(w: torch.Tensor) -> torch.Tensor:
+    """float32 weights (numel % 32 == 0, blocks along the last, contiguous
+    dimension) -> ggml Q8_0 blocks (uint8, 34 bytes per block)."""
+    _need_gpu(w)
+    w = w.to(torch.float32).contiguous()
+    n = w.numel()
+    out = torch.empty(n // 32 * 34, dtype=torch.uint8, device=w.device)
+    st = lib().spc_q8_0_quantize(_stream(w.device), _ptr(w), n, _ptr(out))
+    _check("spc_q8_0_quantize", st)
+    return out
+
+
+def q8_0_dequant(blocks: torch.Tensor, dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """ggml Q8_0 blocks -> f32(d) * q as a flat tensor of `dtype`."""
+    _need_gpu(blocks)
+    blocks = blocks.contiguous()
+    nb = blocks.numel() // 34
+    out = torch.empty(nb * 32, dtype=dtype, device=blocks.device)
+    st = lib().spc_q8_0_dequant(_stream(blocks.device), _ptr(blocks), nb, dtype_code(dtype),
+                                _ptr(out))
+    _check("spc_q8_0_dequant", st)
+    return out
 
 
 def scatter_mean(features: torch.Tensor, rows: torch.Tensor, counts: torch.Tensor,

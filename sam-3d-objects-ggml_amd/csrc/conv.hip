@@ -14,10 +14,20 @@ size_t packed_quant_bytes(int64_t ntaps, int64_t cin, int64_t cout) {
     return (size_t)ntaps * cin * cout * Panel<T, Q8>::WB;
 }
 
+// Element strides of a stored weight tensor per layout (SPC_W_KRSC / TCK / TKC).
+struct WStride {
+    int64_t co, o, ci;
+};
+WStride weight_strides(int layout, int64_t ntaps, int64_t cin, int64_t cout) {
+    if (layout == SPC_W_TCK) return {cin, cout * cin, 1};
+    if (layout == SPC_W_TKC) return {1, cin * cout, cout};
+    return {ntaps * cin, cin, 1};  // SPC_W_KRSC
+}
+
 // One thread per 16-byte panel word: panel (tap, chunk, c32), word g, lane.
 template <typename T, bool Q8>
 __global__ void pack_weights_kernel(const uint8_t* __restrict__ w, u32x4* __restrict__ out,
-                                    int ntaps, int cin, int cout) {
+                                    int ntaps, int cin, int cout, WStride st) {
     using P = Panel<T, Q8>;
     const int kch = cin / P::KC;
     const int ncol32 = cout / 32;
@@ -34,14 +44,17 @@ __global__ void pack_weights_kernel(const uint8_t* __restrict__ w, u32x4* __rest
     const int o = (int)(tk / kch);
     const int co = c32 * 32 + (lane & 31);
     uint8_t bytes[16];
-    constexpr int BPK = 16 / P::G;  // bytes per k-step
 #pragma unroll
     for (int i = 0; i < P::G; ++i) {
         const int ks = g * P::G + i;
-        const int64_t el = ((int64_t)co * ntaps + o) * cin + (int64_t)kc * P::KC +
-                           ks * P::KSUB + (lane >> 5) * P::EPL;
+        const int64_t ci0 = (int64_t)kc * P::KC + ks * P::KSUB + (lane >> 5) * P::EPL;
 #pragma unroll
-        for (int b = 0; b < BPK; ++b) bytes[i * BPK + b] = w[el * P::WB + b];
+        for (int e = 0; e < P::EPL; ++e) {
+            const int64_t el = co * st.co + o * st.o + (ci0 + e) * st.ci;
+#pragma unroll
+            for (int b = 0; b < P::WB; ++b)
+                bytes[(i * P::EPL + e) * P::WB + b] = w[el * P::WB + b];
+        }
     }
     uint32_t v[4];
 #pragma unroll
@@ -51,9 +64,11 @@ __global__ void pack_weights_kernel(const uint8_t* __restrict__ w, u32x4* __rest
     out[id] = u32x4{v[0], v[1], v[2], v[3]};
 }
 
-// Q8_0 scales as f32 per (tap, chunk, co): a 32-channel chunk is one block.
+// Q8_0 scales as f32 per (tap, chunk, co): a 32-channel chunk is one block
+// (block index = element index of its first channel / 32; channels run
+// contiguously, st.ci == 1).
 __global__ void pack_scales_kernel(const uint16_t* __restrict__ d, float* __restrict__ out,
-                                   int ntaps, int cin, int cout) {
+                                   int ntaps, int cin, int cout, WStride st) {
     const int kch = cin / 32;
     const int64_t n = (int64_t)ntaps * kch * cout;
     const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -62,7 +77,7 @@ __global__ void pack_scales_kernel(const uint16_t* __restrict__ d, float* __rest
     const int64_t tk = id / cout;
     const int kc = (int)(tk % kch);
     const int o = (int)(tk / kch);
-    out[id] = f16_bits_to_f32(d[(((int64_t)co * ntaps + o) * cin + (int64_t)kc * 32) >> 5]);
+    out[id] = f16_bits_to_f32(d[(co * st.co + o * st.o + (int64_t)kc * 32) >> 5]);
 }
 
 __global__ void q8_0_repack_kernel(const uint8_t* __restrict__ blocks, int64_t nblocks,
@@ -81,10 +96,65 @@ __global__ void q8_0_repack_kernel(const uint8_t* __restrict__ blocks, int64_t n
     dst[1] = u32x4{words[4], words[5], words[6], words[7]};
 }
 
+// quantize_q8_0 (cpp_ggml/scripts/gguf_schema.py:14-24): one thread per
+// 32-float block.  amax / 127 is an F32 division rounded to fp16; the quants
+// are rint (half to even) of the F32 quotient w / f32(d), clipped to +-127.
+__global__ void q8_0_quantize_kernel(const float* __restrict__ w, int64_t nblocks,
+                                     uint8_t* __restrict__ blocks) {
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nblocks) return;
+    const floatx4* src = reinterpret_cast<const floatx4*>(w + b * 32);
+    float v[32];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const floatx4 q = src[j];
+        v[4 * j] = q.x;
+        v[4 * j + 1] = q.y;
+        v[4 * j + 2] = q.z;
+        v[4 * j + 3] = q.w;
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j]));
+    if (amax == 0.0f) amax = 1e-12f;
+    const uint16_t dh = f32_to_f16_bits(amax / 127.0f);
+    const float d = f16_bits_to_f32(dh);
+    uint8_t* dst = blocks + b * 34;
+    dst[0] = (uint8_t)(dh & 0xff);
+    dst[1] = (uint8_t)(dh >> 8);
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+        float q;
+        if (d == 0.0f) {
+            // amax / 127 below half the smallest fp16 subnormal rounds d to
+            // 0 (always for an all-zero block): the converter's quotient is
+            // +-inf, clipped to +-127, or 0/0, which its int8 cast makes 0
+            q = v[j] > 0.0f ? 127.0f : (v[j] < 0.0f ? -127.0f : 0.0f);
+        } else {
+            q = __builtin_rintf(v[j] / d);
+            q = fminf(fmaxf(q, -127.0f), 127.0f);
+        }
+        dst[2 + j] = (uint8_t)(int8_t)q;
+    }
+}
+
+// ggml Q8_0 blocks -> f32(d) * q (exact in F32), stored as out_dtype.
+__global__ void q8_0_dequant_kernel(const uint8_t* __restrict__ blocks, int64_t n,
+                                    int out_dtype, void* __restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const uint8_t* blk = blocks + (i >> 5) * 34;
+    const float d = f16_bits_to_f32((uint16_t)blk[0] | ((uint16_t)blk[1] << 8));
+    const float v = d * (float)(int8_t)blk[2 + (i & 31)];
+    if (out_dtype == SPC_F32) static_cast<float*>(out)[i] = v;
+    else if (out_dtype == SPC_F16) static_cast<uint16_t*>(out)[i] = f32_to_f16_bits(v);
+    else static_cast<uint16_t*>(out)[i] = f32_to_bf16_bits(v);
+}
+
 int check_shape(const char* fn, int64_t ntaps, int64_t cin, int64_t cout) {
-    if ((ntaps != 27 && ntaps != 8) || cin <= 0 || cout <= 0 || cin % 32 != 0 ||
+    if ((ntaps != 27 && ntaps != 8 && ntaps != 1) || cin <= 0 || cout <= 0 || cin % 32 != 0 ||
         cout % 32 != 0 || cin > (1 << 16) || cout > (1 << 16)) {
-        set_last_error("%s: unsupported shape ntaps=%lld cin=%lld cout=%lld (ntaps 27 or 8, "
+        set_last_error("%s: unsupported shape ntaps=%lld cin=%lld cout=%lld (ntaps 27, 8 or 1, "
                        "cin and cout multiples of 32)",
                        fn, (long long)ntaps, (long long)cin, (long long)cout);
         return SPC_BAD_SHAPE;
@@ -112,8 +182,9 @@ size_t spc_conv_packed_bytes(int w_dtype, int64_t ntaps, int64_t cin, int64_t co
     }
 }
 
-int spc_conv_pack_weights(spc_stream_t stream, int w_dtype, const void* w, const void* w_scale,
-                          int64_t ntaps, int64_t cin, int64_t cout, void* packed) {
+int spc_conv_pack_weights(spc_stream_t stream, int w_dtype, int w_layout, const void* w,
+                          const void* w_scale, int64_t ntaps, int64_t cin, int64_t cout,
+                          void* packed) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int st = check_shape("spc_conv_pack_weights", ntaps, cin, cout);
     if (st != SPC_OK) return st;
@@ -121,31 +192,41 @@ int spc_conv_pack_weights(spc_stream_t stream, int w_dtype, const void* w, const
         set_last_error("spc_conv_pack_weights: null / misaligned pointer");
         return SPC_BAD_ARG;
     }
+    if (w_layout != SPC_W_KRSC && w_layout != SPC_W_TCK && w_layout != SPC_W_TKC) {
+        set_last_error("spc_conv_pack_weights: unknown weight layout %d", w_layout);
+        return SPC_BAD_ARG;
+    }
+    if (w_dtype == SPC_Q8_0 && w_layout == SPC_W_TKC) {
+        set_last_error("spc_conv_pack_weights: Q8_0 blocks must run along cin (SPC_W_KRSC or "
+                       "SPC_W_TCK); dequantise SPC_W_TKC weights first");
+        return SPC_BAD_ARG;
+    }
+    const WStride ws = weight_strides(w_layout, ntaps, cin, cout);
     const uint8_t* wb = static_cast<const uint8_t*>(w);
     u32x4* out = static_cast<u32x4*>(packed);
     switch (w_dtype) {
         case SPC_F32: {
             const int64_t words = (int64_t)packed_quant_bytes<float, false>(ntaps, cin, cout) / 16;
             pack_weights_kernel<float, false><<<(unsigned)ceil_div(words, 256), 256, 0, s>>>(
-                wb, out, (int)ntaps, (int)cin, (int)cout);
+                wb, out, (int)ntaps, (int)cin, (int)cout, ws);
             break;
         }
         case SPC_F16:
         case SPC_BF16: {
             const int64_t words = (int64_t)packed_quant_bytes<__bf16, false>(ntaps, cin, cout) / 16;
             pack_weights_kernel<__bf16, false><<<(unsigned)ceil_div(words, 256), 256, 0, s>>>(
-                wb, out, (int)ntaps, (int)cin, (int)cout);
+                wb, out, (int)ntaps, (int)cin, (int)cout, ws);
             break;
         }
         case SPC_Q8_0: {
             const size_t qbytes = packed_quant_bytes<__bf16, true>(ntaps, cin, cout);
             const int64_t words = (int64_t)qbytes / 16;
             pack_weights_kernel<__bf16, true><<<(unsigned)ceil_div(words, 256), 256, 0, s>>>(
-                wb, out, (int)ntaps, (int)cin, (int)cout);
+                wb, out, (int)ntaps, (int)cin, (int)cout, ws);
             float* sc = reinterpret_cast<float*>(static_cast<char*>(packed) + align_up(qbytes, 256));
             const int64_t ns = ntaps * (cin / 32) * cout;
             pack_scales_kernel<<<(unsigned)ceil_div(ns, 256), 256, 0, s>>>(
-                static_cast<const uint16_t*>(w_scale), sc, (int)ntaps, (int)cin, (int)cout);
+                static_cast<const uint16_t*>(w_scale), sc, (int)ntaps, (int)cin, (int)cout, ws);
             break;
         }
         default:
@@ -169,7 +250,11 @@ int spc_sparse_conv(spc_stream_t stream, int dtype, const void* x, int w_dtype, 
         return SPC_BAD_SHAPE;
     }
     if (n_out == 0) return SPC_OK;
-    if (!x || !w || !y || !idx || !aligned16(x) || !aligned16(w) ||
+    if (!idx && (ntaps != 1 || n_in != n_out)) {
+        set_last_error("spc_sparse_conv: idx may be NULL only for ntaps 1 with n_in == n_out");
+        return SPC_BAD_ARG;
+    }
+    if (!x || !w || !y || !aligned16(x) || !aligned16(w) ||
         (idx_layout != SPC_IDX_TOKEN_MAJOR && idx_layout != SPC_IDX_OFFSET_MAJOR) ||
         (w_layout != SPC_W_KRSC && w_layout != SPC_W_PACKED)) {
         set_last_error("spc_sparse_conv: null / misaligned pointer or bad layout enum");
@@ -242,6 +327,36 @@ int spc_q8_0_repack(spc_stream_t stream, const uint8_t* blocks, int64_t nblocks,
     q8_0_repack_kernel<<<(unsigned)ceil_div(nblocks, 256), 256, 0, s>>>(blocks, nblocks, qs, d);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_status(e, "q8_0_repack launch");
+    return SPC_OK;
+}
+
+int spc_q8_0_quantize(spc_stream_t stream, const float* w, int64_t n, uint8_t* blocks) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (n < 0 || n % 32 != 0 || (n > 0 && (!w || !blocks || !aligned16(w)))) {
+        set_last_error("spc_q8_0_quantize: n must be a multiple of 32, w 16-byte aligned");
+        return SPC_BAD_ARG;
+    }
+    if (n == 0) return SPC_OK;
+    const int64_t nb = n / 32;
+    q8_0_quantize_kernel<<<(unsigned)ceil_div(nb, 256), 256, 0, s>>>(w, nb, blocks);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_status(e, "q8_0_quantize launch");
+    return SPC_OK;
+}
+
+int spc_q8_0_dequant(spc_stream_t stream, const uint8_t* blocks, int64_t nblocks, int out_dtype,
+                     void* out) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (nblocks < 0 || (nblocks > 0 && (!blocks || !out)) ||
+        (out_dtype != SPC_F32 && out_dtype != SPC_F16 && out_dtype != SPC_BF16)) {
+        set_last_error("spc_q8_0_dequant: bad arguments");
+        return SPC_BAD_ARG;
+    }
+    if (nblocks == 0) return SPC_OK;
+    const int64_t n = nblocks * 32;
+    q8_0_dequant_kernel<<<(unsigned)ceil_div(n, 256), 256, 0, s>>>(blocks, n, out_dtype, out);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_status(e, "q8_0_dequant launch");
     return SPC_OK;
 }
 

@@ -34,6 +34,7 @@
 //           stay in that XCD's L2.
 // Tiles whose union exceeds the stage (rows not spatially ordered) fall
 // back to staging each tap's 256 source rows separately.
+// NTAPS = 1 with a null map is the dense 1x1x1 conv: row t reads row t.
 #pragma once
 
 #include <climits>
@@ -206,7 +207,9 @@ __global__ __launch_bounds__(kThreads, 1) void conv_kernel(ConvArgs a) {
         if (e < NQ) {
             const int r = e / NTAPS;
             const int o = e - r * NTAPS;
-            if (contiguous) {
+            if (NTAPS == 1 && a.idx == nullptr) {  // identity map (dense 1x1x1 conv)
+                src = srow[r];
+            } else if (contiguous) {
                 if (r0 + r < a.n_out) src = a.idx[r0 * NTAPS + e];
             } else {
                 const int32_t t = srow[r];
@@ -610,6 +613,8 @@ hipError_t dispatch_conv(hipStream_t s, const ConvArgs& a) {
         return a.packed ? dispatch_tn<T, Q8, true, 27>(s, a) : dispatch_tn<T, Q8, false, 27>(s, a);
     if (a.ntaps == 8)
         return a.packed ? dispatch_tn<T, Q8, true, 8>(s, a) : dispatch_tn<T, Q8, false, 8>(s, a);
+    if (a.ntaps == 1)
+        return a.packed ? dispatch_tn<T, Q8, true, 1>(s, a) : dispatch_tn<T, Q8, false, 1>(s, a);
     return hipErrorInvalidValue;
 }
 

@@ -277,6 +277,24 @@ int bits_for(int64_t v) {  // bits needed to hold values in [0, v)
 
 // ---- subdivide ------------------------------------------------------------
 
+// Transposed stride-2 map: fine row f reads coarse row fine_to_coarse[f] at
+// its own tap k(f) = (x&1)*4 + (y&1)*2 + (z&1); every other tap is nc.
+__global__ void stride2_inverse_kernel(const int4* __restrict__ coords,
+                                       const int32_t* __restrict__ f2c, int64_t nf, int32_t nc,
+                                       int32_t* __restrict__ taps) {
+    const int64_t f = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (f >= nf) return;
+    const int4 c = coords[f];
+    const int k = (c.y & 1) * 4 + (c.z & 1) * 2 + (c.w & 1);
+    const int32_t p = f2c[f];
+    int32_t t[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) t[j] = j == k ? p : nc;
+    int4* dst = reinterpret_cast<int4*>(taps + f * 8);
+    dst[0] = int4{t[0], t[1], t[2], t[3]};
+    dst[1] = int4{t[4], t[5], t[6], t[7]};
+}
+
 __global__ void subdivide_flag_kernel(const uint8_t* __restrict__ keep, int64_t m8,
                                       int32_t* __restrict__ flag) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -502,6 +520,26 @@ int spc_subdivide_map(spc_stream_t stream, const int32_t* coords, int64_t n, con
     const int code = read_status_word(s, status);
     *m_out = m;
     return code;
+}
+
+int spc_stride2_inverse_taps(spc_stream_t stream, const int32_t* coords,
+                             const int32_t* fine_to_coarse, int64_t nf, int64_t nc,
+                             int32_t* taps) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (nf < 0 || nc < 0 || nf > INT32_MAX / 8 || nc > INT32_MAX) {
+        set_last_error("spc_stride2_inverse_taps: nf=%lld nc=%lld out of range", (long long)nf,
+                       (long long)nc);
+        return SPC_BAD_SHAPE;
+    }
+    if (nf == 0) return SPC_OK;
+    if (!coords || !fine_to_coarse || !taps || !aligned16(coords) || !aligned16(taps)) {
+        set_last_error("spc_stride2_inverse_taps: null or misaligned argument");
+        return SPC_BAD_ARG;
+    }
+    stride2_inverse_kernel<<<grid_for(nf, 256), 256, 0, s>>>(
+        reinterpret_cast<const int4*>(coords), fine_to_coarse, nf, (int32_t)nc, taps);
+    SPC_HIP(hipGetLastError());
+    return SPC_OK;
 }
 
 }  // extern "C"

@@ -105,3 +105,15 @@ def test_q8_0_dequant_f16_rounding(orc):
     f32 = orc.q8_0_dequant(blocks, oracle.F32)
     f16 = orc.q8_0_dequant(blocks, oracle.F16)
     assert np.array_equal(f16, f32.astype(H))
+
+
+def test_scatter_case_inputs_follow_recipe(orc):
+    """The regenerated inputs have the recipe's structure: pinned rows,
+    skipped rows -1 / nc, counts = hits, features are f16 in [-4, 4)."""
+    f, rows, counts = orc.scatter_case(128, 26281, 5239, 5)
+    assert np.array_equal(rows[:5239], np.arange(5239))
+    valid = (rows >= 0) & (rows < 5239)
+    assert set(np.unique(rows[~valid])) <= {-1, 5239} and (~valid).sum() > 0
+    assert np.array_equal(np.bincount(rows[valid], minlength=5239).astype(np.float32), counts)
+    v = f.view(np.float16).astype(np.float32)
+    assert v.min() >= -4.0 and v.max() <= 4.0 and abs(float(v.mean())) < 0.05
