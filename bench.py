@@ -69,10 +69,10 @@ class ConvCall:
     overhead per step at a single ctypes call)."""
 
     def __init__(self, nat, x, w, bias, y, idx, *, ntaps, n_out, layout, perm=None,
-                 w_scale=None, wdt=None):
+                 w_scale=None, wdt=None, plan=None):
         import torch
 
-        self.fn = nat.lib().spc_sparse_conv
+        self.fn = nat.lib().spc_sparse_conv_plan
         self.stream = torch.cuda.current_stream().cuda_stream
         dt = nat.dtype_code(x.dtype)
         if isinstance(w, nat.PackedWeights):
@@ -83,7 +83,8 @@ class ConvCall:
             sptr = None if w_scale is None else w_scale.data_ptr()
         self.args = (self.stream, dt, x.data_ptr(), wd, layout_w, wptr, sptr,
                      None if bias is None else bias.data_ptr(), y.data_ptr(), idx.data_ptr(),
-                     layout, None if perm is None else perm.data_ptr(), ntaps, n_out,
+                     layout, None if perm is None else perm.data_ptr(),
+                     None if plan is None else plan.data_ptr(), ntaps, n_out,
                      x.shape[0], x.shape[1], y.shape[1])
         self.nat = nat
 
@@ -281,12 +282,15 @@ def main():
         perm = m.argsort if args.order == "mask" else None
         idx = m.offset_major if args.order == "mask" else m.token_major
         layout = nat.IDX_OFFSET_MAJOR if args.order == "mask" else nat.IDX_TOKEN_MAJOR
+        plan = nat.conv_plan(idx, ntaps=27, n_out=n, idx_layout=layout, row_perm=perm)
+        plan_ms, _ = time_gpu(lambda: nat.conv_plan(idx, ntaps=27, n_out=n, idx_layout=layout,
+                                                    row_perm=perm), 50, 5)
         if cfg == 1:
             x = torch.from_numpy(xf).to(dev)
             w = torch.from_numpy(wf).to(dev)
             b = torch.from_numpy(bf).to(dev)
             call = ConvCall(nat, x, nat.pack_weights(w), b, y, idx, ntaps=27, n_out=n,
-                            layout=layout, perm=perm)
+                            layout=layout, perm=perm, plan=plan)
             dtype = "f32"
             peak = PEAK_F32_TFLOPS
             xb, wb, bb = xf, wf, bf
@@ -298,7 +302,7 @@ def main():
             w, wb = bf16_dev(orc, wf, dev)
             b, bb = bf16_dev(orc, bf, dev)
             call = ConvCall(nat, x, nat.pack_weights(w), b, y, idx, ntaps=27, n_out=n,
-                            layout=layout, perm=perm)
+                            layout=layout, perm=perm, plan=plan)
             dtype = "bf16"
             peak = PEAK_BF16_TFLOPS
             cpu_dt = (oracle.BF16, oracle.BF16)
@@ -310,7 +314,7 @@ def main():
             blocks = orc.q8_0_quantize(wf)
             qs, dsc = nat.q8_0_repack(torch.from_numpy(blocks).to(dev))
             call = ConvCall(nat, x, nat.pack_weights(qs, dsc, cin=cin, cout=cout), b, y, idx,
-                            ntaps=27, n_out=n, layout=layout, perm=perm)
+                            ntaps=27, n_out=n, layout=layout, perm=perm, plan=plan)
             dtype = "bf16 x Q8_0"
             peak = PEAK_BF16_TFLOPS
             wb = orc.q8_0_dequant(blocks, oracle.F16)
@@ -336,6 +340,7 @@ def main():
             "dense_equiv_tflops": 2.0 * 27 * n * cin * cout / t / 1e12,
             "wall_s": wall, "map_build_ms": map_ms,
             "map_build_gbs": map_bytes / (map_ms / 1e3) / 1e9,
+            "conv_plan_ms": plan_ms,
             "compulsory_gbs": comp_bytes / t / 1e9,
             "roofline": {"bound": "mfma", "achieved": tflops, "peak": peak, "unit": "TFLOP/s",
                          "frac": tflops / peak, "traffic": traffic,
@@ -356,10 +361,11 @@ def main():
         w2, _ = bf16_dev(orc, wl.normal((cout, 27, 128), 0.02, seed=303), dev)
         h = torch.empty((nc, 128), dtype=torch.bfloat16, device=dev)
         y = torch.empty((nc, cout), dtype=torch.bfloat16, device=dev)
+        p1 = nat.conv_plan(d.stride2_taps, ntaps=8, n_out=nc, n_in=n)
         c1 = ConvCall(nat, x, nat.pack_weights(w1), None, h, d.stride2_taps, ntaps=8, n_out=nc,
-                      layout=nat.IDX_TOKEN_MAJOR)
+                      layout=nat.IDX_TOKEN_MAJOR, plan=p1)
         c2 = ConvCall(nat, h, nat.pack_weights(w2), None, y, mc.token_major, ntaps=27, n_out=nc,
-                      layout=nat.IDX_TOKEN_MAJOR)
+                      layout=nat.IDX_TOKEN_MAJOR, plan=mc.plan())
         ms1, _ = time_gpu(c1, args.steps, args.warmup)
         ms2, _ = time_gpu(c2, args.steps, args.warmup)
         f1 = 2.0 * n * cin * 128
@@ -385,7 +391,7 @@ def main():
             w, _ = bf16_dev(orc, wl.normal((ch, 27, ch), 0.02, seed=401 + ch), dev)
             y = torch.empty((nl, ch), dtype=torch.bfloat16, device=dev)
             call = ConvCall(nat, x, nat.pack_weights(w), None, y, ml.token_major, ntaps=27,
-                            n_out=nl, layout=nat.IDX_TOKEN_MAJOR)
+                            n_out=nl, layout=nat.IDX_TOKEN_MAJOR, plan=ml.plan())
             msl, _ = time_gpu(call, args.steps, args.warmup)
             tl = msl / 1e3
             byt = nl * ch * 2 * 2 + w.numel() * 2 + 108 * nl

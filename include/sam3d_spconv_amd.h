@@ -177,6 +177,25 @@ int spc_sparse_conv(spc_stream_t stream, int dtype, const void* x, int w_dtype, 
                     const int32_t* idx, int idx_layout, const int32_t* row_perm, int64_t ntaps,
                     int64_t n_out, int64_t n_in, int64_t cin, int64_t cout);
 
+/* Tile plan: the per-256-row-tile setup of the conv kernel (active tap
+ * set, deduplicated source rows, slot table), built once per index table
+ * and reused by every conv over it -- like the map, it depends only on
+ * (idx, idx_layout, row_perm, ntaps, n_out, n_in), not on channels or
+ * weights.  spc_sparse_conv_plan takes the same arguments as
+ * spc_sparse_conv plus a plan built from those same arguments (256-byte
+ * aligned); a plan from other arguments gives wrong results.  No
+ * reference counterpart: a cache of this library's kernel setup, in the
+ * role of spconv's indice_key pair cache (SP/conv/conv_spconv.py:30-50). */
+size_t spc_conv_plan_bytes(int64_t n_out, int64_t ntaps);
+int spc_conv_plan(spc_stream_t stream, const int32_t* idx, int idx_layout,
+                  const int32_t* row_perm, int64_t ntaps, int64_t n_out, int64_t n_in, void* plan,
+                  size_t plan_bytes);
+int spc_sparse_conv_plan(spc_stream_t stream, int dtype, const void* x, int w_dtype,
+                         int w_layout, const void* w, const void* w_scale, const void* bias,
+                         void* y, const int32_t* idx, int idx_layout, const int32_t* row_perm,
+                         const void* plan, int64_t ntaps, int64_t n_out, int64_t n_in,
+                         int64_t cin, int64_t cout);
+
 /* Bytes of the SPC_W_PACKED form of ntaps x cout x cin weights of w_dtype
  * (Q8_0: quants then f32 scales), and the packer.  w_layout (SPC_W_KRSC,
  * SPC_W_TCK or SPC_W_TKC) says how w is stored.  Q8_0 quants (int8) come

@@ -68,6 +68,11 @@ def lib() -> ctypes.CDLL:
     L.spc_subdivide_map.argtypes = [_P, _P, _I64, _P, _P, _P, _P, _P, _SZ]
     L.spc_sparse_conv.argtypes = [_P, _INT, _P, _INT, _INT, _P, _P, _P, _P, _P, _INT, _P, _I64,
                                   _I64, _I64, _I64, _I64]
+    L.spc_sparse_conv_plan.argtypes = [_P, _INT, _P, _INT, _INT, _P, _P, _P, _P, _P, _INT, _P,
+                                       _P, _I64, _I64, _I64, _I64, _I64]
+    L.spc_conv_plan_bytes.restype = _SZ
+    L.spc_conv_plan_bytes.argtypes = [_I64, _I64]
+    L.spc_conv_plan.argtypes = [_P, _P, _INT, _P, _I64, _I64, _I64, _P, _SZ]
     L.spc_conv_packed_bytes.restype = _SZ
     L.spc_conv_packed_bytes.argtypes = [_INT, _I64, _I64, _I64]
     L.spc_conv_pack_weights.argtypes = [_P, _INT, _INT, _P, _P, _I64, _I64, _I64, _P]
@@ -130,10 +135,17 @@ class SubmMap:
     mask_sorted: torch.Tensor   # [n] int32
     argsort: torch.Tensor       # [n] int32
     mask_natural: torch.Tensor  # [n] int32
+    _plan: torch.Tensor | None = None
 
     @property
     def pairs(self) -> int:
         return int((self.token_major < self.n).sum().item())
+
+    def plan(self) -> torch.Tensor:
+        """The conv kernel's tile plan for the token-major table (built once)."""
+        if self._plan is None:
+            self._plan = conv_plan(self.token_major, ntaps=27, n_out=self.n)
+        return self._plan
 
 
 def map_build(coords: torch.Tensor, *, mesh_resolution: int | None = None,
@@ -289,11 +301,30 @@ def pack_weights(weight: torch.Tensor, w_scale: torch.Tensor | None = None, *,
     return PackedWeights(out, wdt, ntaps, cin, cout)
 
 
+def conv_plan(idx: torch.Tensor | None, *, ntaps: int, n_out: int, n_in: int | None = None,
+              idx_layout: int = IDX_TOKEN_MAJOR,
+              row_perm: torch.Tensor | None = None, device=None) -> torch.Tensor:
+    """spc_conv_plan: the conv kernel's per-tile setup for this index table
+    (reusable by every conv over it)."""
+    _need_gpu(idx, row_perm)
+    dev = idx.device if idx is not None else device
+    if dev is None or torch.device(dev).type != "cuda":
+        raise RuntimeError("sparse-conv kernels run on the GPU only; got a CPU tensor")
+    n_in = n_out if n_in is None else n_in
+    L = lib()
+    nbytes = L.spc_conv_plan_bytes(n_out, ntaps)
+    plan = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    st = L.spc_conv_plan(_stream(dev), _ptr(idx), idx_layout, _ptr(row_perm), ntaps, n_out, n_in,
+                         _ptr(plan), nbytes)
+    _check("spc_conv_plan", st)
+    return plan
+
+
 def sparse_conv(x: torch.Tensor, weight, bias: torch.Tensor | None,
                 idx: torch.Tensor | None, *, ntaps: int, n_out: int,
                 idx_layout: int = IDX_TOKEN_MAJOR, row_perm: torch.Tensor | None = None,
                 w_scale: torch.Tensor | None = None, out: torch.Tensor | None = None,
-                cout: int | None = None) -> torch.Tensor:
+                cout: int | None = None, plan: torch.Tensor | None = None) -> torch.Tensor:
     """y = conv(x) through spc_sparse_conv.  `weight` is a PackedWeights, a
     [Cout, ntaps, Cin] tensor in the feature dtype, or int8 Q8_0 quants with
     w_scale (fp16 block scales).  idx None with ntaps 1 is the identity map
@@ -326,9 +357,9 @@ def sparse_conv(x: torch.Tensor, weight, bias: torch.Tensor | None,
         bias = bias.contiguous()
     if out is None:
         out = torch.empty((n_out, cout), dtype=x.dtype, device=x.device)
-    st = lib().spc_sparse_conv(_stream(x.device), dt, _ptr(x), wdt, layout, wptr, sptr,
-                               _ptr(bias), _ptr(out), _ptr(idx), idx_layout, _ptr(row_perm),
-                               ntaps, n_out, x.shape[0], cin, cout)
+    st = lib().spc_sparse_conv_plan(_stream(x.device), dt, _ptr(x), wdt, layout, wptr, sptr,
+                                    _ptr(bias), _ptr(out), _ptr(idx), idx_layout, _ptr(row_perm),
+                                    _ptr(plan), ntaps, n_out, x.shape[0], cin, cout)
     _check("spc_sparse_conv", st)
     return out
 

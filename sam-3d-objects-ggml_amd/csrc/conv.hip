@@ -237,10 +237,60 @@ int spc_conv_pack_weights(spc_stream_t stream, int w_dtype, int w_layout, const 
     return SPC_OK;
 }
 
+size_t spc_conv_plan_bytes(int64_t n_out, int64_t ntaps) {
+    if (n_out <= 0 || (ntaps != 27 && ntaps != 8 && ntaps != 1)) return 0;
+    return (size_t)(ceil_div(n_out, kTM) * plan_tile_bytes((int)ntaps));
+}
+
+int spc_conv_plan(spc_stream_t stream, const int32_t* idx, int idx_layout,
+                  const int32_t* row_perm, int64_t ntaps, int64_t n_out, int64_t n_in, void* plan,
+                  size_t plan_bytes) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if ((ntaps != 27 && ntaps != 8 && ntaps != 1) || n_out < 0 || n_in < 0 ||
+        n_out > INT32_MAX || n_in > INT32_MAX) {
+        set_last_error("spc_conv_plan: unsupported ntaps=%lld / n_out=%lld / n_in=%lld",
+                       (long long)ntaps, (long long)n_out, (long long)n_in);
+        return SPC_BAD_SHAPE;
+    }
+    if (n_out == 0) return SPC_OK;
+    if ((!idx && (ntaps != 1 || n_in != n_out)) || !plan || ((uintptr_t)plan & 255u) != 0 ||
+        (idx_layout != SPC_IDX_TOKEN_MAJOR && idx_layout != SPC_IDX_OFFSET_MAJOR)) {
+        set_last_error("spc_conv_plan: null / misaligned (256 bytes) pointer or bad layout");
+        return SPC_BAD_ARG;
+    }
+    if (plan_bytes < spc_conv_plan_bytes(n_out, ntaps)) {
+        set_last_error("spc_conv_plan: plan buffer too small");
+        return SPC_OOM;
+    }
+    ConvArgs a{};
+    a.idx = idx;
+    a.row_perm = row_perm;
+    a.n_out = n_out;
+    a.n_in = n_in;
+    a.idx_layout = idx_layout;
+    a.ntaps = (int32_t)ntaps;
+    const unsigned grid = (unsigned)ceil_div(n_out, kTM);
+    char* pl = static_cast<char*>(plan);
+    if (ntaps == 27) conv_plan_kernel<27><<<grid, 512, 0, s>>>(a, pl);
+    else if (ntaps == 8) conv_plan_kernel<8><<<grid, 512, 0, s>>>(a, pl);
+    else conv_plan_kernel<1><<<grid, 512, 0, s>>>(a, pl);
+    SPC_HIP(hipGetLastError());
+    return SPC_OK;
+}
+
 int spc_sparse_conv(spc_stream_t stream, int dtype, const void* x, int w_dtype, int w_layout,
                     const void* w, const void* w_scale, const void* bias, void* y,
                     const int32_t* idx, int idx_layout, const int32_t* row_perm, int64_t ntaps,
                     int64_t n_out, int64_t n_in, int64_t cin, int64_t cout) {
+    return spc_sparse_conv_plan(stream, dtype, x, w_dtype, w_layout, w, w_scale, bias, y, idx,
+                                idx_layout, row_perm, nullptr, ntaps, n_out, n_in, cin, cout);
+}
+
+int spc_sparse_conv_plan(spc_stream_t stream, int dtype, const void* x, int w_dtype,
+                         int w_layout, const void* w, const void* w_scale, const void* bias,
+                         void* y, const int32_t* idx, int idx_layout, const int32_t* row_perm,
+                         const void* plan, int64_t ntaps, int64_t n_out, int64_t n_in,
+                         int64_t cin, int64_t cout) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int st = check_shape("spc_sparse_conv", ntaps, cin, cout);
     if (st != SPC_OK) return st;
@@ -275,6 +325,11 @@ int spc_sparse_conv(spc_stream_t stream, int dtype, const void* x, int w_dtype, 
     a.cin = (int32_t)cin;
     a.cout = (int32_t)cout;
     a.packed = w_layout == SPC_W_PACKED;
+    if (plan && ((uintptr_t)plan & 255u) != 0) {
+        set_last_error("spc_sparse_conv_plan: plan must be 256-byte aligned");
+        return SPC_BAD_ARG;
+    }
+    a.plan = plan;
     hipError_t e = hipSuccess;
     if (w_dtype == SPC_Q8_0) {
         if (dtype != SPC_BF16) {

@@ -7,7 +7,9 @@
 // once to the output dtype.  Taps whose source is outside [0, n_in) add
 // nothing (PATCH:255).
 //
-// Structure (one 8-wave workgroup per 256-row x TN output tile):
+// Structure (one 8-wave workgroup -- two waves per SIMD -- per 256-row x TN
+// output tile; with TN = 128 each wave owns a 64 x 64 block of F32
+// accumulators):
 //   setup   the tile's NTAPS x 256 neighbour indices are loaded (contiguous,
 //           coalesced for the token-major table) into registers; the OR of
 //           the valid taps is formed (taps no row uses are skipped -- the
@@ -18,17 +20,23 @@
 //           spatially coherent tile references ~3.2 x 256 distinct rows
 //           instead of ~21 x 256, and ranks by popcount number them in
 //           ascending row order, so the rows one wave reads for one tap sit
-//           in consecutive LDS slots.
-//   K loop  for each 64-byte channel chunk the union rows are staged once in
-//           LDS (slot U = zeros for missing taps); then every wave walks
-//           the active taps with no further barrier: its B fragments come
-//           straight from global memory (weights prepacked in MFMA fragment
-//           order -- one contiguous 1 KB load per fragment, L2-resident),
-//           prefetched kPD steps ahead in registers; its A fragments are
-//           read from the union slots.
+//           in nearly consecutive LDS slots.
+//   K loop  channels are consumed in 64-byte chunks.  A chunk's union rows
+//           live in one of two LDS buffers (slot U = zeros for missing
+//           taps); while the waves run the MFMAs of chunk kc over all active
+//           taps, the next chunk is fetched in two halves into registers
+//           and written to the other buffer, so one barrier per chunk is
+//           the only synchronisation.  B fragments come straight from
+//           global memory (weights prepacked in MFMA fragment order -- one
+//           contiguous 1 KB load per fragment, L2-resident) through a
+//           register ring PD steps deep; A fragments and their slots are
+//           read from LDS one and two steps ahead.
 //   Q8_0    int8 quants + per-block scales are dequantised in registers to
 //           bf16 operands: w = bf16(f32(d) * q).
-//   store   + bias in F32, one rounding, each output row written once.
+//   store   + bias in F32, one rounding; the MFMAs produce the transposed
+//           tile, so each lane holds runs of consecutive output channels of
+//           one row and stores them directly; every output element is
+//           written once.
 //   tiles   XCD-major: workgroup b runs on XCD b % 8 and each XCD gets a
 //           contiguous range of row tiles, so a neighbourhood's feature rows
 //           stay in that XCD's L2.
@@ -62,6 +70,7 @@ struct ConvArgs {
     int32_t tiles_n;
     int64_t total_tiles;
     int64_t tiles_per_xcd;
+    const void* plan;         // per-row-tile setup from conv_plan_kernel, or null
 };
 
 // MFMA operand traits per activation type.
@@ -128,76 +137,80 @@ struct Panel {
 };
 
 constexpr int kTM = 256;        // output rows per tile
-constexpr int kThreads = 512;   // 8 waves
 constexpr int kUMax = 1024;     // capacity of the deduplicated source-row stage
 constexpr int kWinWords = 1024; // dedupe bitmap: 32768 source rows
-constexpr int kPD = 3;          // weight prefetch distance (steps)
+constexpr int kSegs = 4;        // 16-byte segments per staged 64-byte row chunk
 
-template <typename T, bool Q8, bool PACKED, int NTAPS, int TN, int WM, int WN>
-__global__ __launch_bounds__(kThreads, 1) void conv_kernel(ConvArgs a) {
-    using M = Mfma<T>;
-    using P = Panel<T, Q8>;
+// LDS position (in 16-byte units) of segment s of staged row r.  The XOR
+// swizzle puts one segment of 8 (and of 16) consecutive rows on distinct
+// banks, so a wave reading one k-slice of 32 nearly consecutive slots, and
+// the stage writes, run without bank conflicts.  slot_key(r) ^ s is the
+// same position, the form the slot table stores.
+__device__ __forceinline__ int slot_key(int r) { return r * kSegs + (((r >> 1) ^ (r >> 3)) & 3); }
+__device__ __forceinline__ int seg_pos(int r, int s) { return slot_key(r) ^ s; }
+
+constexpr int kTapWords = 8;  // step taps, four per word: up to 28 steps per chunk
+
+// Bytes of one row tile's plan: header (U, tap mask, fast flag, tap words),
+// output rows, union rows, slot keys.  The plan depends only on the index
+// table, its layout, the row order and NTAPS -- not on channels or weights.
+__host__ __device__ constexpr int64_t plan_tile_bytes(int ntaps) {
+    return (64 + 4 * kTM + 4 * kUMax + 2 * (int64_t)(ntaps + 1) * kTM + 255) / 256 * 256;
+}
+constexpr int kPlanSrow = 64;
+constexpr int kPlanUrow = kPlanSrow + 4 * kTM;
+constexpr int kPlanSidx = kPlanUrow + 4 * kUMax;
+
+// Shared-memory arrays of one tile's setup.
+struct TileLds {
+    uint32_t* scratch;  // 2 * kWinWords words: dedupe bitmap + word ranks
+    uint16_t* sidx;     // (NTAPS + 1) x kTM slot keys; row NTAPS = the zero slot
+    uint32_t* tlw;      // kTapWords
+    int32_t* urow;      // kUMax source rows of the union slots
+    int32_t* srow;      // kTM output rows of the tile rows
+    int32_t* wsum;      // one per wave
+    int32_t* misc;      // [0] tap mask [1] min source row [2] fail [3] U [4] fast
+};
+
+// Tile setup: the tile's NTAPS x 256 neighbour indices are loaded
+// (contiguous, coalesced for the token-major table) into registers; the OR
+// of the valid taps is formed (taps no row uses are skipped -- the per-tile
+// offset set of the reference's spconv kernel, cpp_ggml/third_party/
+// sam3d-spconv/src/.../ConvKernel_conv_kernel.cu:62-80); the referenced
+// source rows are deduplicated with a bitmap over a 32768-row window: a
+// spatially coherent tile references ~3.2 x 256 distinct rows instead of
+// ~21 x 256, and ranks by popcount number them in ascending row order.
+// Ends with a barrier; results in L (misc[0], misc[3], misc[4]).
+template <int NTAPS, int NT, int PD>
+__device__ __forceinline__ void tile_setup(const ConvArgs& a, int64_t r0, const TileLds& L) {
     constexpr int TM = kTM;
-    constexpr int NT = kThreads;
     constexpr int NW = NT / 64;
-    constexpr int ES = sizeof(T);
-    constexpr int KC = P::KC;
-    constexpr int CH = 16 / ES;     // elements per 16-byte chunk
-    constexpr int CPR = KC / CH;    // chunks per staged row
-    constexpr int PITCH = KC + CH;  // LDS row pitch (elements): +16 bytes against conflicts
-    constexpr int WTM = TM / WM;
-    constexpr int WTN = TN / WN;
-    constexpr int FM = WTM / 32;
-    constexpr int FN = WTN / 32;
     constexpr int NQ = NTAPS * TM;
-    constexpr int EPT = (NQ + NT - 1) / NT;  // index entries per thread
-    static_assert(WM * WN == NW && FM >= 1 && FN >= 1, "wave geometry");
-    static_assert(!Q8 || ES == 2, "Q8_0 weights feed 16-bit MFMA operands");
-    static_assert((kUMax + 1) * PITCH * ES >= 2 * kWinWords * 4, "bitmap aliases the A stage");
-    static_assert(NTAPS <= 32, "tap mask is 32-bit");
-
-    __shared__ __attribute__((aligned(16))) T Au[(kUMax + 1) * PITCH];
-    __shared__ int32_t sidx[NQ];      // [tap][row]: union slot, or source row (fallback)
-    __shared__ int32_t urow[kUMax];   // source row of each union slot
-    __shared__ int32_t srow[TM];      // output row of each tile row
-    __shared__ int32_t wsum[NW];
-    __shared__ uint32_t smask;
-    __shared__ int32_t smin;
-    __shared__ int32_t s_fail;
-
+    constexpr int EPT = (NQ + NT - 1) / NT;
+    constexpr int WPT = kWinWords / NT;
+    static_assert(kWinWords % NT == 0, "setup geometry");
+    static_assert((NTAPS + PD - 1) / PD < kTapWords, "tap words");
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
-
-    // XCD-major tile mapping
-    const int64_t xcd = blockIdx.x & 7;
-    const int64_t local = blockIdx.x >> 3;
-    const int64_t tile = xcd * a.tiles_per_xcd + local;
-    if (local >= a.tiles_per_xcd || tile >= a.total_tiles) return;
-    const int64_t tm = tile / a.tiles_n;
-    const int tn = (int)(tile % a.tiles_n);
-    const int64_t r0 = tm * TM;
-    const int co0 = tn * TN;
-
-    uint32_t* bm = reinterpret_cast<uint32_t*>(Au);      // setup-phase aliases
-    int32_t* wbase = reinterpret_cast<int32_t*>(Au) + kWinWords;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    uint32_t* bm = L.scratch;
+    int32_t* wbase = reinterpret_cast<int32_t*>(L.scratch) + kWinWords;
 
     if (tid == 0) {
-        smask = 0;
-        smin = INT_MAX;
-        s_fail = 0;
+        L.misc[0] = 0;
+        L.misc[1] = INT_MAX;
+        L.misc[2] = 0;
     }
     for (int r = tid; r < TM; r += NT) {
         const int64_t rr = r0 + r;
         int32_t t = -1;
         if (rr < a.n_out) t = a.row_perm ? a.row_perm[rr] : (int32_t)rr;
         if (t >= a.n_out) t = -1;  // a bad permutation entry writes nothing
-        srow[r] = t;
+        L.srow[r] = t;
     }
     for (int i = tid; i < kWinWords; i += NT) bm[i] = 0u;
     lds_barrier();
 
-    // ---- indices: entry e = r*NTAPS + o, held in registers ----
     const bool contiguous = a.idx_layout == SPC_IDX_TOKEN_MAJOR && a.row_perm == nullptr;
     int32_t ent[EPT];
 #pragma unroll
@@ -207,15 +220,15 @@ __global__ __launch_bounds__(kThreads, 1) void conv_kernel(ConvArgs a) {
         if (e < NQ) {
             const int r = e / NTAPS;
             const int o = e - r * NTAPS;
-            if (NTAPS == 1 && a.idx == nullptr) {  // identity map (dense 1x1x1 conv)
-                src = srow[r];
-            } else if (contiguous) {
+            if (contiguous && a.idx != nullptr) {
                 if (r0 + r < a.n_out) src = a.idx[r0 * NTAPS + e];
             } else {
-                const int32_t t = srow[r];
-                if (t >= 0)
-                    src = a.idx_layout == SPC_IDX_TOKEN_MAJOR ? a.idx[(int64_t)t * NTAPS + o]
-                                                              : a.idx[(int64_t)o * a.n_out + t];
+                const int32_t t = L.srow[r];
+                if (t >= 0) {
+                    if (NTAPS == 1 && a.idx == nullptr) src = t;  // identity map (dense 1x1x1)
+                    else if (a.idx_layout == SPC_IDX_TOKEN_MAJOR) src = a.idx[(int64_t)t * NTAPS + o];
+                    else src = a.idx[(int64_t)o * a.n_out + t];
+                }
             }
             if (src < 0 || src >= a.n_in) src = -1;
         }
@@ -236,13 +249,13 @@ __global__ __launch_bounds__(kThreads, 1) void conv_kernel(ConvArgs a) {
         my_min = min(my_min, __shfl_xor(my_min, off));
     }
     if (lane == 0) {
-        if (my_mask) atomicOr(&smask, my_mask);
-        atomicMin(&smin, my_min);
+        if (my_mask) atomicOr(reinterpret_cast<uint32_t*>(&L.misc[0]), my_mask);
+        atomicMin(&L.misc[1], my_min);
     }
     lds_barrier();
 
     // ---- dedupe: bitmap over [lo, lo + 32768) ----
-    const int32_t lo = smin;
+    const int32_t lo = L.misc[1];
     bool fail = false;
 #pragma unroll
     for (int k = 0; k < EPT; ++k) {
@@ -252,72 +265,216 @@ __global__ __launch_bounds__(kThreads, 1) void conv_kernel(ConvArgs a) {
             else atomicOr(&bm[off >> 5], 1u << (off & 31));
         }
     }
-    if (fail) s_fail = 1;
+    if (fail) L.misc[2] = 1;
     lds_barrier();
-    // ranks: thread tid owns words 2*tid, 2*tid+1
-    const uint32_t w0 = bm[2 * tid];
-    const uint32_t w1 = bm[2 * tid + 1];
-    const int cnt = __popc(w0) + __popc(w1);
+    // ranks: thread tid owns words WPT*tid .. WPT*tid + WPT - 1
+    uint32_t wv[WPT];
+    int cnt = 0;
+#pragma unroll
+    for (int w = 0; w < WPT; ++w) {
+        wv[w] = bm[WPT * tid + w];
+        cnt += __popc(wv[w]);
+    }
     int incl = cnt;
     for (int off = 1; off < 64; off <<= 1) {
         const int v = __shfl_up(incl, off);
         if (lane >= off) incl += v;
     }
-    if (lane == 63) wsum[wave] = incl;
+    if (lane == 63) L.wsum[wave] = incl;
     lds_barrier();
     int base = incl - cnt;
     int U = 0;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-        if (w < wave) base += wsum[w];
-        U += wsum[w];
+        if (w < wave) base += L.wsum[w];
+        U += L.wsum[w];
     }
-    const bool fast = !s_fail && U <= kUMax;
-    wbase[2 * tid] = base;
-    wbase[2 * tid + 1] = base + __popc(w0);
-    if (fast) {
-        int id = base;
-        uint32_t m = w0;
-        while (m) {
-            const int b = __ffs(m) - 1;
-            m &= m - 1;
-            urow[id++] = lo + (2 * tid) * 32 + b;
-        }
-        m = w1;
-        while (m) {
-            const int b = __ffs(m) - 1;
-            m &= m - 1;
-            urow[id++] = lo + (2 * tid + 1) * 32 + b;
+    const bool fast = !L.misc[2] && U <= kUMax;
+    {
+        int b = base;
+#pragma unroll
+        for (int w = 0; w < WPT; ++w) {
+            wbase[WPT * tid + w] = b;
+            if (fast) {
+                uint32_t m = wv[w];
+                while (m) {
+                    const int bit = __ffs(m) - 1;
+                    m &= m - 1;
+                    L.urow[b++] = lo + (WPT * tid + w) * 32 + bit;
+                }
+            } else {
+                b += __popc(wv[w]);
+            }
         }
     }
     lds_barrier();
+    if (fast) {
 #pragma unroll
-    for (int k = 0; k < EPT; ++k) {
-        const int e = tid + k * NT;
-        if (e < NQ) {
-            const int r = e / NTAPS;
-            const int o = e - r * NTAPS;
-            int32_t out;
-            if (fast) {
+        for (int k = 0; k < EPT; ++k) {
+            const int e = tid + k * NT;
+            if (e < NQ) {
+                const int r = e / NTAPS;
+                const int o = e - r * NTAPS;
+                int32_t out = U;  // the zero row
                 if (ent[k] >= 0) {
                     const int32_t off = ent[k] - lo;
                     const int wi = off >> 5;
                     out = wbase[wi] + __popc(bm[wi] & ((1u << (off & 31)) - 1u));
-                } else {
-                    out = U;  // the zero row
                 }
-            } else {
-                out = ent[k];
+                L.sidx[o * TM + r] = (uint16_t)slot_key(out);
             }
-            sidx[o * TM + r] = out;
         }
+        for (int r = tid; r < TM; r += NT) L.sidx[NTAPS * TM + r] = (uint16_t)slot_key(U);
+    }
+    if (tid == 0) {
+        // the active taps in ascending order, four per word; padding 0xff
+        uint32_t m = (uint32_t)L.misc[0];
+        for (int w = 0; w < kTapWords; ++w) {
+            uint32_t word = 0;
+            for (int b = 0; b < PD; ++b) {
+                uint32_t t = 0xffu;
+                if (m) {
+                    t = (uint32_t)(__ffs(m) - 1);
+                    m &= m - 1;
+                }
+                word |= t << (8 * b);
+            }
+            L.tlw[w] = word;
+        }
+        L.misc[3] = U;
+        L.misc[4] = fast ? 1 : 0;
     }
     lds_barrier();
+}
 
-    const uint32_t tile_mask = smask;
+// One block per 256-row tile: runs the tile setup once and stores it, so
+// every conv over the same index table skips it.
+template <int NTAPS>
+__global__ __launch_bounds__(512) void conv_plan_kernel(ConvArgs a, char* plan) {
+    __shared__ uint32_t scratch[2 * kWinWords];
+    __shared__ __attribute__((aligned(16))) uint16_t sidx[(NTAPS + 1) * kTM];
+    __shared__ __attribute__((aligned(16))) uint32_t tlw[kTapWords];
+    __shared__ __attribute__((aligned(16))) int32_t urow[kUMax];
+    __shared__ __attribute__((aligned(16))) int32_t srow[kTM];
+    __shared__ int32_t wsum[8];
+    __shared__ int32_t misc[8];
+    const TileLds L{scratch, sidx, tlw, urow, srow, wsum, misc};
+    const int64_t tm = blockIdx.x;
+    tile_setup<NTAPS, 512, 4>(a, tm * kTM, L);
+    char* pt = plan + tm * plan_tile_bytes(NTAPS);
+    int32_t* hdr = reinterpret_cast<int32_t*>(pt);
+    const int U = misc[3];
+    const int tid = threadIdx.x;
+    if (tid < 8) hdr[tid] = tid == 0 ? U : tid == 1 ? misc[0] : tid == 2 ? misc[4] : 0;
+    else if (tid < 16) hdr[tid] = (int32_t)tlw[tid - 8];
+    for (int i = tid; i < kTM; i += 512) reinterpret_cast<int32_t*>(pt + kPlanSrow)[i] = srow[i];
+    if (misc[4]) {
+        for (int i = tid; i < U; i += 512) reinterpret_cast<int32_t*>(pt + kPlanUrow)[i] = urow[i];
+        for (int i = tid; i < (NTAPS + 1) * kTM; i += 512)
+            reinterpret_cast<uint16_t*>(pt + kPlanSidx)[i] = sidx[i];
+    }
+}
+
+template <typename T, bool Q8, bool PACKED, int NTAPS, int TN, int WM, int WN, int PD>
+__global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
+    using M = Mfma<T>;
+    using P = Panel<T, Q8>;
+    constexpr int TM = kTM;
+    constexpr int NW = WM * WN;
+    constexpr int NT = NW * 64;
+    constexpr int ES = sizeof(T);
+    constexpr int KC = P::KC;
+    constexpr int WTM = TM / WM;
+    constexpr int WTN = TN / WN;
+    constexpr int FM = WTM / 32;
+    constexpr int FN = WTN / 32;
+    constexpr int NQ = NTAPS * TM;
+    constexpr int STAGE = (kUMax + 1) * kSegs;  // 16-byte units per A buffer
+    constexpr int HALF = (STAGE + 1) / 2;
+    constexpr int SPT = (HALF + NT - 1) / NT;   // staged units per thread per half
+    static_assert(WM * WN == NW && FM >= 1 && FN >= 1, "wave geometry");
+    static_assert(!Q8 || ES == 2, "Q8_0 weights feed 16-bit MFMA operands");
+    static_assert(NTAPS <= 32, "tap mask is 32-bit");
+    static_assert(SPT <= 32, "stage geometry");
+    static_assert(2 * kWinWords * 4 <= STAGE * 16, "bitmap aliases the A stage");
+    static_assert(PD == 4, "the step groups pack four taps per word");
+
+    __shared__ u32x4 Au[2 * STAGE];    // two A buffers: (U + 1) rows x 64 bytes each
+    __shared__ __attribute__((aligned(16))) uint16_t sidx[NQ + TM];  // slot keys; row NTAPS = zeros
+    __shared__ __attribute__((aligned(16))) uint32_t tlw[kTapWords]; // step taps, 4 per word
+    __shared__ __attribute__((aligned(16))) int32_t urow[kUMax];     // source row of each union slot
+    __shared__ __attribute__((aligned(16))) int32_t srow[TM];        // output row of each tile row
+    __shared__ int32_t wsum[NW];
+    __shared__ int32_t misc[8];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+
+    // XCD-major tile mapping
+    const int64_t xcd = blockIdx.x & 7;
+    const int64_t local = blockIdx.x >> 3;
+    const int64_t tile = xcd * a.tiles_per_xcd + local;
+    if (local >= a.tiles_per_xcd || tile >= a.total_tiles) return;
+    const int64_t tm = tile / a.tiles_n;
+    const int tn = (int)(tile % a.tiles_n);
+    const int64_t r0 = tm * TM;
+    const int co0 = tn * TN;
+
+    uint32_t tile_mask;
+    int U;
+    bool fast;
+    if (a.plan) {
+        // the tile's setup from the plan: 16-byte copies into LDS
+        const char* pt = static_cast<const char*>(a.plan) + tm * plan_tile_bytes(NTAPS);
+        const int32_t* hdr = reinterpret_cast<const int32_t*>(pt);
+        U = hdr[0];
+        tile_mask = (uint32_t)hdr[1];
+        fast = hdr[2] != 0;
+        constexpr int NSR = TM / 4;                 // srow units
+        constexpr int NSI = (NTAPS + 1) * TM / 8;   // sidx units
+        const int nur = fast ? (U + 3) / 4 : 0;     // urow units
+        const int total = 2 + NSR + (fast ? NSI : 0) + nur;
+        for (int u = tid; u < total; u += NT) {
+            const u32x4* src;
+            u32x4* dst;
+            if (u < 2) {
+                src = reinterpret_cast<const u32x4*>(pt + 32) + u;
+                dst = reinterpret_cast<u32x4*>(tlw) + u;
+            } else if (u < 2 + NSR) {
+                src = reinterpret_cast<const u32x4*>(pt + kPlanSrow) + (u - 2);
+                dst = reinterpret_cast<u32x4*>(srow) + (u - 2);
+            } else if (u < 2 + NSR + nur) {
+                src = reinterpret_cast<const u32x4*>(pt + kPlanUrow) + (u - 2 - NSR);
+                dst = reinterpret_cast<u32x4*>(urow) + (u - 2 - NSR);
+            } else {
+                src = reinterpret_cast<const u32x4*>(pt + kPlanSidx) + (u - 2 - NSR - nur);
+                dst = reinterpret_cast<u32x4*>(sidx) + (u - 2 - NSR - nur);
+            }
+            *dst = *src;
+        }
+        lds_barrier();
+    } else {
+        const TileLds L{reinterpret_cast<uint32_t*>(Au), sidx, tlw, urow, srow, wsum, misc};
+        tile_setup<NTAPS, NT, PD>(a, r0, L);
+        tile_mask = (uint32_t)misc[0];
+        U = misc[3];
+        fast = misc[4] != 0;
+    }
+
+    // source row of (tap o, tile row r), -1 when missing (fallback tiles)
+    auto src_of = [&](int o, int r) __attribute__((always_inline)) -> int32_t {
+        const int32_t t = srow[r];
+        if (t < 0) return -1;
+        int32_t s;
+        if (NTAPS == 1 && a.idx == nullptr) s = t;  // identity map (dense 1x1x1 conv)
+        else if (a.idx_layout == SPC_IDX_TOKEN_MAJOR) s = a.idx[(int64_t)t * NTAPS + o];
+        else s = a.idx[(int64_t)o * a.n_out + t];
+        return (s < 0 || s >= a.n_in) ? -1 : s;
+    };
+
     const int nt = __popc(tile_mask);
     const int kch = a.cin / KC;
-    const int nsteps = nt * kch;
     const int ncol32 = a.cout / 32;
 
     const int wm = wave / WN;
@@ -332,40 +489,25 @@ __global__ __launch_bounds__(kThreads, 1) void conv_kernel(ConvArgs a) {
             for (int k = 0; k < 16; ++k) acc[i][j][k] = 0.0f;
 
     const char* xb = static_cast<const char*>(a.x);
-
-    // step cursor: (remaining taps of the chunk, chunk); tap = lowest bit
-    struct Cursor {
-        uint32_t m;
-        int kc;
-    };
-    auto advance = [&](Cursor c) __attribute__((always_inline)) -> Cursor {
-        c.m &= c.m - 1;
-        if (c.m == 0) {
-            c.m = tile_mask;
-            ++c.kc;
-        }
-        return c;
-    };
+    const u32x4 zero4 = {0u, 0u, 0u, 0u};
 
     struct Slot {
         u32x4 q[FN][P::NG];
         float d[Q8 ? FN : 1];
     };
-    Slot ring[kPD];
 
-    // B operands of (tap, chunk) for this wave's FN column blocks
-    auto load_b = [&](Cursor c, Slot& sl) __attribute__((always_inline)) {
-        const int o = __ffs(c.m) - 1;
-        const int kc = c.kc;
+    // B operands of (tap o, chunk kc) for this wave's FN column blocks
+    auto load_b = [&](int o, int kc, Slot& sl) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
-            const int c32 = (co0 + wn * WTN) / 32 + j;
+            const int c32 = (co0 + wn * WTN) / 32 + j;  // wave-uniform
             const int co = c32 * 32 + (lane & 31);
             if constexpr (PACKED) {
                 const int64_t panel = ((int64_t)o * kch + kc) * ncol32 + c32;
-                const u32x4* src = static_cast<const u32x4*>(a.w) + panel * (P::NG * 64);
+                const char* pb = static_cast<const char*>(a.w) + panel * (P::NG * 1024);
 #pragma unroll
-                for (int g = 0; g < P::NG; ++g) sl.q[j][g] = src[g * 64 + lane];
+                for (int g = 0; g < P::NG; ++g)
+                    sl.q[j][g] = *reinterpret_cast<const u32x4*>(pb + g * 1024 + lane * 16);
                 if constexpr (Q8)
                     sl.d[j] = static_cast<const float*>(a.wscale)[((int64_t)o * kch + kc) * a.cout + co];
             } else {
@@ -397,14 +539,14 @@ __global__ __launch_bounds__(kThreads, 1) void conv_kernel(ConvArgs a) {
         }
     };
 
-    // B fragment of k-step ks from a prefetched slot
+    // B fragment of k-step ks from a loaded slot
     auto b_frag = [&](const Slot& sl, int j, int ks) __attribute__((always_inline)) {
         typename M::frag f;
-        const u32x4 wv = sl.q[j][ks / P::G];
+        const u32x4 wv4 = sl.q[j][ks / P::G];
         if constexpr (Q8) {
             // 8 int8 quants of this k-step -> bf16(d * q)
-            const uint32_t lo32 = (ks % P::G) == 0 ? wv.x : wv.z;
-            const uint32_t hi32 = (ks % P::G) == 0 ? wv.y : wv.w;
+            const uint32_t lo32 = (ks % P::G) == 0 ? wv4.x : wv4.z;
+            const uint32_t hi32 = (ks % P::G) == 0 ? wv4.y : wv4.w;
             uint16_t h[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
@@ -418,167 +560,237 @@ __global__ __launch_bounds__(kThreads, 1) void conv_kernel(ConvArgs a) {
                               (uint32_t)h[6] | ((uint32_t)h[7] << 16)};
             f = __builtin_bit_cast(typename M::frag, pk);
         } else if constexpr (P::G == 1) {
-            f = __builtin_bit_cast(typename M::frag, wv);
+            f = __builtin_bit_cast(typename M::frag, wv4);
         } else {
             // explicit component select: indexing the vector by (ks % G) read
             // component 0 for every k-step in generated code
             const int c = ks % P::G;
-            const uint32_t word = c == 0 ? wv.x : c == 1 ? wv.y : c == 2 ? wv.z : wv.w;
+            const uint32_t word = c == 0 ? wv4.x : c == 1 ? wv4.y : c == 2 ? wv4.z : wv4.w;
             f = __builtin_bit_cast(float, word);
         }
         return f;
     };
 
-    // stage the gathered source rows of (tap o, chunk kc) into Au: the whole
-    // deduplicated union (fast; slot U is the zero row) or the tap's TM
-    // rows.  All indices first, then all loads, then all stores, so a
-    // batch's global loads are in flight together; missing rows load row 0
-    // (valid whenever a step exists) and are zeroed.
-    auto stage_a = [&](int o, int kc) __attribute__((always_inline)) {
-        const int rows = fast ? U + 1 : TM;
-        const int nchunks = rows * CPR;
-        const int64_t koff = (int64_t)kc * KC;
-        for (int c0 = 0; c0 < nchunks; c0 += NT * 8) {
-            int32_t src[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int c = min(c0 + j * NT + tid, nchunks - 1);
-                const int r = c / CPR;
-                src[j] = fast ? (r < U ? urow[r] : -1) : sidx[o * TM + r];
-            }
-            u32x4 v[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int c = min(c0 + j * NT + tid, nchunks - 1);
-                const int seg = c % CPR;
-                const int64_t row = src[j] >= 0 ? src[j] : 0;
-                v[j] = *reinterpret_cast<const u32x4*>(xb + (row * a.cin + koff + seg * CH) * ES);
-            }
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int c = c0 + j * NT + tid;
-                if (c < nchunks) {
-                    const int r = c / CPR;
-                    const int seg = c % CPR;
-                    const u32x4 z = {0u, 0u, 0u, 0u};
-                    *reinterpret_cast<u32x4*>(&Au[r * PITCH + seg * CH]) = src[j] >= 0 ? v[j] : z;
-                }
-            }
-        }
-    };
-
-    Cursor cc{tile_mask, 0};  // step being computed
-    Cursor pc{tile_mask, 0};  // next weight prefetch
-
-    // Weight ring: the operands of step m are loaded into ring[m % kPD]
-    // during step m - kPD; the step body is instantiated once per ring
-    // position so every slot index is a compile-time constant.
-    // A operands of one step: union slots of the wave's rows for a tap, and
-    // the fragments read from them.  Slots depend only on the tap, so they
-    // are read two steps ahead; fragments one step ahead (within a chunk),
-    // overlapping the LDS latency with the current step's MFMAs.
     typedef typename M::frag AFrag[P::KS][FM];
-    auto read_slots = [&](int o, int* sl) __attribute__((always_inline)) {
-#pragma unroll
-        for (int i = 0; i < FM; ++i) {
-            const int rl = wm * WTM + i * 32 + (lane & 31);
-            sl[i] = fast ? sidx[o * TM + rl] : rl;
-        }
-    };
-    auto read_frags = [&](const int* sl, AFrag& f) __attribute__((always_inline)) {
-#pragma unroll
-        for (int ks = 0; ks < P::KS; ++ks) {
-            const int kof = ks * M::KSUB + (lane >> 5) * M::EPL;
-#pragma unroll
-            for (int i = 0; i < FM; ++i)
-                f[ks][i] = *reinterpret_cast<const typename M::frag*>(&Au[sl[i] * PITCH + kof]);
-        }
-    };
-    AFrag afc;         // fragments of the current step
-    int slot_n[FM];    // slots of the next step
-
-    auto step = [&](int s, auto u_const) __attribute__((always_inline)) {
-        constexpr int u = decltype(u_const)::value;
-        const int o = __ffs(cc.m) - 1;
-        const Cursor nc = advance(cc);  // step s+1
-        if (fast ? cc.m == tile_mask : true) {  // first tap of a chunk, or every step
-            if (s > 0) lds_barrier();           // every wave is done reading Au
-            stage_a(o, cc.kc);
-            lds_barrier();
-            int sl[FM];
-            read_slots(o, sl);
-            read_frags(sl, afc);
-            if (s + 1 < nsteps) read_slots(__ffs(nc.m) - 1, slot_n);
-        }
-        // prefetch: fragments of step s+1 (same chunk) and slots of step s+2
-        const bool next_same_chunk = fast && s + 1 < nsteps && nc.kc == cc.kc;
-        AFrag afn;
-        if (next_same_chunk) read_frags(slot_n, afn);
-        int slot_nn[FM];
-        if (s + 2 < nsteps) read_slots(__ffs(advance(nc).m) - 1, slot_nn);
+    // The MFMA computes the transposed block (weights as the 32-row operand,
+    // gathered features as the 32-column one): the accumulator of lane l then
+    // holds output row l%32 and output channels 8*(k/4) + 4*(l/32) + k%4 for
+    // element k -- four runs of four consecutive channels per lane, stored
+    // straight to global memory.
+    auto mma_step = [&](const AFrag& af, const Slot& bs) __attribute__((always_inline)) {
 #pragma unroll
         for (int ks = 0; ks < P::KS; ++ks) {
 #pragma unroll
             for (int j = 0; j < FN; ++j) {
-                const typename M::frag bf = b_frag(ring[u], j, ks);
+                const typename M::frag bf = b_frag(bs, j, ks);
 #pragma unroll
-                for (int i = 0; i < FM; ++i) acc[i][j] = M::mma(afc[ks][i], bf, acc[i][j]);
+                for (int i = 0; i < FM; ++i) acc[i][j] = M::mma(bf, af[ks][i], acc[i][j]);
             }
         }
-        if (next_same_chunk) {
+    };
+    // A fragments of k-slices of 32 rows per FM block.  sl[] holds slot
+    // keys (fast tiles) or tile rows (fallback, turned into keys here); the
+    // segment and byte of each k-step within the 64-byte row are lane
+    // constants.
+    auto read_frags = [&](int buf, const int* sl, AFrag& f) __attribute__((always_inline)) {
+        const char* ab = reinterpret_cast<const char*>(Au + buf * STAGE);
 #pragma unroll
-            for (int ks = 0; ks < P::KS; ++ks)
+        for (int ks = 0; ks < P::KS; ++ks) {
+            const int byte = (ks * M::KSUB + (lane >> 5) * M::EPL) * ES;  // within the 64-byte row
 #pragma unroll
-                for (int i = 0; i < FM; ++i) afc[ks][i] = afn[ks][i];
+            for (int i = 0; i < FM; ++i)
+                f[ks][i] = *reinterpret_cast<const typename M::frag*>(
+                    ab + (sl[i] ^ (byte >> 4)) * 16 + (byte & 15));
         }
-        if (s + 2 < nsteps) {
+    };
+    // union slots of the wave's rows for sidx row `row` (a tap, or NTAPS = zeros)
+    auto read_slots = [&](int row, int* sl) __attribute__((always_inline)) {
 #pragma unroll
-            for (int i = 0; i < FM; ++i) slot_n[i] = slot_nn[i];
-        }
-        if (s + kPD < nsteps) {
-            load_b(pc, ring[u]);
-            pc = advance(pc);
-        }
-        cc = nc;
+        for (int i = 0; i < FM; ++i) sl[i] = sidx[row * TM + wm * WTM + i * 32 + (lane & 31)];
     };
 
-    static_assert(kPD == 3, "the prologue and the unrolled loop assume a 3-deep ring");
-    if (nsteps > 0) {
-        load_b(pc, ring[0]);
-        pc = advance(pc);
-        if (1 < nsteps) {
-            load_b(pc, ring[1]);
-            pc = advance(pc);
+    if (fast && nt > 0) {
+        // ---- A staging: half h of chunk kc's union rows ------------------
+        // Units u = slot * 4 + segment of the (U + 1) staged rows; half h
+        // covers [h * hu, min(total, (h + 1) * hu)).  Loads go to registers
+        // half a chunk ahead of their use; slot U and units past the end are
+        // zeros.  The commit writes them to the chunk's LDS buffer.
+        const int total_u = (U + 1) * kSegs;
+        const int hu = (total_u + 1) / 2;
+        u32x4 stg[SPT];
+        uint32_t stg_zero = 0;
+        auto stage_issue = [&](int kc, int h) __attribute__((always_inline)) {
+            const int beg = h * hu;
+            const int end = min(total_u, beg + hu);
+            const int64_t koff = (int64_t)kc * KC * ES;
+            stg_zero = 0;
+#pragma unroll
+            for (int j = 0; j < SPT; ++j) {
+                const int u = beg + j * NT + tid;
+                const int slot = u >> 2;
+                const int32_t row = (u < end && slot < U) ? urow[slot] : -1;
+                if (row < 0) stg_zero |= 1u << j;
+                const int64_t rr = row >= 0 ? row : 0;
+                stg[j] = *reinterpret_cast<const u32x4*>(xb + rr * a.cin * ES + koff + (u & 3) * 16);
+            }
+        };
+        auto stage_commit = [&](int buf, int h) __attribute__((always_inline)) {
+            const int beg = h * hu;
+            const int end = min(total_u, beg + hu);
+            u32x4* dst = Au + buf * STAGE;
+#pragma unroll
+            for (int j = 0; j < SPT; ++j) {
+                const int u = beg + j * NT + tid;
+                if (u < end) dst[seg_pos(u >> 2, u & 3)] = ((stg_zero >> j) & 1u) ? zero4 : stg[j];
+            }
+        };
+
+        // Steps of a chunk: the active taps in ascending order, padded to a
+        // multiple of PD with steps that read the zero slot (row NTAPS)
+        // against the first tap's weights.  A group of PD steps is unrolled;
+        // every register-array index inside it is a compile-time constant:
+        // B operands of step i live in ring[i % PD] (loaded PD steps ahead),
+        // A fragments in afr[i % 2] (read one step ahead, within a chunk),
+        // union slots in sreg[i % 2] (read two steps ahead; slots do not
+        // depend on the chunk, so they run ahead across chunk boundaries).
+        const int ngr = (nt + PD - 1) / PD;
+        const int gmid = ngr / 2;
+        const int tfirst = __ffs(tile_mask) - 1;
+        auto b_tap = [&](uint32_t word, int b) __attribute__((always_inline)) -> int {
+            const int t = (int)((word >> (8 * b)) & 0xffu);
+            return t == 0xff ? tfirst : t;
+        };
+        auto s_row = [&](uint32_t word, int b) __attribute__((always_inline)) -> int {
+            const int t = (int)((word >> (8 * b)) & 0xffu);
+            return t == 0xff ? NTAPS : t;
+        };
+
+        Slot ring[PD];
+        AFrag afr[2];
+        int sreg[2][FM];
+
+        {
+            const uint32_t w0 = tlw[0];
+#pragma unroll
+            for (int p = 0; p < PD; ++p) load_b(b_tap(w0, p), 0, ring[p]);
+            read_slots(s_row(w0, 0), sreg[0]);
+            read_slots(s_row(w0, 1), sreg[1]);
+            stage_issue(0, 0);
+            stage_commit(0, 0);
+            stage_issue(0, 1);
+            stage_commit(0, 1);
+            lds_barrier();
+            if (kch > 1) stage_issue(1, 0);
+            read_frags(0, sreg[0], afr[0]);
         }
-        if (2 < nsteps) {
-            load_b(pc, ring[2]);
-            pc = advance(pc);
+
+        for (int kc = 0; kc < kch; ++kc) {
+            const int buf = kc & 1;
+            if (kc > 0) {
+                stage_commit(buf, 1);  // second half of this chunk
+                lds_barrier();         // chunk complete; every wave done with the other buffer
+                if (kc + 1 < kch) stage_issue(kc + 1, 0);
+                read_frags(buf, sreg[0], afr[0]);
+            }
+            for (int g = 0; g < ngr; ++g) {
+                const bool last_g = g + 1 == ngr;
+                const uint32_t w0 = tlw[g];
+                const uint32_t w1 = tlw[last_g ? 0 : g + 1];
+                const int kc_next = last_g ? kc + 1 : kc;  // chunk of the steps PD ahead
+                const int kc_b = min(kc_next, kch - 1);  // past the last chunk: a valid, unused panel
+                auto step = [&](auto u_const) __attribute__((always_inline)) {
+                    constexpr int u = decltype(u_const)::value;
+                    // slots of the step after next (they do not depend on the chunk)
+                    read_slots(u + 2 < PD ? s_row(w0, u + 2) : s_row(w1, u + 2 - PD), sreg[u & 1]);
+                    // A fragments of the next step; after a chunk's last step they
+                    // are re-read behind the barrier, so this read is unused
+                    read_frags(buf, sreg[(u + 1) & 1], afr[(u + 1) & 1]);
+                    mma_step(afr[u & 1], ring[u]);
+                    // weights of the step PD ahead
+                    load_b(b_tap(w1, u), kc_b, ring[u]);
+                    // issue order: slot reads, then MFMAs interleaved with the
+                    // fragment reads and their address arithmetic, then the
+                    // weight loads
+                    constexpr int NMF = P::KS * FM * FN;
+                    constexpr int NFR = P::KS * FM;
+                    __builtin_amdgcn_sched_group_barrier(0x100, FM, 0);
+#pragma unroll
+                    for (int q = 0; q < NMF; ++q) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                        if (q < NFR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+                    }
+                    __builtin_amdgcn_sched_group_barrier(0x020, FN * P::NG, 0);
+                };
+                step(std::integral_constant<int, 0>{});
+                step(std::integral_constant<int, 1>{});
+                step(std::integral_constant<int, 2>{});
+                step(std::integral_constant<int, 3>{});
+                if (g == gmid && kc + 1 < kch) {
+                    stage_commit(buf ^ 1, 0);
+                    stage_issue(kc + 1, 1);
+                }
+            }
         }
-    }
-    for (int s0 = 0; s0 < nsteps; s0 += kPD) {
-        step(s0, std::integral_constant<int, 0>{});
-        if (s0 + 1 < nsteps) step(s0 + 1, std::integral_constant<int, 1>{});
-        if (s0 + 2 < nsteps) step(s0 + 2, std::integral_constant<int, 2>{});
+    } else if (nt > 0) {
+        // Fallback (the union does not fit the stage): each tap's 256 source
+        // rows are staged separately, one synchronous step at a time.
+        for (int kc = 0; kc < kch; ++kc) {
+            uint32_t m = tile_mask;
+            while (m) {
+                const int o = __ffs(m) - 1;
+                m &= m - 1;
+                lds_barrier();  // every wave is done reading the stage
+                {
+                    const int64_t koff = (int64_t)kc * KC * ES;
+                    constexpr int UPT = TM * kSegs / NT;
+#pragma unroll
+                    for (int j = 0; j < UPT; ++j) {
+                        const int u = j * NT + tid;
+                        const int32_t src = src_of(o, u >> 2);
+                        u32x4 v = zero4;
+                        if (src >= 0)
+                            v = *reinterpret_cast<const u32x4*>(xb + (int64_t)src * a.cin * ES + koff +
+                                                                (u & 3) * 16);
+                        Au[seg_pos(u >> 2, u & 3)] = v;
+                    }
+                }
+                lds_barrier();
+                int sl[FM];
+#pragma unroll
+                for (int i = 0; i < FM; ++i) sl[i] = slot_key(wm * WTM + i * 32 + (lane & 31));
+                AFrag af;
+                read_frags(0, sl, af);
+                Slot bs;
+                load_b(o, kc, bs);
+                mma_step(af, bs);
+            }
+        }
     }
 
-    // epilogue: 32x32 accumulator layout -- element k of lane l holds
-    // row 8*(k/4) + 4*(l/32) + k%4, column l%32
+    // ---- epilogue: + bias in F32, one rounding, each lane stores its row's
+    // four runs of four channels (8 bytes in 16-bit dtypes, 16 in f32)
+    char* yb = static_cast<char*>(a.y);
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-        const int col = co0 + wn * WTN + j * 32 + (lane & 31);
-        const float bv = a.bias ? M::ld(a.bias, col) : 0.0f;
+    for (int i = 0; i < FM; ++i) {
+        const int32_t t = srow[wm * WTM + i * 32 + (lane & 31)];
 #pragma unroll
-        for (int i = 0; i < FM; ++i) {
+        for (int j = 0; j < FN; ++j) {
 #pragma unroll
-            for (int k = 0; k < 16; ++k) {
-                const int rl = wm * WTM + i * 32 + 8 * (k >> 2) + 4 * (lane >> 5) + (k & 3);
-                const int32_t t = srow[rl];
+            for (int g = 0; g < 4; ++g) {
+                const int col = co0 + wn * WTN + j * 32 + 8 * g + 4 * (lane >> 5);
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    v[e] = acc[i][j][4 * g + e] + (a.bias ? M::ld(a.bias, col + e) : 0.0f);
                 if (t >= 0) {
-                    const float v = acc[i][j][k] + bv;
+                    char* dst = yb + ((int64_t)t * a.cout + col) * ES;
                     if constexpr (ES == 4) {
-                        static_cast<float*>(a.y)[(int64_t)t * a.cout + col] = v;
+                        *reinterpret_cast<floatx4*>(dst) = floatx4{v[0], v[1], v[2], v[3]};
                     } else {
-                        static_cast<uint16_t*>(a.y)[(int64_t)t * a.cout + col] = M::cvt(v);
+                        *reinterpret_cast<u32x2*>(dst) =
+                            u32x2{(uint32_t)M::cvt(v[0]) | ((uint32_t)M::cvt(v[1]) << 16),
+                                  (uint32_t)M::cvt(v[2]) | ((uint32_t)M::cvt(v[3]) << 16)};
                     }
                 }
             }
@@ -594,16 +806,16 @@ hipError_t launch_conv(hipStream_t s, ConvArgs a) {
     a.tiles_per_xcd = ceil_div(a.total_tiles, 8);
     const int64_t grid = a.tiles_per_xcd * 8;
     if (grid == 0) return hipSuccess;
-    conv_kernel<T, Q8, PACKED, NTAPS, TN, WM, WN><<<(unsigned)grid, kThreads, 0, s>>>(a);
+    conv_kernel<T, Q8, PACKED, NTAPS, TN, WM, WN, 4><<<(unsigned)grid, WM * WN * 64, 0, s>>>(a);
     return hipGetLastError();
 }
 
 // TN = largest of {128, 64, 32} dividing cout; 8 waves as 4x2 (64x64 wave
-// tiles) or 8x1.
+// tiles), 4x2 (64x32) or 8x1 (32x32).
 template <typename T, bool Q8, bool PACKED, int NTAPS>
 hipError_t dispatch_tn(hipStream_t s, const ConvArgs& a) {
     if (a.cout % 128 == 0) return launch_conv<T, Q8, PACKED, NTAPS, 128, 4, 2>(s, a);
-    if (a.cout % 64 == 0) return launch_conv<T, Q8, PACKED, NTAPS, 64, 8, 1>(s, a);
+    if (a.cout % 64 == 0) return launch_conv<T, Q8, PACKED, NTAPS, 64, 4, 2>(s, a);
     return launch_conv<T, Q8, PACKED, NTAPS, 32, 8, 1>(s, a);
 }
 

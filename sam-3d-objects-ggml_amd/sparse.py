@@ -386,6 +386,12 @@ def _resolution(x: SparseTensor) -> int:
     return max(2, max(x.data.spatial_shape) if x.data.spatial_shape else 2)
 
 
+def _plan(x: SparseTensor, key, idx, ntaps: int, n_out: int, n_in: int):
+    """Tile plan of an index table, cached with the coordinates like the maps."""
+    return x.data.cached(("plan", key), lambda c: nat.conv_plan(
+        idx, ntaps=ntaps, n_out=n_out, n_in=n_in, device=c.device))
+
+
 def _downsample_map(x: SparseTensor) -> nat.DownsampleMap:
     return x.data.cached(
         "down2", lambda c: nat.downsample_map(c.contiguous(), x.data.batch_size,
@@ -544,7 +550,8 @@ class _ConvCore:
             b = torch.nn.functional.pad(b, (0, cout_p - b.shape[0]))
         return b.contiguous()
 
-    def _conv(self, feats: torch.Tensor, idx: Optional[torch.Tensor], n_out: int) -> torch.Tensor:
+    def _conv(self, feats: torch.Tensor, idx: Optional[torch.Tensor], n_out: int,
+              plan: Optional[torch.Tensor] = None) -> torch.Tensor:
         c = self.conv
         if feats.dim() != 2 or feats.shape[1] != c.in_channels:
             raise ValueError(f"expected feats [N, {c.in_channels}], got {tuple(feats.shape)}")
@@ -557,7 +564,7 @@ class _ConvCore:
                 x = torch.nn.functional.pad(x, (0, cin_p - c.in_channels))
             w = self._weight_operand(x.dtype, x.device)
             b = self._bias_operand(x.dtype, x.device)
-            y = nat.sparse_conv(x, w, b, idx, ntaps=self._ntaps, n_out=n_out)
+            y = nat.sparse_conv(x, w, b, idx, ntaps=self._ntaps, n_out=n_out, plan=plan)
             if y.shape[1] != c.out_channels:
                 y = y[:, : c.out_channels].contiguous()
             return y
@@ -601,14 +608,17 @@ class SparseConv3d(nn.Module, _ConvCore):
         scale = tuple(s * k for s, k in zip(x._scale, self.stride))
         if self._kind == "subm3":
             m = _subm_map(x)
-            feats = self._conv(x.feats, m.token_major, x.feats.shape[0])
+            n = x.feats.shape[0]
+            feats = self._conv(x.feats, m.token_major, n, _plan(x, "subm3", m.token_major, 27, n, n))
             data = x.data.replace_feature(feats)
         elif self._kind == "subm1":
-            feats = self._conv(x.feats, None, x.feats.shape[0])
+            n = x.feats.shape[0]
+            feats = self._conv(x.feats, None, n, _plan(x, "dense1", None, 1, n, n))
             data = x.data.replace_feature(feats)
         else:
             d = _downsample_map(x)
-            feats = self._conv(x.feats, d.stride2_taps, d.nc)
+            feats = self._conv(x.feats, d.stride2_taps, d.nc,
+                               _plan(x, "down2", d.stride2_taps, 8, d.nc, d.nf))
             spatial = [(s + 1) // 2 for s in x.data.spatial_shape]
             data = SparseTensorData(feats, d.coarse_coords, spatial, x.data.batch_size)
         out = SparseTensor(data, shape=new_shape, layout=None if spatial_changed else x.layout,
@@ -650,7 +660,9 @@ class SparseInverseConv3d(nn.Module, _ConvCore):
                              "SparseConv3d at this scale")
         taps = fine.cached(("inverse2", d.nc), lambda c: nat.stride2_inverse_taps(
             c.contiguous(), d.fine_to_coarse, d.nc))
-        feats = self._conv(x.feats, taps, d.nf)
+        plan = fine.cached(("inverse2_plan", d.nc), lambda c: nat.conv_plan(
+            taps, ntaps=8, n_out=d.nf, n_in=d.nc))
+        feats = self._conv(x.feats, taps, d.nf, plan)
         data = SparseTensorData(feats, fine.indices, fine.spatial_shape, fine.batch_size,
                                 fine.indice_dict)
         return SparseTensor(data, shape=torch.Size([x.shape[0], self.conv.out_channels]),

@@ -220,3 +220,55 @@ def test_empty_and_missing(spc, orc, dev):
     y = nat.sparse_conv(xb, wb, bb, idx, ntaps=27, n_out=n)
     torch.cuda.synchronize()
     assert torch.equal(y, bb.unsqueeze(0).expand(n, 32))
+
+
+@pytest.mark.parametrize("case", ["bf16_natural", "bf16_mask_order", "f32", "q8_0", "stride2",
+                                  "dense1", "fallback_unsorted"])
+def test_plan_matches_in_kernel_setup(spc, orc, dev, case):
+    """spc_sparse_conv_plan with a plan from spc_conv_plan computes exactly
+    what spc_sparse_conv computes with its in-kernel tile setup."""
+    import torch
+
+    nat = spc._native
+    wl = spc.workloads
+    _case(f"plan vs in-kernel setup: {case}")
+    if case == "fallback_unsorted":
+        # shell rows in random order: a tile's 256 rows reference ~5000
+        # distinct rows, beyond the 1024-row stage -- the fallback path
+        coords = wl.ellipsoid_batch(2, seed=72)
+        coords = np.ascontiguousarray(coords[np.random.default_rng(71).permutation(len(coords))])
+    else:
+        coords = wl.ellipsoid_batch(2, seed=72)
+    n = coords.shape[0]
+    c_dev = torch.from_numpy(coords).to(dev)
+    cin, cout, ntaps, n_out, n_in = 64, 128, 27, n, n
+    idx_layout, perm = nat.IDX_TOKEN_MAJOR, None
+    if case == "stride2":
+        d = nat.downsample_map(c_dev, 2, 64)
+        idx, ntaps, n_out = d.stride2_taps, 8, d.nc
+    elif case == "dense1":
+        idx, ntaps = None, 1
+    else:
+        m = nat.map_build(c_dev)
+        idx = m.token_major
+        if case == "bf16_mask_order":
+            idx, idx_layout, perm = m.offset_major, nat.IDX_OFFSET_MAJOR, m.argsort
+    g = torch.Generator(device="cpu").manual_seed(7)
+    dt = torch.float32 if case == "f32" else torch.bfloat16
+    x = torch.randn((n_in, cin), generator=g).to(dev, dt)
+    b = (torch.randn(cout, generator=g) * 0.1).to(dev, dt)
+    if case == "q8_0":
+        blocks = nat.q8_0_quantize((torch.randn((cout, ntaps, cin), generator=g) * 0.02).to(dev))
+        qs, dsc = nat.q8_0_repack(blocks)
+        w = nat.pack_weights(qs, dsc, cin=cin, cout=cout, ntaps=ntaps)
+    else:
+        w = nat.pack_weights((torch.randn((cout, ntaps, cin), generator=g) * 0.02).to(dev, dt))
+    plan = nat.conv_plan(idx, ntaps=ntaps, n_out=n_out, n_in=n_in, idx_layout=idx_layout,
+                         row_perm=perm, device=dev)
+    y0 = nat.sparse_conv(x, w, b, idx, ntaps=ntaps, n_out=n_out, idx_layout=idx_layout,
+                         row_perm=perm)
+    y1 = nat.sparse_conv(x, w, b, idx, ntaps=ntaps, n_out=n_out, idx_layout=idx_layout,
+                         row_perm=perm, plan=plan)
+    torch.cuda.synchronize()
+    assert torch.equal(y0, y1)
+    assert torch.isfinite(y1.float()).all()

@@ -78,7 +78,7 @@ def test_subm3_bf16_module_map_cached(spc, orc, dev):
         h = c1(xt)
         y = c2(h)
     # the second conv reuses the first conv's map (same coordinate tensor)
-    assert len(xt.data.indice_dict) == 1 and h.data.indice_dict is xt.data.indice_dict
+    assert len(xt.data.indice_dict) == 2 and h.data.indice_dict is xt.data.indice_dict  # map + plan
     tm = orc.conv_table_slat(coords)
     w1 = bf16_bits(orc, c1.conv.weight.detach().float().cpu().numpy().reshape(128, 27, 128))
     b1 = bf16_bits(orc, c1.conv.bias.detach().float().cpu().numpy())
