@@ -35,8 +35,8 @@
 //           bf16 operands: w = bf16(f32(d) * q).
 //   store   + bias in F32, one rounding; the MFMAs produce the transposed
 //           tile, so each lane holds runs of consecutive output channels of
-//           one row and stores them directly; every output element is
-//           written once.
+//           one row: they pass through an LDS output tile and every output
+//           row is written once with coalesced 16-byte stores.
 //   tiles   XCD-major: workgroup b runs on XCD b % 8 and each XCD gets a
 //           contiguous range of row tiles, so a neighbourhood's feature rows
 //           stay in that XCD's L2.
@@ -406,6 +406,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
     __shared__ __attribute__((aligned(16))) int32_t srow[TM];        // output row of each tile row
     __shared__ int32_t wsum[NW];
     __shared__ int32_t misc[8];
+    __shared__ float sbias[TN];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -420,6 +421,8 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
     const int tn = (int)(tile % a.tiles_n);
     const int64_t r0 = tm * TM;
     const int co0 = tn * TN;
+
+    for (int c = tid; c < TN; c += NT) sbias[c] = a.bias ? M::ld(a.bias, co0 + c) : 0.0f;
 
     uint32_t tile_mask;
     int U;
@@ -544,21 +547,20 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
         typename M::frag f;
         const u32x4 wv4 = sl.q[j][ks / P::G];
         if constexpr (Q8) {
-            // 8 int8 quants of this k-step -> bf16(d * q)
-            const uint32_t lo32 = (ks % P::G) == 0 ? wv4.x : wv4.z;
-            const uint32_t hi32 = (ks % P::G) == 0 ? wv4.y : wv4.w;
-            uint16_t h[8];
+            // 8 int8 quants of this k-step -> bf16(d * q), rounded to nearest
+            // even.  The bytes are biased to unsigned (u = q + 128, one xor
+            // per word) so each converts with a single unsigned-byte convert;
+            // fma(d, u, -128 d) is exactly d * q (d is an fp16 value and
+            // |q| <= 127, so every intermediate is exact in F32).
+            const uint32_t lo32 = ((ks % P::G) == 0 ? wv4.x : wv4.z) ^ 0x80808080u;
+            const uint32_t hi32 = ((ks % P::G) == 0 ? wv4.y : wv4.w) ^ 0x80808080u;
+            const float d = sl.d[j];
+            const float nb = -128.0f * d;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const uint32_t word = e < 4 ? lo32 : hi32;
-                const int8_t q = (int8_t)((word >> (8 * (e & 3))) & 0xff);
-                h[e] = f32_to_bf16_bits(sl.d[j] * (float)q);
+                f[e] = (__bf16)__builtin_fmaf(d, (float)((word >> (8 * (e & 3))) & 0xffu), nb);
             }
-            const u32x4 pk = {(uint32_t)h[0] | ((uint32_t)h[1] << 16),
-                              (uint32_t)h[2] | ((uint32_t)h[3] << 16),
-                              (uint32_t)h[4] | ((uint32_t)h[5] << 16),
-                              (uint32_t)h[6] | ((uint32_t)h[7] << 16)};
-            f = __builtin_bit_cast(typename M::frag, pk);
         } else if constexpr (P::G == 1) {
             f = __builtin_bit_cast(typename M::frag, wv4);
         } else {
@@ -768,31 +770,55 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
         }
     }
 
-    // ---- epilogue: + bias in F32, one rounding, each lane stores its row's
-    // four runs of four channels (8 bytes in 16-bit dtypes, 16 in f32)
+    // ---- epilogue: + bias in F32, one rounding.  Each lane holds four runs
+    // of four consecutive channels of one row; they go to an LDS output
+    // tile (8-byte writes, 16 in f32), then whole rows leave with coalesced
+    // 16-byte stores.
+    constexpr int OPITCH = TN * ES + 8;  // bytes per output-tile row in LDS
+    constexpr int NPASS = TM * OPITCH <= 2 * STAGE * 16 ? 1 : 2;  // f32 tiles go in two halves
+    constexpr int RPP = TM / NPASS;      // tile rows per pass
+    static_assert(RPP * OPITCH <= 2 * STAGE * 16 && RPP % 32 == 0, "output tile fits the A stage");
+    constexpr int UPR = TN * ES / 16;    // 16-byte units per output row
+    char* ob = reinterpret_cast<char*>(Au);
     char* yb = static_cast<char*>(a.y);
 #pragma unroll
-    for (int i = 0; i < FM; ++i) {
-        const int32_t t = srow[wm * WTM + i * 32 + (lane & 31)];
+    for (int p = 0; p < NPASS; ++p) {
+        lds_barrier();  // every wave is done with the A stage / the previous pass
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
+        for (int i = 0; i < FM; ++i) {
+            const int rl = wm * WTM + i * 32 + (lane & 31);
+            if (wm * WTM + i * 32 < p * RPP || wm * WTM + i * 32 >= (p + 1) * RPP) continue;
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int col = co0 + wn * WTN + j * 32 + 8 * g + 4 * (lane >> 5);
-                float v[4];
+            for (int j = 0; j < FN; ++j) {
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    v[e] = acc[i][j][4 * g + e] + (a.bias ? M::ld(a.bias, col + e) : 0.0f);
-                if (t >= 0) {
-                    char* dst = yb + ((int64_t)t * a.cout + col) * ES;
+                for (int g = 0; g < 4; ++g) {
+                    const int cl = wn * WTN + j * 32 + 8 * g + 4 * (lane >> 5);
+                    float v[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * g + e] + sbias[cl + e];
+                    char* dst = ob + (rl - p * RPP) * OPITCH + cl * ES;
                     if constexpr (ES == 4) {
-                        *reinterpret_cast<floatx4*>(dst) = floatx4{v[0], v[1], v[2], v[3]};
+                        *reinterpret_cast<float2*>(dst) = float2{v[0], v[1]};
+                        *reinterpret_cast<float2*>(dst + 8) = float2{v[2], v[3]};
                     } else {
                         *reinterpret_cast<u32x2*>(dst) =
                             u32x2{(uint32_t)M::cvt(v[0]) | ((uint32_t)M::cvt(v[1]) << 16),
                                   (uint32_t)M::cvt(v[2]) | ((uint32_t)M::cvt(v[3]) << 16)};
                     }
                 }
+            }
+        }
+        lds_barrier();
+        for (int c = tid; c < RPP * UPR; c += NT) {
+            const int r = c / UPR;
+            const int q = c - r * UPR;
+            const int32_t t = srow[p * RPP + r];
+            if (t >= 0) {
+                const char* src = ob + r * OPITCH + q * 16;
+                const u32x2 lo = *reinterpret_cast<const u32x2*>(src);
+                const u32x2 hi = *reinterpret_cast<const u32x2*>(src + 8);
+                *reinterpret_cast<u32x4*>(yb + ((int64_t)t * a.cout + co0) * ES + q * 16) =
+                    u32x4{lo.x, lo.y, hi.x, hi.y};
             }
         }
     }
@@ -811,10 +837,15 @@ hipError_t launch_conv(hipStream_t s, ConvArgs a) {
 }
 
 // TN = largest of {128, 64, 32} dividing cout; 8 waves as 4x2 (64x64 wave
-// tiles), 4x2 (64x32) or 8x1 (32x32).
+// tiles), 4x2 (64x32) or 8x1 (32x32).  Q8_0 weights use 4 waves of 128x64:
+// each in-register dequantised B fragment then feeds four MFMAs instead of
+// two.
 template <typename T, bool Q8, bool PACKED, int NTAPS>
 hipError_t dispatch_tn(hipStream_t s, const ConvArgs& a) {
-    if (a.cout % 128 == 0) return launch_conv<T, Q8, PACKED, NTAPS, 128, 4, 2>(s, a);
+    if (a.cout % 128 == 0) {
+        if constexpr (Q8) return launch_conv<T, Q8, PACKED, NTAPS, 128, 2, 2>(s, a);
+        return launch_conv<T, Q8, PACKED, NTAPS, 128, 4, 2>(s, a);
+    }
     if (a.cout % 64 == 0) return launch_conv<T, Q8, PACKED, NTAPS, 64, 4, 2>(s, a);
     return launch_conv<T, Q8, PACKED, NTAPS, 32, 8, 1>(s, a);
 }
