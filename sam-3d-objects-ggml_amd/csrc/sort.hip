@@ -7,10 +7,11 @@
 // input order is token order, so (mask, token) comes out exactly as
 // std::stable_sort orders it.
 //
-// Per pass (8-bit digit, 256 bins):
+// Per pass (9-bit digit, 512 bins; 27-bit masks take 3 passes):
 //   upsweep   : per-tile digit histogram (tile = 256 threads x 8 keys)
-//   scan      : one workgroup turns the digit-major [256 x tiles] counts
-//               into exclusive global offsets
+//   offsets   : up to 128 tiles, every downsweep block derives its own
+//               offsets from the digit-major [512 x tiles] counts; beyond
+//               that one workgroup scans them first
 //   downsweep : per tile, stable rank of every key among equal digits via
 //               64-lane ballots (peer mask -> popcount of lower lanes), wave
 //               counts combined in LDS, scattered to offset + rank
@@ -28,15 +29,30 @@ thread_local char g_last_error[512] = "";
 constexpr int kRsThreads = 256;
 constexpr int kRsItems = 8;
 constexpr int kRsTile = kRsThreads * kRsItems;
-constexpr int kRsBins = 256;
+constexpr int kRsBits = 9;                 // digit bits: 27-bit masks sort in 3 passes
+constexpr int kRsBins = 1 << kRsBits;
 constexpr int kRsWaves = kRsThreads / 64;
+constexpr int kRsBinsPerThread = kRsBins / kRsThreads;
+constexpr int kRsFusedBlocks = 128;        // up to here each downsweep block scans the counts
 
+// Inclusive prefix sum across the 64 lanes of a wave.
+__device__ inline int32_t wave_incl_scan(int32_t v, int lane) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int32_t t = __shfl_up(v, off);
+        if (lane >= off) v += t;
+    }
+    return v;
+}
+
+// Per-tile digit histogram, digit-major: counts[d * nblocks + block].
 template <typename K>
 __global__ __launch_bounds__(kRsThreads) void rs_upsweep(const K* __restrict__ keys, int64_t n,
                                                          int shift, int32_t* __restrict__ counts,
                                                          int nblocks) {
     __shared__ int32_t hist[kRsBins];
-    hist[threadIdx.x] = 0;
+#pragma unroll
+    for (int j = 0; j < kRsBinsPerThread; ++j) hist[j * kRsThreads + threadIdx.x] = 0;
     __syncthreads();
     const int64_t base = (int64_t)blockIdx.x * kRsTile;
 #pragma unroll
@@ -48,25 +64,74 @@ __global__ __launch_bounds__(kRsThreads) void rs_upsweep(const K* __restrict__ k
         }
     }
     __syncthreads();
-    counts[(int64_t)threadIdx.x * nblocks + blockIdx.x] = hist[threadIdx.x];
+#pragma unroll
+    for (int j = 0; j < kRsBinsPerThread; ++j) {
+        const int d = j * kRsThreads + threadIdx.x;
+        counts[(int64_t)d * nblocks + blockIdx.x] = hist[d];
+    }
 }
 
-template <typename K>
+// Stable scatter of one tile.  `offsets` (digit-major, as the scan leaves
+// them) gives each (digit, block) its first output position; with
+// FUSED the block derives its own offsets from the raw counts instead:
+// offset(d) = (keys of smaller digits) + (keys of digit d in earlier
+// blocks).  Within the tile every key is ranked among equal digits by
+// 64-lane ballots (peer mask -> popcount of lower lanes), wave counts
+// combined in LDS, rounds in input order.
+template <typename K, bool FUSED>
 __global__ __launch_bounds__(kRsThreads) void rs_downsweep(
     const K* __restrict__ keys_in, const int32_t* __restrict__ vals_in, K* __restrict__ keys_out,
     int32_t* __restrict__ vals_out, int64_t n, int shift, const int32_t* __restrict__ offsets,
     int nblocks) {
     __shared__ int32_t wave_off[kRsWaves][kRsBins];
     __shared__ int32_t run[kRsBins];
+    __shared__ int32_t wsum[kRsWaves];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    run[tid] = offsets[(int64_t)tid * nblocks + blockIdx.x];
+    if constexpr (FUSED) {
+        // thread tid owns digits kRsBinsPerThread*tid .. +kRsBinsPerThread-1
+        int32_t tot[kRsBinsPerThread], before[kRsBinsPerThread];
+        int32_t mine = 0;
+#pragma unroll
+        for (int j = 0; j < kRsBinsPerThread; ++j) {
+            const int32_t* c = offsets + (int64_t)(kRsBinsPerThread * tid + j) * nblocks;
+            int32_t t = 0, bsum = 0;
+            for (int b = 0; b < nblocks; ++b) {
+                const int32_t v = c[b];
+                t += v;
+                if (b < (int)blockIdx.x) bsum += v;
+            }
+            tot[j] = t;
+            before[j] = bsum;
+            mine += t;
+        }
+        const int32_t incl = wave_incl_scan(mine, lane);
+        if (lane == 63) wsum[wave] = incl;
+        __syncthreads();
+        int32_t excl = incl - mine;
+#pragma unroll
+        for (int w = 0; w < kRsWaves; ++w)
+            if (w < wave) excl += wsum[w];
+#pragma unroll
+        for (int j = 0; j < kRsBinsPerThread; ++j) {
+            run[kRsBinsPerThread * tid + j] = excl + before[j];
+            excl += tot[j];
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < kRsBinsPerThread; ++j) {
+            const int d = j * kRsThreads + tid;
+            run[d] = offsets[(int64_t)d * nblocks + blockIdx.x];
+        }
+    }
     const int64_t base = (int64_t)blockIdx.x * kRsTile;
     const unsigned long long lower = (1ull << lane) - 1ull;
     for (int r = 0; r < kRsItems; ++r) {
 #pragma unroll
-        for (int w = 0; w < kRsWaves; ++w) wave_off[w][tid] = 0;
+        for (int w = 0; w < kRsWaves; ++w)
+#pragma unroll
+            for (int j = 0; j < kRsBinsPerThread; ++j) wave_off[w][j * kRsThreads + tid] = 0;
         __syncthreads();
         const int64_t i = base + r * kRsThreads + tid;
         const bool valid = i < n;
@@ -76,7 +141,7 @@ __global__ __launch_bounds__(kRsThreads) void rs_downsweep(
         // lanes of this wave holding the same digit
         unsigned long long peers = __ballot(valid);
 #pragma unroll
-        for (int b = 0; b < 8; ++b) {
+        for (int b = 0; b < kRsBits; ++b) {
             const bool bit = (d >> b) & 1u;
             const unsigned long long bal = __ballot(bit);
             peers &= bit ? bal : ~bal;
@@ -84,17 +149,19 @@ __global__ __launch_bounds__(kRsThreads) void rs_downsweep(
         const int rank = __popcll(peers & lower);
         if (valid && rank == 0) wave_off[wave][d] = __popcll(peers);
         __syncthreads();
-        {
-            // thread tid owns digit tid: wave counts -> offsets (global base +
-            // keys of this digit already placed by earlier rounds)
-            int32_t acc = run[tid];
+#pragma unroll
+        for (int j = 0; j < kRsBinsPerThread; ++j) {
+            // wave counts -> offsets (global base + keys of this digit already
+            // placed by earlier rounds)
+            const int dd = j * kRsThreads + tid;
+            int32_t acc = run[dd];
 #pragma unroll
             for (int w = 0; w < kRsWaves; ++w) {
-                const int32_t c = wave_off[w][tid];
-                wave_off[w][tid] = acc;
+                const int32_t c = wave_off[w][dd];
+                wave_off[w][dd] = acc;
                 acc += c;
             }
-            run[tid] = acc;
+            run[dd] = acc;
         }
         __syncthreads();
         if (valid) {
@@ -106,32 +173,46 @@ __global__ __launch_bounds__(kRsThreads) void rs_downsweep(
     }
 }
 
-// Exclusive scan of L int32 with one 1024-thread workgroup (contiguous
-// chunk per thread, Hillis-Steele across the chunk sums).  In-place safe.
+// Exclusive scan of len int32 with one 1024-thread workgroup: rounds of
+// 4096 elements (4 contiguous per thread), wave shuffles and one LDS step per
+// round, a running carry across rounds.  In-place safe.
 __global__ __launch_bounds__(1024) void scan_one_block(const int32_t* in, int32_t* out,
                                                        int32_t* total, int64_t len) {
-    __shared__ int32_t s[1024];
+    constexpr int IT = 4;
+    __shared__ int32_t wsum[16];
     const int tid = threadIdx.x;
-    const int64_t per = (len + 1023) / 1024;
-    const int64_t b = tid * per;
-    const int64_t e = b + per < len ? b + per : len;
-    int32_t sum = 0;
-    for (int64_t i = b; i < e; ++i) sum += in[i];
-    s[tid] = sum;
-    __syncthreads();
-    for (int off = 1; off < 1024; off <<= 1) {
-        const int32_t v = tid >= off ? s[tid - off] : 0;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    int32_t carry = 0;
+    for (int64_t base = 0; base < len; base += 1024 * IT) {
+        int32_t v[IT];
+        int32_t mine = 0;
+#pragma unroll
+        for (int j = 0; j < IT; ++j) {
+            const int64_t i = base + (int64_t)tid * IT + j;
+            v[j] = i < len ? in[i] : 0;
+            mine += v[j];
+        }
+        const int32_t incl = wave_incl_scan(mine, lane);
+        if (lane == 63) wsum[wave] = incl;
         __syncthreads();
-        s[tid] += v;
-        __syncthreads();
+        int32_t excl = carry + incl - mine;
+        int32_t round_total = 0;
+#pragma unroll
+        for (int w = 0; w < 16; ++w) {
+            if (w < wave) excl += wsum[w];
+            round_total += wsum[w];
+        }
+#pragma unroll
+        for (int j = 0; j < IT; ++j) {
+            const int64_t i = base + (int64_t)tid * IT + j;
+            if (i < len) out[i] = excl;
+            excl += v[j];
+        }
+        carry += round_total;
+        __syncthreads();  // wsum is rewritten by the next round
     }
-    int32_t acc = s[tid] - sum;
-    for (int64_t i = b; i < e; ++i) {
-        const int32_t v = in[i];
-        out[i] = acc;
-        acc += v;
-    }
-    if (tid == 1023 && total) *total = s[1023];
+    if (tid == 0 && total) *total = carry;
 }
 
 constexpr int kScanThreads = 256;
@@ -211,19 +292,25 @@ hipError_t radix_sort(hipStream_t s, const K* keys_in, const int32_t* vals_in, K
     K* tk[2] = {c.take<K>(n), c.take<K>(n)};
     int32_t* tv[2] = {c.take<int32_t>(n), c.take<int32_t>(n)};
     if (!c.ok) return hipErrorInvalidValue;
-    int passes = (end_bit + 7) / 8;
+    int passes = (end_bit + kRsBits - 1) / kRsBits;
     if (passes < 1) passes = 1;
+    const bool fused = nblocks <= kRsFusedBlocks;
     const K* kin = keys_in;
     const int32_t* vin = vals_in;
     for (int p = 0; p < passes; ++p) {
         const bool last = p == passes - 1;
         K* kout = last ? keys_out : tk[p & 1];
         int32_t* vout = last ? vals_out : tv[p & 1];
-        const int shift = p * 8;
+        const int shift = p * kRsBits;
         rs_upsweep<K><<<nblocks, kRsThreads, 0, s>>>(kin, n, shift, counts, nblocks);
-        scan_one_block<<<1, 1024, 0, s>>>(counts, counts, nullptr, (int64_t)kRsBins * nblocks);
-        rs_downsweep<K><<<nblocks, kRsThreads, 0, s>>>(kin, vin, kout, vout, n, shift, counts,
-                                                       nblocks);
+        if (fused) {
+            rs_downsweep<K, true><<<nblocks, kRsThreads, 0, s>>>(kin, vin, kout, vout, n, shift,
+                                                                 counts, nblocks);
+        } else {
+            scan_one_block<<<1, 1024, 0, s>>>(counts, counts, nullptr, (int64_t)kRsBins * nblocks);
+            rs_downsweep<K, false><<<nblocks, kRsThreads, 0, s>>>(kin, vin, kout, vout, n, shift,
+                                                                  counts, nblocks);
+        }
         kin = kout;
         vin = vout;
     }
