@@ -168,7 +168,7 @@ int spc_subdivide_map(spc_stream_t stream, const int32_t* coords, int64_t n, con
  *            (natural) order are fastest: the kernel deduplicates the
  *            gathered rows of each 256-row tile.
  *   bias     may be NULL
- * Requires ntaps 27, 8 or 1, cin % 32 == 0, cout % 32 == 0.  With ntaps 1
+ * Requires ntaps 27, 8 or 1, cin % 32 == 0, cout % 32 == 0, ntaps*cin*cout*4 < 2^31.  With ntaps 1
  * and idx NULL the map is the identity (n_in == n_out): the dense 1x1x1
  * conv y = x W^T + b of sparse_conv_1x1 (SRC/mesh_decoder_graph.cpp:349-384).
  * ------------------------------------------------------------------------ */

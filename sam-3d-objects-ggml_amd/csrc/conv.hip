@@ -153,9 +153,10 @@ __global__ void q8_0_dequant_kernel(const uint8_t* __restrict__ blocks, int64_t 
 
 int check_shape(const char* fn, int64_t ntaps, int64_t cin, int64_t cout) {
     if ((ntaps != 27 && ntaps != 8 && ntaps != 1) || cin <= 0 || cout <= 0 || cin % 32 != 0 ||
-        cout % 32 != 0 || cin > (1 << 16) || cout > (1 << 16)) {
+        cout % 32 != 0 || cin > (1 << 16) || cout > (1 << 16) ||
+        ntaps * cin * cout * 4 >= ((int64_t)1 << 31)) {
         set_last_error("%s: unsupported shape ntaps=%lld cin=%lld cout=%lld (ntaps 27, 8 or 1, "
-                       "cin and cout multiples of 32)",
+                       "cin and cout multiples of 32, ntaps*cin*cout*4 below 2^31 bytes)",
                        fn, (long long)ntaps, (long long)cin, (long long)cout);
         return SPC_BAD_SHAPE;
     }

@@ -137,17 +137,19 @@ struct Panel {
 };
 
 constexpr int kTM = 256;        // output rows per tile
-constexpr int kUMax = 1024;     // capacity of the deduplicated source-row stage
+constexpr int kUMax = 896;      // capacity of the deduplicated source-row stage
 constexpr int kWinWords = 1024; // dedupe bitmap: 32768 source rows
 constexpr int kSegs = 4;        // 16-byte segments per staged 64-byte row chunk
+constexpr int kPitch = 5;       // staged row pitch in 16-byte units (64 bytes + 16 of padding)
 
-// LDS position (in 16-byte units) of segment s of staged row r.  The XOR
-// swizzle puts one segment of 8 (and of 16) consecutive rows on distinct
-// banks, so a wave reading one k-slice of 32 nearly consecutive slots, and
-// the stage writes, run without bank conflicts.  slot_key(r) ^ s is the
-// same position, the form the slot table stores.
-__device__ __forceinline__ int slot_key(int r) { return r * kSegs + (((r >> 1) ^ (r >> 3)) & 3); }
-__device__ __forceinline__ int seg_pos(int r, int s) { return slot_key(r) ^ s; }
+// LDS position (in 16-byte units) of segment s of staged row r.  The 80-byte
+// pitch puts one segment of 8 (and of 16) consecutive rows on distinct banks,
+// so a wave reading one k-slice of 32 nearly consecutive slots, and the stage
+// writes, run without bank conflicts; the slot table stores slot_key(r), so
+// a fragment address is one multiply-add and the k-steps are immediate
+// offsets.
+__device__ __forceinline__ int slot_key(int r) { return r * kPitch; }
+__device__ __forceinline__ int seg_pos(int r, int s) { return r * kPitch + s; }
 
 constexpr int kTapWords = 8;  // step taps, four per word: up to 28 steps per chunk
 
@@ -389,7 +391,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
     constexpr int FM = WTM / 32;
     constexpr int FN = WTN / 32;
     constexpr int NQ = NTAPS * TM;
-    constexpr int STAGE = (kUMax + 1) * kSegs;  // 16-byte units per A buffer
+    constexpr int STAGE = (kUMax + 1) * kPitch;  // 16-byte units per A buffer
     constexpr int HALF = (STAGE + 1) / 2;
     constexpr int SPT = (HALF + NT - 1) / NT;   // staged units per thread per half
     static_assert(WM * WN == NW && FM >= 1 && FN >= 1, "wave geometry");
@@ -499,6 +501,12 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
         float d[Q8 ? FN : 1];
     };
 
+    // Packed weights through a buffer resource: the panel offset is a scalar,
+    // the lane offset a constant register, so a fragment load costs no vector
+    // address arithmetic (and reads past the packed size return zeros).
+    const uint32_t wbytes = (uint32_t)((int64_t)a.ntaps * a.cin * a.cout * P::WB);
+    const __amdgpu_buffer_rsrc_t wrsrc =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a.w), (short)0, (int)wbytes, 0x00020000);
     // B operands of (tap o, chunk kc) for this wave's FN column blocks
     auto load_b = [&](int o, int kc, Slot& sl) __attribute__((always_inline)) {
 #pragma unroll
@@ -506,11 +514,13 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
             const int c32 = (co0 + wn * WTN) / 32 + j;  // wave-uniform
             const int co = c32 * 32 + (lane & 31);
             if constexpr (PACKED) {
-                const int64_t panel = ((int64_t)o * kch + kc) * ncol32 + c32;
-                const char* pb = static_cast<const char*>(a.w) + panel * (P::NG * 1024);
+                const uint32_t panel = ((uint32_t)o * (uint32_t)kch + (uint32_t)kc) * (uint32_t)ncol32 +
+                                       (uint32_t)c32;
+                const int poff = (int)(panel * (uint32_t)(P::NG * 1024));
 #pragma unroll
                 for (int g = 0; g < P::NG; ++g)
-                    sl.q[j][g] = *reinterpret_cast<const u32x4*>(pb + g * 1024 + lane * 16);
+                    sl.q[j][g] = __builtin_bit_cast(
+                        u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrsrc, lane * 16 + g * 1024, poff, 0));
                 if constexpr (Q8)
                     sl.d[j] = static_cast<const float*>(a.wscale)[((int64_t)o * kch + kc) * a.cout + co];
             } else {
@@ -591,9 +601,8 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
         }
     };
     // A fragments of k-slices of 32 rows per FM block.  sl[] holds slot
-    // keys (fast tiles) or tile rows (fallback, turned into keys here); the
-    // segment and byte of each k-step within the 64-byte row are lane
-    // constants.
+    // keys (the row's first 16-byte unit); the byte of each k-step within
+    // the 64-byte row is a lane constant.
     auto read_frags = [&](int buf, const int* sl, AFrag& f) __attribute__((always_inline)) {
         const char* ab = reinterpret_cast<const char*>(Au + buf * STAGE);
 #pragma unroll
@@ -601,8 +610,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
             const int byte = (ks * M::KSUB + (lane >> 5) * M::EPL) * ES;  // within the 64-byte row
 #pragma unroll
             for (int i = 0; i < FM; ++i)
-                f[ks][i] = *reinterpret_cast<const typename M::frag*>(
-                    ab + (sl[i] ^ (byte >> 4)) * 16 + (byte & 15));
+                f[ks][i] = *reinterpret_cast<const typename M::frag*>(ab + sl[i] * 16 + byte);
         }
     };
     // union slots of the wave's rows for sidx row `row` (a tap, or NTAPS = zeros)
@@ -670,9 +678,15 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
         Slot ring[PD];
         AFrag afr[2];
         int sreg[2][FM];
+        // the tap words in scalar registers: tw0 holds the running group's
+        // word, the rest shift down one word per group; tw_first restores
+        // them at every chunk start
+        uint32_t tw_first[kTapWords], tw[kTapWords];
+#pragma unroll
+        for (int w = 0; w < kTapWords; ++w) tw_first[w] = __builtin_amdgcn_readfirstlane(tlw[w]);
 
         {
-            const uint32_t w0 = tlw[0];
+            const uint32_t w0 = tw_first[0];
 #pragma unroll
             for (int p = 0; p < PD; ++p) load_b(b_tap(w0, p), 0, ring[p]);
             read_slots(s_row(w0, 0), sreg[0]);
@@ -694,10 +708,12 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
                 if (kc + 1 < kch) stage_issue(kc + 1, 0);
                 read_frags(buf, sreg[0], afr[0]);
             }
+#pragma unroll
+            for (int w = 0; w < kTapWords; ++w) tw[w] = tw_first[w];
             for (int g = 0; g < ngr; ++g) {
                 const bool last_g = g + 1 == ngr;
-                const uint32_t w0 = tlw[g];
-                const uint32_t w1 = tlw[last_g ? 0 : g + 1];
+                const uint32_t w0 = tw[0];
+                const uint32_t w1 = last_g ? tw_first[0] : tw[1];
                 const int kc_next = last_g ? kc + 1 : kc;  // chunk of the steps PD ahead
                 const int kc_b = min(kc_next, kch - 1);  // past the last chunk: a valid, unused panel
                 auto step = [&](auto u_const) __attribute__((always_inline)) {
@@ -732,6 +748,8 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
                     stage_commit(buf ^ 1, 0);
                     stage_issue(kc + 1, 1);
                 }
+#pragma unroll
+                for (int w = 0; w + 1 < kTapWords; ++w) tw[w] = tw[w + 1];
             }
         }
     } else if (nt > 0) {
