@@ -49,6 +49,50 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// s_waitcnt on the vector-memory counter alone (gfx9 encoding: vmcnt in bits
+// [3:0] and [15:14]; expcnt [6:4] and lgkmcnt [11:8] at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// One LDS-DMA load (gfx950 buffer_load_dwordx4 ... lds): lane l's 16 bytes
+// at buffer offset voff + soff go to LDS byte address lds_addr + 16 l; an
+// out-of-range offset writes zeros.  Issued from inline assembly so that the
+// compiler's wait-count tracking does not make every later LDS read wait
+// for it; callers wait for completion themselves (dma_barrier).  M0 needs
+// one wait state before the load.
+// The scalar operands pass through readfirstlane so that they are in SGPRs
+// at the asm (they must be wave-uniform).
+__device__ __forceinline__ void lds_dma_x4(u32x4 rsrc, uint32_t lds_addr, uint32_t voff, uint32_t soff) {
+    const u32x4 rs = {(uint32_t)__builtin_amdgcn_readfirstlane(rsrc.x),
+                      (uint32_t)__builtin_amdgcn_readfirstlane(rsrc.y),
+                      (uint32_t)__builtin_amdgcn_readfirstlane(rsrc.z),
+                      (uint32_t)__builtin_amdgcn_readfirstlane(rsrc.w)};
+    const uint32_t m0v = (uint32_t)__builtin_amdgcn_readfirstlane(lds_addr);
+    const uint32_t so = (uint32_t)__builtin_amdgcn_readfirstlane(soff);
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :
+                 : "s"(m0v), "v"(voff), "s"(rs), "s"(so)
+                 : "memory", "m0");
+}
+
+// Workgroup barrier for LDS filled by LDS-DMA loads: waits until at most N
+// of this wave's vector-memory loads are outstanding (the DMA loads are
+// older than the last N) and its LDS operations are done, then s_barrier.
+// No memory fence: a release fence on LDS would also wait for the N younger
+// loads, weight prefetches meant to cross the barrier.  The signal fences
+// keep the compiler from moving memory accesses across it.
+template <int N>
+__device__ __forceinline__ void dma_barrier() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    wait_vmcnt<N>();
+    __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // Round-to-nearest-even float -> bf16 / f16 bits (device), from the formats'
 // definitions; NaN payloads are quieted.
 __device__ inline uint16_t f32_to_bf16_bits(float f) {

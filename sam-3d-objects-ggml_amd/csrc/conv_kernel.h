@@ -137,10 +137,15 @@ struct Panel {
 };
 
 constexpr int kTM = 256;        // output rows per tile
-constexpr int kUMax = 896;      // capacity of the deduplicated source-row stage
+constexpr int kUMax = 895;      // capacity of the deduplicated source-row stage
+constexpr int kURowCap = (kUMax + 3) / 4 * 4;  // union-row table entries (16-byte multiple)
 constexpr int kWinWords = 1024; // dedupe bitmap: 32768 source rows
 constexpr int kSegs = 4;        // 16-byte segments per staged 64-byte row chunk
 constexpr int kPitch = 5;       // staged row pitch in 16-byte units (64 bytes + 16 of padding)
+// 16-byte units per A stage buffer: whole 64-unit blocks (one LDS-DMA
+// instruction each) holding the kUMax union rows and the zero row
+constexpr int kStageUnits = ((kUMax + 1) * kPitch + 63) / 64 * 64;
+static_assert(kStageUnits == 4480, "stage geometry");
 
 // LDS position (in 16-byte units) of segment s of staged row r.  The 80-byte
 // pitch puts one segment of 8 (and of 16) consecutive rows on distinct banks,
@@ -157,11 +162,11 @@ constexpr int kTapWords = 8;  // step taps, four per word: up to 28 steps per ch
 // output rows, union rows, slot keys.  The plan depends only on the index
 // table, its layout, the row order and NTAPS -- not on channels or weights.
 __host__ __device__ constexpr int64_t plan_tile_bytes(int ntaps) {
-    return (64 + 4 * kTM + 4 * kUMax + 2 * (int64_t)(ntaps + 1) * kTM + 255) / 256 * 256;
+    return (64 + 4 * kTM + 4 * kURowCap + 2 * (int64_t)(ntaps + 1) * kTM + 255) / 256 * 256;
 }
 constexpr int kPlanSrow = 64;
 constexpr int kPlanUrow = kPlanSrow + 4 * kTM;
-constexpr int kPlanSidx = kPlanUrow + 4 * kUMax;
+constexpr int kPlanSidx = kPlanUrow + 4 * kURowCap;
 
 // Shared-memory arrays of one tile's setup.
 struct TileLds {
@@ -356,7 +361,7 @@ __global__ __launch_bounds__(512) void conv_plan_kernel(ConvArgs a, char* plan) 
     __shared__ uint32_t scratch[2 * kWinWords];
     __shared__ __attribute__((aligned(16))) uint16_t sidx[(NTAPS + 1) * kTM];
     __shared__ __attribute__((aligned(16))) uint32_t tlw[kTapWords];
-    __shared__ __attribute__((aligned(16))) int32_t urow[kUMax];
+    __shared__ __attribute__((aligned(16))) int32_t urow[kURowCap];
     __shared__ __attribute__((aligned(16))) int32_t srow[kTM];
     __shared__ int32_t wsum[8];
     __shared__ int32_t misc[8];
@@ -377,13 +382,19 @@ __global__ __launch_bounds__(512) void conv_plan_kernel(ConvArgs a, char* plan) 
     }
 }
 
-template <typename T, bool Q8, bool PACKED, int NTAPS, int TN, int WM, int WN, int PD>
-__global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
+template <typename T, bool Q8, bool PACKED, int NTAPS, int TN, int WM, int WN, int KSP, int PD>
+__global__ __launch_bounds__(WM * WN * KSP * 64, 1) void conv_kernel(ConvArgs a) {
     using M = Mfma<T>;
     using P = Panel<T, Q8>;
     constexpr int TM = kTM;
-    constexpr int NW = WM * WN;
+    constexpr int NW = WM * WN * KSP;
     constexpr int NT = NW * 64;
+    // KSP = 2 splits each chunk's MFMA k-steps between the two waves of a
+    // pair that own the same output block: every weight fragment is then
+    // fetched by WM waves instead of 2 * WM, and the pair's partial sums are
+    // added through LDS before the store.
+    constexpr int KSW = P::KS / KSP;   // k-steps per wave per step
+    constexpr int NGW = P::NG / KSP;   // 16-byte weight words per lane per wave
     constexpr int ES = sizeof(T);
     constexpr int KC = P::KC;
     constexpr int WTM = TM / WM;
@@ -391,20 +402,19 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
     constexpr int FM = WTM / 32;
     constexpr int FN = WTN / 32;
     constexpr int NQ = NTAPS * TM;
-    constexpr int STAGE = (kUMax + 1) * kPitch;  // 16-byte units per A buffer
-    constexpr int HALF = (STAGE + 1) / 2;
-    constexpr int SPT = (HALF + NT - 1) / NT;   // staged units per thread per half
-    static_assert(WM * WN == NW && FM >= 1 && FN >= 1, "wave geometry");
+    constexpr int STAGE = kStageUnits;          // 16-byte units per A buffer
+    constexpr int NPART = 4;                    // parts of a chunk's staging
+    static_assert(FM >= 1 && FN >= 1, "wave geometry");
+    static_assert(KSP == 1 || (KSP == 2 && KSW % P::G == 0 && FM % 2 == 0), "k-split geometry");
     static_assert(!Q8 || ES == 2, "Q8_0 weights feed 16-bit MFMA operands");
     static_assert(NTAPS <= 32, "tap mask is 32-bit");
-    static_assert(SPT <= 32, "stage geometry");
     static_assert(2 * kWinWords * 4 <= STAGE * 16, "bitmap aliases the A stage");
     static_assert(PD == 4, "the step groups pack four taps per word");
 
     __shared__ u32x4 Au[2 * STAGE];    // two A buffers: (U + 1) rows x 64 bytes each
     __shared__ __attribute__((aligned(16))) uint16_t sidx[NQ + TM];  // slot keys; row NTAPS = zeros
     __shared__ __attribute__((aligned(16))) uint32_t tlw[kTapWords]; // step taps, 4 per word
-    __shared__ __attribute__((aligned(16))) int32_t urow[kUMax];     // source row of each union slot
+    __shared__ __attribute__((aligned(16))) int32_t urow[kURowCap];  // source row of each union slot
     __shared__ __attribute__((aligned(16))) int32_t srow[TM];        // output row of each tile row
     __shared__ int32_t wsum[NW];
     __shared__ int32_t misc[8];
@@ -466,6 +476,10 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
         U = misc[3];
         fast = misc[4] != 0;
     }
+    // tile-uniform values: keep them (and the control flow they drive) scalar
+    U = __builtin_amdgcn_readfirstlane(U);
+    tile_mask = (uint32_t)__builtin_amdgcn_readfirstlane(tile_mask);
+    fast = __builtin_amdgcn_readfirstlane((int)fast) != 0;
 
     // source row of (tap o, tile row r), -1 when missing (fallback tiles)
     auto src_of = [&](int o, int r) __attribute__((always_inline)) -> int32_t {
@@ -482,8 +496,9 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
     const int kch = a.cin / KC;
     const int ncol32 = a.cout / 32;
 
-    const int wm = wave / WN;
-    const int wn = wave % WN;
+    const int kh = wave % KSP;          // k-half of the wave (0 without a split)
+    const int wm = wave / KSP / WN;
+    const int wn = wave / KSP % WN;
 
     floatx16 acc[FM][FN];
 #pragma unroll
@@ -497,7 +512,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
     const u32x4 zero4 = {0u, 0u, 0u, 0u};
 
     struct Slot {
-        u32x4 q[FN][P::NG];
+        u32x4 q[FN][NGW];
         float d[Q8 ? FN : 1];
     };
 
@@ -516,9 +531,9 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
             if constexpr (PACKED) {
                 const uint32_t panel = ((uint32_t)o * (uint32_t)kch + (uint32_t)kc) * (uint32_t)ncol32 +
                                        (uint32_t)c32;
-                const int poff = (int)(panel * (uint32_t)(P::NG * 1024));
+                const int poff = (int)(panel * (uint32_t)(P::NG * 1024)) + kh * (NGW * 1024);
 #pragma unroll
-                for (int g = 0; g < P::NG; ++g)
+                for (int g = 0; g < NGW; ++g)
                     sl.q[j][g] = __builtin_bit_cast(
                         u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrsrc, lane * 16 + g * 1024, poff, 0));
                 if constexpr (Q8)
@@ -526,10 +541,11 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
             } else {
                 const int64_t rowbase = ((int64_t)co * NTAPS + o) * a.cin + (int64_t)kc * KC;
 #pragma unroll
-                for (int g = 0; g < P::NG; ++g) {
+                for (int gg = 0; gg < NGW; ++gg) {
+                    const int g = kh * NGW + gg;
                     if constexpr (P::G == 1) {
                         const int64_t el = rowbase + g * P::KSUB + (lane >> 5) * P::EPL;
-                        sl.q[j][g] = *reinterpret_cast<const u32x4*>(
+                        sl.q[j][gg] = *reinterpret_cast<const u32x4*>(
                             static_cast<const char*>(a.w) + el * P::WB);
                     } else {
                         uint32_t words[4];
@@ -543,7 +559,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
 #pragma unroll
                             for (int h = 0; h < WPK; ++h) words[i * WPK + h] = wp[h];
                         }
-                        sl.q[j][g] = u32x4{words[0], words[1], words[2], words[3]};
+                        sl.q[j][gg] = u32x4{words[0], words[1], words[2], words[3]};
                     }
                 }
                 if constexpr (Q8)
@@ -552,7 +568,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
         }
     };
 
-    // B fragment of k-step ks from a loaded slot
+    // B fragment of the wave's k-step ks (0 .. KSW-1) from a loaded slot
     auto b_frag = [&](const Slot& sl, int j, int ks) __attribute__((always_inline)) {
         typename M::frag f;
         const u32x4 wv4 = sl.q[j][ks / P::G];
@@ -583,7 +599,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
         return f;
     };
 
-    typedef typename M::frag AFrag[P::KS][FM];
+    typedef typename M::frag AFrag[KSW][FM];
     // The MFMA computes the transposed block (weights as the 32-row operand,
     // gathered features as the 32-column one): the accumulator of lane l then
     // holds output row l%32 and output channels 8*(k/4) + 4*(l/32) + k%4 for
@@ -591,7 +607,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
     // straight to global memory.
     auto mma_step = [&](const AFrag& af, const Slot& bs) __attribute__((always_inline)) {
 #pragma unroll
-        for (int ks = 0; ks < P::KS; ++ks) {
+        for (int ks = 0; ks < KSW; ++ks) {
 #pragma unroll
             for (int j = 0; j < FN; ++j) {
                 const typename M::frag bf = b_frag(bs, j, ks);
@@ -604,9 +620,9 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
     // keys (the row's first 16-byte unit); the byte of each k-step within
     // the 64-byte row is a lane constant.
     auto read_frags = [&](int buf, const int* sl, AFrag& f) __attribute__((always_inline)) {
-        const char* ab = reinterpret_cast<const char*>(Au + buf * STAGE);
+        const char* ab = reinterpret_cast<const char*>(Au + buf * STAGE) + kh * (KSW * M::KSUB * ES);
 #pragma unroll
-        for (int ks = 0; ks < P::KS; ++ks) {
+        for (int ks = 0; ks < KSW; ++ks) {
             const int byte = (ks * M::KSUB + (lane >> 5) * M::EPL) * ES;  // within the 64-byte row
 #pragma unroll
             for (int i = 0; i < FM; ++i)
@@ -619,41 +635,49 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
         for (int i = 0; i < FM; ++i) sl[i] = sidx[row * TM + wm * WTM + i * 32 + (lane & 31)];
     };
 
-    if (fast && nt > 0) {
-        // ---- A staging: half h of chunk kc's union rows ------------------
-        // Units u = slot * 4 + segment of the (U + 1) staged rows; half h
-        // covers [h * hu, min(total, (h + 1) * hu)).  Loads go to registers
-        // half a chunk ahead of their use; slot U and units past the end are
-        // zeros.  The commit writes them to the chunk's LDS buffer.
-        const int total_u = (U + 1) * kSegs;
-        const int hu = (total_u + 1) / 2;
-        u32x4 stg[SPT];
-        uint32_t stg_zero = 0;
-        auto stage_issue = [&](int kc, int h) __attribute__((always_inline)) {
-            const int beg = h * hu;
-            const int end = min(total_u, beg + hu);
-            const int64_t koff = (int64_t)kc * KC * ES;
-            stg_zero = 0;
-#pragma unroll
-            for (int j = 0; j < SPT; ++j) {
-                const int u = beg + j * NT + tid;
-                const int slot = u >> 2;
-                const int32_t row = (u < end && slot < U) ? urow[slot] : -1;
-                if (row < 0) stg_zero |= 1u << j;
-                const int64_t rr = row >= 0 ? row : 0;
-                stg[j] = *reinterpret_cast<const u32x4*>(xb + rr * a.cin * ES + koff + (u & 3) * 16);
+    // The fast path stages through LDS DMA with 32-bit offsets from the
+    // tile's lowest source row.
+    const int64_t rowbytes = (int64_t)a.cin * ES;
+    const bool dma = fast && nt > 0 && U > 0 && U <= kUMax &&
+                     (int64_t)(urow[U - 1] - urow[0] + 1) * rowbytes <= 0x7fffffffLL;
+
+    if (dma) {
+        // ---- A staging through LDS DMA -----------------------------------
+        // A chunk's stage is U + 1 rows at an 80-byte pitch, in 64-unit
+        // blocks of 16 bytes; one buffer_load_dwordx4 ... lds fills a block
+        // (lane l -> unit 64 * block + l).  Unit 5 r + s holds segment s of
+        // union row r; padding units (s = 4), the zero row U and units past
+        // it read out of range, which writes zeros.  The next chunk's blocks
+        // are issued in NPART parts at the starts of the first step groups;
+        // they land in the free buffer while the MFMAs run and are waited
+        // for once, before the chunk barrier.
+        const int32_t row0 = __builtin_amdgcn_readfirstlane(urow[0]);
+        const uint32_t nrec = (uint32_t)min<int64_t>((a.n_in - row0) * rowbytes, 0x7fffffffLL);
+        const uint64_t xbase = reinterpret_cast<uint64_t>(xb + (int64_t)row0 * rowbytes);
+        // buffer descriptor: base, stride 0, num_records, raw-buffer flags
+        const u32x4 xrsrc = {(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)xbase),
+                             (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(xbase >> 32) & 0xffffu),
+                             (uint32_t)__builtin_amdgcn_readfirstlane(nrec), 0x00020000u};
+        const uint32_t au_lds = __builtin_amdgcn_readfirstlane(
+            (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) u32x4*)Au));
+        const int nblk = ((U + 1) * kPitch + 63) / 64;
+        const int bpp = (nblk + NPART - 1) / NPART;  // blocks per part
+        auto stage_part = [&](int kc, int buf, int h) __attribute__((always_inline)) {
+            const int koff = kc * KC * ES;
+            const int bend = min(nblk, (h + 1) * bpp);
+            for (int blk = h * bpp + wave; blk < bend; blk += NW) {
+                const int v = blk * 64 + lane;
+                const int r = v / kPitch;
+                const int sg = v - r * kPitch;
+                uint32_t off = 0x80000000u;  // out of range: zeros
+                if (sg < kSegs && r < U)
+                    off = (uint32_t)(urow[r] - row0) * (uint32_t)rowbytes + (uint32_t)(sg * 16);
+                lds_dma_x4(xrsrc, au_lds + (uint32_t)((buf * STAGE + blk * 64) * 16), off,
+                           __builtin_amdgcn_readfirstlane((uint32_t)koff));
             }
         };
-        auto stage_commit = [&](int buf, int h) __attribute__((always_inline)) {
-            const int beg = h * hu;
-            const int end = min(total_u, beg + hu);
-            u32x4* dst = Au + buf * STAGE;
-#pragma unroll
-            for (int j = 0; j < SPT; ++j) {
-                const int u = beg + j * NT + tid;
-                if (u < end) dst[seg_pos(u >> 2, u & 3)] = ((stg_zero >> j) & 1u) ? zero4 : stg[j];
-            }
-        };
+        // vector-memory loads per step (weight words, plus Q8_0 scales)
+        constexpr int LPS = PACKED ? FN * NGW + (Q8 ? FN : 0) : 0;
 
         // Steps of a chunk: the active taps in ascending order, padded to a
         // multiple of PD with steps that read the zero slot (row NTAPS)
@@ -664,7 +688,6 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
         // union slots in sreg[i % 2] (read two steps ahead; slots do not
         // depend on the chunk, so they run ahead across chunk boundaries).
         const int ngr = (nt + PD - 1) / PD;
-        const int gmid = ngr / 2;
         const int tfirst = __ffs(tile_mask) - 1;
         auto b_tap = [&](uint32_t word, int b) __attribute__((always_inline)) -> int {
             const int t = (int)((word >> (8 * b)) & 0xffu);
@@ -691,31 +714,35 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
             for (int p = 0; p < PD; ++p) load_b(b_tap(w0, p), 0, ring[p]);
             read_slots(s_row(w0, 0), sreg[0]);
             read_slots(s_row(w0, 1), sreg[1]);
-            stage_issue(0, 0);
-            stage_commit(0, 0);
-            stage_issue(0, 1);
-            stage_commit(0, 1);
-            lds_barrier();
-            if (kch > 1) stage_issue(1, 0);
+            for (int h = 0; h < NPART; ++h) stage_part(0, 0, h);
+            dma_barrier<0>();
             read_frags(0, sreg[0], afr[0]);
         }
 
         for (int kc = 0; kc < kch; ++kc) {
             const int buf = kc & 1;
+            const bool more = kc + 1 < kch;
             if (kc > 0) {
-                stage_commit(buf, 1);  // second half of this chunk
-                lds_barrier();         // chunk complete; every wave done with the other buffer
-                if (kc + 1 < kch) stage_issue(kc + 1, 0);
+                // chunk staged; every wave done with the other buffer.  With
+                // ngr >= NPART the last part preceded a whole group's loads.
+                if (ngr >= NPART && LPS > 0) dma_barrier<PD * LPS>();
+                else dma_barrier<0>();
                 read_frags(buf, sreg[0], afr[0]);
             }
 #pragma unroll
             for (int w = 0; w < kTapWords; ++w) tw[w] = tw_first[w];
-            for (int g = 0; g < ngr; ++g) {
-                const bool last_g = g + 1 == ngr;
+            // The last group of a chunk is peeled: its steps past the chunk's
+            // taps (padding) skip their MFMAs but keep their loads, so every
+            // step issues the same number of weight loads.
+            const int nreal = nt - PD * (ngr - 1);  // real steps of the last group
+            auto run_group = [&](int g, auto last_const) __attribute__((always_inline)) {
+                constexpr bool last_g = decltype(last_const)::value;
                 const uint32_t w0 = tw[0];
                 const uint32_t w1 = last_g ? tw_first[0] : tw[1];
                 const int kc_next = last_g ? kc + 1 : kc;  // chunk of the steps PD ahead
                 const int kc_b = min(kc_next, kch - 1);  // past the last chunk: a valid, unused panel
+                if (more && g < NPART) stage_part(kc + 1, buf ^ 1, g);
+                __builtin_amdgcn_sched_barrier(0);  // the part's loads precede the group's
                 auto step = [&](auto u_const) __attribute__((always_inline)) {
                     constexpr int u = decltype(u_const)::value;
                     // slots of the step after next (they do not depend on the chunk)
@@ -723,14 +750,18 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
                     // A fragments of the next step; after a chunk's last step they
                     // are re-read behind the barrier, so this read is unused
                     read_frags(buf, sreg[(u + 1) & 1], afr[(u + 1) & 1]);
-                    mma_step(afr[u & 1], ring[u]);
+                    if constexpr (last_g && u > 0) {
+                        if (u < nreal) mma_step(afr[u & 1], ring[u]);
+                    } else {
+                        mma_step(afr[u & 1], ring[u]);
+                    }
                     // weights of the step PD ahead
                     load_b(b_tap(w1, u), kc_b, ring[u]);
                     // issue order: slot reads, then MFMAs interleaved with the
                     // fragment reads and their address arithmetic, then the
                     // weight loads
-                    constexpr int NMF = P::KS * FM * FN;
-                    constexpr int NFR = P::KS * FM;
+                    constexpr int NMF = KSW * FM * FN;
+                    constexpr int NFR = KSW * FM;
                     __builtin_amdgcn_sched_group_barrier(0x100, FM, 0);
 #pragma unroll
                     for (int q = 0; q < NMF; ++q) {
@@ -738,19 +769,23 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
                         if (q < NFR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
                         __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
                     }
-                    __builtin_amdgcn_sched_group_barrier(0x020, FN * P::NG, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x020, FN * NGW, 0);
+                    // nothing crosses a step boundary: without this fence the
+                    // scheduler sinks every weight load of the group to its
+                    // end, which leaves the next group's first steps waiting
+                    __builtin_amdgcn_sched_barrier(0);
                 };
                 step(std::integral_constant<int, 0>{});
                 step(std::integral_constant<int, 1>{});
                 step(std::integral_constant<int, 2>{});
                 step(std::integral_constant<int, 3>{});
-                if (g == gmid && kc + 1 < kch) {
-                    stage_commit(buf ^ 1, 0);
-                    stage_issue(kc + 1, 1);
-                }
 #pragma unroll
                 for (int w = 0; w + 1 < kTapWords; ++w) tw[w] = tw[w + 1];
-            }
+            };
+            for (int g = 0; g + 1 < ngr; ++g) run_group(g, std::false_type{});
+            run_group(ngr - 1, std::true_type{});
+            if (more)  // short chunks: the parts the group loop did not reach
+                for (int h = ngr; h < NPART; ++h) stage_part(kc + 1, buf ^ 1, h);
         }
     } else if (nt > 0) {
         // Fallback (the union does not fit the stage): each tap's 256 source
@@ -788,6 +823,47 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
         }
     }
 
+    // ---- k-split: the pair's partial sums meet in LDS.  Wave kh keeps the
+    // row blocks [kh * FM/2, (kh + 1) * FM/2) and hands the other half to
+    // its partner (wave ^ 1), which adds it to its own.
+    if constexpr (KSP == 2) {
+        constexpr int HB = FM / 2;
+        constexpr int NV = HB * FN * 4;  // 16-byte values per lane handed over
+        static_assert(NW * NV * 64 <= 2 * STAGE, "the exchange fits the A stage");
+        floatx4* xs = reinterpret_cast<floatx4*>(Au);
+        auto put = [&](auto b0_const) __attribute__((always_inline)) {
+            constexpr int B0 = decltype(b0_const)::value;
+#pragma unroll
+            for (int ii = 0; ii < HB; ++ii)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        xs[(wave * NV + (ii * FN + j) * 4 + q) * 64 + lane] =
+                            floatx4{acc[B0 + ii][j][4 * q], acc[B0 + ii][j][4 * q + 1],
+                                    acc[B0 + ii][j][4 * q + 2], acc[B0 + ii][j][4 * q + 3]};
+        };
+        auto take = [&](auto b0_const) __attribute__((always_inline)) {
+            constexpr int B0 = decltype(b0_const)::value;
+#pragma unroll
+            for (int ii = 0; ii < HB; ++ii)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const floatx4 v = xs[((wave ^ 1) * NV + (ii * FN + j) * 4 + q) * 64 + lane];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) acc[B0 + ii][j][4 * q + e] += v[e];
+                    }
+        };
+        lds_barrier();  // every wave is done with the A stage
+        if (kh == 0) put(std::integral_constant<int, HB>{});
+        else put(std::integral_constant<int, 0>{});
+        lds_barrier();
+        if (kh == 0) take(std::integral_constant<int, 0>{});
+        else take(std::integral_constant<int, HB>{});
+    }
+
     // ---- epilogue: + bias in F32, one rounding.  Each lane holds four runs
     // of four consecutive channels of one row; they go to an LDS output
     // tile (8-byte writes, 16 in f32), then whole rows leave with coalesced
@@ -804,6 +880,9 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
         lds_barrier();  // every wave is done with the A stage / the previous pass
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
+            if constexpr (KSP == 2) {
+                if ((i >= FM / 2) != (kh == 1)) continue;  // the partner stores this block
+            }
             const int rl = wm * WTM + i * 32 + (lane & 31);
             if (wm * WTM + i * 32 < p * RPP || wm * WTM + i * 32 >= (p + 1) * RPP) continue;
 #pragma unroll
@@ -842,7 +921,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
     }
 }
 
-template <typename T, bool Q8, bool PACKED, int NTAPS, int TN, int WM, int WN>
+template <typename T, bool Q8, bool PACKED, int NTAPS, int TN, int WM, int WN, int KSP>
 hipError_t launch_conv(hipStream_t s, ConvArgs a) {
     const int64_t tiles_m = ceil_div(a.n_out, kTM);
     a.tiles_n = a.cout / TN;
@@ -850,22 +929,24 @@ hipError_t launch_conv(hipStream_t s, ConvArgs a) {
     a.tiles_per_xcd = ceil_div(a.total_tiles, 8);
     const int64_t grid = a.tiles_per_xcd * 8;
     if (grid == 0) return hipSuccess;
-    conv_kernel<T, Q8, PACKED, NTAPS, TN, WM, WN, 4><<<(unsigned)grid, WM * WN * 64, 0, s>>>(a);
+    conv_kernel<T, Q8, PACKED, NTAPS, TN, WM, WN, KSP, 4><<<(unsigned)grid, WM * WN * KSP * 64, 0, s>>>(a);
     return hipGetLastError();
 }
 
-// TN = largest of {128, 64, 32} dividing cout; 8 waves as 4x2 (64x64 wave
-// tiles), 4x2 (64x32) or 8x1 (32x32).  Q8_0 weights use 4 waves of 128x64:
-// each in-register dequantised B fragment then feeds four MFMAs instead of
-// two.
+// TN = largest of {128, 64, 32} dividing cout.  16-bit activations with
+// TN = 128 run 8 waves as 2x2 blocks of 128x64 with the chunk's k-steps
+// split between the two waves of a block (half the weight-fragment traffic
+// of 4x2 blocks of 64x64); fp32 runs 4x2 (64x64); TN = 64 4x2 (64x32);
+// TN = 32 8x1 (32x32).  Q8_0 weights use 4 waves of 128x64: each
+// in-register dequantised B fragment then feeds four MFMAs instead of two.
 template <typename T, bool Q8, bool PACKED, int NTAPS>
 hipError_t dispatch_tn(hipStream_t s, const ConvArgs& a) {
     if (a.cout % 128 == 0) {
-        if constexpr (Q8) return launch_conv<T, Q8, PACKED, NTAPS, 128, 2, 2>(s, a);
-        return launch_conv<T, Q8, PACKED, NTAPS, 128, 4, 2>(s, a);
+        if constexpr (Q8) return launch_conv<T, Q8, PACKED, NTAPS, 128, 2, 2, 1>(s, a);
+        else return launch_conv<T, Q8, PACKED, NTAPS, 128, 4, 2, 1>(s, a);
     }
-    if (a.cout % 64 == 0) return launch_conv<T, Q8, PACKED, NTAPS, 64, 4, 2>(s, a);
-    return launch_conv<T, Q8, PACKED, NTAPS, 32, 8, 1>(s, a);
+    if (a.cout % 64 == 0) return launch_conv<T, Q8, PACKED, NTAPS, 64, 4, 2, 1>(s, a);
+    return launch_conv<T, Q8, PACKED, NTAPS, 32, 8, 1, 1>(s, a);
 }
 
 template <typename T, bool Q8>
