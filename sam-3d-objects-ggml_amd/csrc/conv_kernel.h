@@ -24,10 +24,10 @@
 //   K loop  channels are consumed in 64-byte chunks.  A chunk's union rows
 //           live in one of two LDS buffers (slot U = zeros for missing
 //           taps); while the waves run the MFMAs of chunk kc over all active
-//           taps, the next chunk is fetched in two halves into registers
-//           and written to the other buffer, so one barrier per chunk is
-//           the only synchronisation.  B fragments come straight from
-//           global memory (weights prepacked in MFMA fragment order -- one
+//           taps, LDS-DMA loads (buffer_load_dwordx4 ... lds) fill the other
+//           buffer with the next chunk, so one barrier per chunk is the
+//           only synchronisation.  B fragments come straight from global
+//           memory (weights prepacked in MFMA fragment order -- one
 //           contiguous 1 KB load per fragment, L2-resident) through a
 //           register ring PD steps deep; A fragments and their slots are
 //           read from LDS one and two steps ahead.
@@ -382,19 +382,13 @@ __global__ __launch_bounds__(512) void conv_plan_kernel(ConvArgs a, char* plan) 
     }
 }
 
-template <typename T, bool Q8, bool PACKED, int NTAPS, int TN, int WM, int WN, int KSP, int PD>
-__global__ __launch_bounds__(WM * WN * KSP * 64, 1) void conv_kernel(ConvArgs a) {
+template <typename T, bool Q8, bool PACKED, int NTAPS, int TN, int WM, int WN, int PD>
+__global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
     using M = Mfma<T>;
     using P = Panel<T, Q8>;
     constexpr int TM = kTM;
-    constexpr int NW = WM * WN * KSP;
+    constexpr int NW = WM * WN;
     constexpr int NT = NW * 64;
-    // KSP = 2 splits each chunk's MFMA k-steps between the two waves of a
-    // pair that own the same output block: every weight fragment is then
-    // fetched by WM waves instead of 2 * WM, and the pair's partial sums are
-    // added through LDS before the store.
-    constexpr int KSW = P::KS / KSP;   // k-steps per wave per step
-    constexpr int NGW = P::NG / KSP;   // 16-byte weight words per lane per wave
     constexpr int ES = sizeof(T);
     constexpr int KC = P::KC;
     constexpr int WTM = TM / WM;
@@ -405,7 +399,6 @@ __global__ __launch_bounds__(WM * WN * KSP * 64, 1) void conv_kernel(ConvArgs a)
     constexpr int STAGE = kStageUnits;          // 16-byte units per A buffer
     constexpr int NPART = 4;                    // parts of a chunk's staging
     static_assert(FM >= 1 && FN >= 1, "wave geometry");
-    static_assert(KSP == 1 || (KSP == 2 && KSW % P::G == 0 && FM % 2 == 0), "k-split geometry");
     static_assert(!Q8 || ES == 2, "Q8_0 weights feed 16-bit MFMA operands");
     static_assert(NTAPS <= 32, "tap mask is 32-bit");
     static_assert(2 * kWinWords * 4 <= STAGE * 16, "bitmap aliases the A stage");
@@ -496,9 +489,8 @@ __global__ __launch_bounds__(WM * WN * KSP * 64, 1) void conv_kernel(ConvArgs a)
     const int kch = a.cin / KC;
     const int ncol32 = a.cout / 32;
 
-    const int kh = wave % KSP;          // k-half of the wave (0 without a split)
-    const int wm = wave / KSP / WN;
-    const int wn = wave / KSP % WN;
+    const int wm = wave / WN;
+    const int wn = wave % WN;
 
     floatx16 acc[FM][FN];
 #pragma unroll
@@ -512,7 +504,7 @@ __global__ __launch_bounds__(WM * WN * KSP * 64, 1) void conv_kernel(ConvArgs a)
     const u32x4 zero4 = {0u, 0u, 0u, 0u};
 
     struct Slot {
-        u32x4 q[FN][NGW];
+        u32x4 q[FN][P::NG];
         float d[Q8 ? FN : 1];
     };
 
@@ -531,9 +523,9 @@ __global__ __launch_bounds__(WM * WN * KSP * 64, 1) void conv_kernel(ConvArgs a)
             if constexpr (PACKED) {
                 const uint32_t panel = ((uint32_t)o * (uint32_t)kch + (uint32_t)kc) * (uint32_t)ncol32 +
                                        (uint32_t)c32;
-                const int poff = (int)(panel * (uint32_t)(P::NG * 1024)) + kh * (NGW * 1024);
+                const int poff = (int)(panel * (uint32_t)(P::NG * 1024));
 #pragma unroll
-                for (int g = 0; g < NGW; ++g)
+                for (int g = 0; g < P::NG; ++g)
                     sl.q[j][g] = __builtin_bit_cast(
                         u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrsrc, lane * 16 + g * 1024, poff, 0));
                 if constexpr (Q8)
@@ -541,11 +533,10 @@ __global__ __launch_bounds__(WM * WN * KSP * 64, 1) void conv_kernel(ConvArgs a)
             } else {
                 const int64_t rowbase = ((int64_t)co * NTAPS + o) * a.cin + (int64_t)kc * KC;
 #pragma unroll
-                for (int gg = 0; gg < NGW; ++gg) {
-                    const int g = kh * NGW + gg;
+                for (int g = 0; g < P::NG; ++g) {
                     if constexpr (P::G == 1) {
                         const int64_t el = rowbase + g * P::KSUB + (lane >> 5) * P::EPL;
-                        sl.q[j][gg] = *reinterpret_cast<const u32x4*>(
+                        sl.q[j][g] = *reinterpret_cast<const u32x4*>(
                             static_cast<const char*>(a.w) + el * P::WB);
                     } else {
                         uint32_t words[4];
@@ -559,7 +550,7 @@ __global__ __launch_bounds__(WM * WN * KSP * 64, 1) void conv_kernel(ConvArgs a)
 #pragma unroll
                             for (int h = 0; h < WPK; ++h) words[i * WPK + h] = wp[h];
                         }
-                        sl.q[j][gg] = u32x4{words[0], words[1], words[2], words[3]};
+                        sl.q[j][g] = u32x4{words[0], words[1], words[2], words[3]};
                     }
                 }
                 if constexpr (Q8)
@@ -568,7 +559,7 @@ __global__ __launch_bounds__(WM * WN * KSP * 64, 1) void conv_kernel(ConvArgs a)
         }
     };
 
-    // B fragment of the wave's k-step ks (0 .. KSW-1) from a loaded slot
+    // B fragment of k-step ks from a loaded slot
     auto b_frag = [&](const Slot& sl, int j, int ks) __attribute__((always_inline)) {
         typename M::frag f;
         const u32x4 wv4 = sl.q[j][ks / P::G];
@@ -599,7 +590,7 @@ __global__ __launch_bounds__(WM * WN * KSP * 64, 1) void conv_kernel(ConvArgs a)
         return f;
     };
 
-    typedef typename M::frag AFrag[KSW][FM];
+    typedef typename M::frag AFrag[P::KS][FM];
     // The MFMA computes the transposed block (weights as the 32-row operand,
     // gathered features as the 32-column one): the accumulator of lane l then
     // holds output row l%32 and output channels 8*(k/4) + 4*(l/32) + k%4 for
@@ -607,7 +598,7 @@ __global__ __launch_bounds__(WM * WN * KSP * 64, 1) void conv_kernel(ConvArgs a)
     // straight to global memory.
     auto mma_step = [&](const AFrag& af, const Slot& bs) __attribute__((always_inline)) {
 #pragma unroll
-        for (int ks = 0; ks < KSW; ++ks) {
+        for (int ks = 0; ks < P::KS; ++ks) {
 #pragma unroll
             for (int j = 0; j < FN; ++j) {
                 const typename M::frag bf = b_frag(bs, j, ks);
@@ -620,9 +611,9 @@ __global__ __launch_bounds__(WM * WN * KSP * 64, 1) void conv_kernel(ConvArgs a)
     // keys (the row's first 16-byte unit); the byte of each k-step within
     // the 64-byte row is a lane constant.
     auto read_frags = [&](int buf, const int* sl, AFrag& f) __attribute__((always_inline)) {
-        const char* ab = reinterpret_cast<const char*>(Au + buf * STAGE) + kh * (KSW * M::KSUB * ES);
+        const char* ab = reinterpret_cast<const char*>(Au + buf * STAGE);
 #pragma unroll
-        for (int ks = 0; ks < KSW; ++ks) {
+        for (int ks = 0; ks < P::KS; ++ks) {
             const int byte = (ks * M::KSUB + (lane >> 5) * M::EPL) * ES;  // within the 64-byte row
 #pragma unroll
             for (int i = 0; i < FM; ++i)
@@ -661,23 +652,40 @@ __global__ __launch_bounds__(WM * WN * KSP * 64, 1) void conv_kernel(ConvArgs a)
         const uint32_t au_lds = __builtin_amdgcn_readfirstlane(
             (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) u32x4*)Au));
         const int nblk = ((U + 1) * kPitch + 63) / 64;
-        const int bpp = (nblk + NPART - 1) / NPART;  // blocks per part
-        auto stage_part = [&](int kc, int buf, int h) __attribute__((always_inline)) {
-            const int koff = kc * KC * ES;
-            const int bend = min(nblk, (h + 1) * bpp);
-            for (int blk = h * bpp + wave; blk < bend; blk += NW) {
-                const int v = blk * 64 + lane;
-                const int r = v / kPitch;
-                const int sg = v - r * kPitch;
-                uint32_t off = 0x80000000u;  // out of range: zeros
-                if (sg < kSegs && r < U)
-                    off = (uint32_t)(urow[r] - row0) * (uint32_t)rowbytes + (uint32_t)(sg * 16);
-                lds_dma_x4(xrsrc, au_lds + (uint32_t)((buf * STAGE + blk * 64) * 16), off,
-                           __builtin_amdgcn_readfirstlane((uint32_t)koff));
+        // Wave w fills blocks w + NW j.  The per-lane source offsets do not
+        // depend on the chunk (it enters as the scalar offset), so they are
+        // computed once per tile and kept in registers.
+        constexpr int NJ = (STAGE / 64 + NW - 1) / NW;  // blocks per wave, at most
+        uint32_t doff[NJ];
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int v = (wave + NW * j) * 64 + lane;
+            const int r = v / kPitch;
+            const int sg = v - r * kPitch;
+            doff[j] = 0x80000000u;  // out of range: zeros
+            if (sg < kSegs && r < U)
+                doff[j] = (uint32_t)(urow[r] - row0) * (uint32_t)rowbytes + (uint32_t)(sg * 16);
+        }
+        // part h of a chunk: the wave's blocks j in [h NJ / NPART, (h + 1) NJ / NPART)
+        auto stage_part = [&](int kc, int buf, auto h_const) __attribute__((always_inline)) {
+            constexpr int H = decltype(h_const)::value;
+            const uint32_t koff = (uint32_t)__builtin_amdgcn_readfirstlane(kc * KC * ES);
+#pragma unroll
+            for (int j = H * NJ / NPART; j < (H + 1) * NJ / NPART; ++j) {
+                const int blk = wave + NW * j;
+                if (blk < nblk) lds_dma_x4(xrsrc, au_lds + (uint32_t)((buf * STAGE + blk * 64) * 16), doff[j], koff);
             }
         };
+        // part h for a run-time h < NPART
+        auto stage_part_rt = [&](int kc, int buf, int h) __attribute__((always_inline)) {
+            static_assert(NPART == 4, "parts");
+            if (h == 0) stage_part(kc, buf, std::integral_constant<int, 0>{});
+            else if (h == 1) stage_part(kc, buf, std::integral_constant<int, 1>{});
+            else if (h == 2) stage_part(kc, buf, std::integral_constant<int, 2>{});
+            else stage_part(kc, buf, std::integral_constant<int, 3>{});
+        };
         // vector-memory loads per step (weight words, plus Q8_0 scales)
-        constexpr int LPS = PACKED ? FN * NGW + (Q8 ? FN : 0) : 0;
+        constexpr int LPS = PACKED ? FN * P::NG + (Q8 ? FN : 0) : 0;
 
         // Steps of a chunk: the active taps in ascending order, padded to a
         // multiple of PD with steps that read the zero slot (row NTAPS)
@@ -714,7 +722,7 @@ __global__ __launch_bounds__(WM * WN * KSP * 64, 1) void conv_kernel(ConvArgs a)
             for (int p = 0; p < PD; ++p) load_b(b_tap(w0, p), 0, ring[p]);
             read_slots(s_row(w0, 0), sreg[0]);
             read_slots(s_row(w0, 1), sreg[1]);
-            for (int h = 0; h < NPART; ++h) stage_part(0, 0, h);
+            for (int h = 0; h < NPART; ++h) stage_part_rt(0, 0, h);
             dma_barrier<0>();
             read_frags(0, sreg[0], afr[0]);
         }
@@ -741,7 +749,7 @@ __global__ __launch_bounds__(WM * WN * KSP * 64, 1) void conv_kernel(ConvArgs a)
                 const uint32_t w1 = last_g ? tw_first[0] : tw[1];
                 const int kc_next = last_g ? kc + 1 : kc;  // chunk of the steps PD ahead
                 const int kc_b = min(kc_next, kch - 1);  // past the last chunk: a valid, unused panel
-                if (more && g < NPART) stage_part(kc + 1, buf ^ 1, g);
+                if (more && g < NPART) stage_part_rt(kc + 1, buf ^ 1, g);
                 __builtin_amdgcn_sched_barrier(0);  // the part's loads precede the group's
                 auto step = [&](auto u_const) __attribute__((always_inline)) {
                     constexpr int u = decltype(u_const)::value;
@@ -760,8 +768,8 @@ __global__ __launch_bounds__(WM * WN * KSP * 64, 1) void conv_kernel(ConvArgs a)
                     // issue order: slot reads, then MFMAs interleaved with the
                     // fragment reads and their address arithmetic, then the
                     // weight loads
-                    constexpr int NMF = KSW * FM * FN;
-                    constexpr int NFR = KSW * FM;
+                    constexpr int NMF = P::KS * FM * FN;
+                    constexpr int NFR = P::KS * FM;
                     __builtin_amdgcn_sched_group_barrier(0x100, FM, 0);
 #pragma unroll
                     for (int q = 0; q < NMF; ++q) {
@@ -769,7 +777,7 @@ __global__ __launch_bounds__(WM * WN * KSP * 64, 1) void conv_kernel(ConvArgs a)
                         if (q < NFR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
                         __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
                     }
-                    __builtin_amdgcn_sched_group_barrier(0x020, FN * NGW, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x020, FN * P::NG, 0);
                     // nothing crosses a step boundary: without this fence the
                     // scheduler sinks every weight load of the group to its
                     // end, which leaves the next group's first steps waiting
@@ -785,7 +793,7 @@ __global__ __launch_bounds__(WM * WN * KSP * 64, 1) void conv_kernel(ConvArgs a)
             for (int g = 0; g + 1 < ngr; ++g) run_group(g, std::false_type{});
             run_group(ngr - 1, std::true_type{});
             if (more)  // short chunks: the parts the group loop did not reach
-                for (int h = ngr; h < NPART; ++h) stage_part(kc + 1, buf ^ 1, h);
+                for (int h = ngr; h < NPART; ++h) stage_part_rt(kc + 1, buf ^ 1, h);
         }
     } else if (nt > 0) {
         // Fallback (the union does not fit the stage): each tap's 256 source
@@ -823,47 +831,6 @@ __global__ __launch_bounds__(WM * WN * KSP * 64, 1) void conv_kernel(ConvArgs a)
         }
     }
 
-    // ---- k-split: the pair's partial sums meet in LDS.  Wave kh keeps the
-    // row blocks [kh * FM/2, (kh + 1) * FM/2) and hands the other half to
-    // its partner (wave ^ 1), which adds it to its own.
-    if constexpr (KSP == 2) {
-        constexpr int HB = FM / 2;
-        constexpr int NV = HB * FN * 4;  // 16-byte values per lane handed over
-        static_assert(NW * NV * 64 <= 2 * STAGE, "the exchange fits the A stage");
-        floatx4* xs = reinterpret_cast<floatx4*>(Au);
-        auto put = [&](auto b0_const) __attribute__((always_inline)) {
-            constexpr int B0 = decltype(b0_const)::value;
-#pragma unroll
-            for (int ii = 0; ii < HB; ++ii)
-#pragma unroll
-                for (int j = 0; j < FN; ++j)
-#pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        xs[(wave * NV + (ii * FN + j) * 4 + q) * 64 + lane] =
-                            floatx4{acc[B0 + ii][j][4 * q], acc[B0 + ii][j][4 * q + 1],
-                                    acc[B0 + ii][j][4 * q + 2], acc[B0 + ii][j][4 * q + 3]};
-        };
-        auto take = [&](auto b0_const) __attribute__((always_inline)) {
-            constexpr int B0 = decltype(b0_const)::value;
-#pragma unroll
-            for (int ii = 0; ii < HB; ++ii)
-#pragma unroll
-                for (int j = 0; j < FN; ++j)
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const floatx4 v = xs[((wave ^ 1) * NV + (ii * FN + j) * 4 + q) * 64 + lane];
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) acc[B0 + ii][j][4 * q + e] += v[e];
-                    }
-        };
-        lds_barrier();  // every wave is done with the A stage
-        if (kh == 0) put(std::integral_constant<int, HB>{});
-        else put(std::integral_constant<int, 0>{});
-        lds_barrier();
-        if (kh == 0) take(std::integral_constant<int, 0>{});
-        else take(std::integral_constant<int, HB>{});
-    }
-
     // ---- epilogue: + bias in F32, one rounding.  Each lane holds four runs
     // of four consecutive channels of one row; they go to an LDS output
     // tile (8-byte writes, 16 in f32), then whole rows leave with coalesced
@@ -880,9 +847,6 @@ __global__ __launch_bounds__(WM * WN * KSP * 64, 1) void conv_kernel(ConvArgs a)
         lds_barrier();  // every wave is done with the A stage / the previous pass
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
-            if constexpr (KSP == 2) {
-                if ((i >= FM / 2) != (kh == 1)) continue;  // the partner stores this block
-            }
             const int rl = wm * WTM + i * 32 + (lane & 31);
             if (wm * WTM + i * 32 < p * RPP || wm * WTM + i * 32 >= (p + 1) * RPP) continue;
 #pragma unroll
@@ -921,7 +885,7 @@ __global__ __launch_bounds__(WM * WN * KSP * 64, 1) void conv_kernel(ConvArgs a)
     }
 }
 
-template <typename T, bool Q8, bool PACKED, int NTAPS, int TN, int WM, int WN, int KSP>
+template <typename T, bool Q8, bool PACKED, int NTAPS, int TN, int WM, int WN>
 hipError_t launch_conv(hipStream_t s, ConvArgs a) {
     const int64_t tiles_m = ceil_div(a.n_out, kTM);
     a.tiles_n = a.cout / TN;
@@ -929,24 +893,22 @@ hipError_t launch_conv(hipStream_t s, ConvArgs a) {
     a.tiles_per_xcd = ceil_div(a.total_tiles, 8);
     const int64_t grid = a.tiles_per_xcd * 8;
     if (grid == 0) return hipSuccess;
-    conv_kernel<T, Q8, PACKED, NTAPS, TN, WM, WN, KSP, 4><<<(unsigned)grid, WM * WN * KSP * 64, 0, s>>>(a);
+    conv_kernel<T, Q8, PACKED, NTAPS, TN, WM, WN, 4><<<(unsigned)grid, WM * WN * 64, 0, s>>>(a);
     return hipGetLastError();
 }
 
-// TN = largest of {128, 64, 32} dividing cout.  16-bit activations with
-// TN = 128 run 8 waves as 2x2 blocks of 128x64 with the chunk's k-steps
-// split between the two waves of a block (half the weight-fragment traffic
-// of 4x2 blocks of 64x64); fp32 runs 4x2 (64x64); TN = 64 4x2 (64x32);
-// TN = 32 8x1 (32x32).  Q8_0 weights use 4 waves of 128x64: each
-// in-register dequantised B fragment then feeds four MFMAs instead of two.
+// TN = largest of {128, 64, 32} dividing cout; 8 waves as 4x2 (64x64 wave
+// tiles), 4x2 (64x32) or 8x1 (32x32).  Q8_0 weights use 4 waves of 128x64:
+// each in-register dequantised B fragment then feeds four MFMAs instead of
+// two.
 template <typename T, bool Q8, bool PACKED, int NTAPS>
 hipError_t dispatch_tn(hipStream_t s, const ConvArgs& a) {
     if (a.cout % 128 == 0) {
-        if constexpr (Q8) return launch_conv<T, Q8, PACKED, NTAPS, 128, 2, 2, 1>(s, a);
-        else return launch_conv<T, Q8, PACKED, NTAPS, 128, 4, 2, 1>(s, a);
+        if constexpr (Q8) return launch_conv<T, Q8, PACKED, NTAPS, 128, 2, 2>(s, a);
+        else return launch_conv<T, Q8, PACKED, NTAPS, 128, 4, 2>(s, a);
     }
-    if (a.cout % 64 == 0) return launch_conv<T, Q8, PACKED, NTAPS, 64, 4, 2, 1>(s, a);
-    return launch_conv<T, Q8, PACKED, NTAPS, 32, 8, 1, 1>(s, a);
+    if (a.cout % 64 == 0) return launch_conv<T, Q8, PACKED, NTAPS, 64, 4, 2>(s, a);
+    return launch_conv<T, Q8, PACKED, NTAPS, 32, 8, 1>(s, a);
 }
 
 template <typename T, bool Q8>
