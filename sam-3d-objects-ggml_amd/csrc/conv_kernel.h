@@ -410,8 +410,8 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
     __shared__ __attribute__((aligned(16))) int32_t urow[kURowCap];  // source row of each union slot
     __shared__ __attribute__((aligned(16))) int32_t srow[TM];        // output row of each tile row
     __shared__ int32_t wsum[NW];
-    __shared__ int32_t misc[8];
-    __shared__ float sbias[TN];
+    __shared__ __attribute__((aligned(16))) int32_t misc[8];
+    __shared__ __attribute__((aligned(16))) float sbias[TN];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -433,35 +433,42 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
     int U;
     bool fast;
     if (a.plan) {
-        // the tile's setup from the plan: 16-byte copies into LDS
-        const char* pt = static_cast<const char*>(a.plan) + tm * plan_tile_bytes(NTAPS);
-        const int32_t* hdr = reinterpret_cast<const int32_t*>(pt);
-        U = hdr[0];
-        tile_mask = (uint32_t)hdr[1];
-        fast = hdr[2] != 0;
-        constexpr int NSR = TM / 4;                 // srow units
-        constexpr int NSI = (NTAPS + 1) * TM / 8;   // sidx units
-        const int nur = fast ? (U + 3) / 4 : 0;     // urow units
-        const int total = 2 + NSR + (fast ? NSI : 0) + nur;
-        for (int u = tid; u < total; u += NT) {
-            const u32x4* src;
+        // the tile's setup from the plan: one batch of 16-byte copies of the
+        // whole plan tile (header, tap words, output rows, union rows, slot
+        // keys -- contiguous in the plan) into LDS, all loads in flight at once
+        const u32x4* pt = reinterpret_cast<const u32x4*>(static_cast<const char*>(a.plan) +
+                                                         tm * plan_tile_bytes(NTAPS));
+        constexpr int NHD = 2, NTW = 2;              // header and tap-word units
+        constexpr int NSR = TM / 4;                  // srow units
+        constexpr int NUR = kURowCap / 4;            // urow units
+        constexpr int NSI = (NTAPS + 1) * TM / 8;    // sidx units
+        constexpr int TOTAL = NHD + NTW + NSR + NUR + NSI;
+        constexpr int IT = (TOTAL + NT - 1) / NT;
+        static_assert(kPlanSrow == 16 * (NHD + NTW) && kPlanUrow == kPlanSrow + 16 * NSR &&
+                          kPlanSidx == kPlanUrow + 16 * NUR,
+                      "plan sections are contiguous");
+        u32x4 pv[IT];
+#pragma unroll
+        for (int k = 0; k < IT; ++k) {
+            const int u = tid + k * NT;
+            if (u < TOTAL) pv[k] = pt[u];
+        }
+#pragma unroll
+        for (int k = 0; k < IT; ++k) {
+            const int u = tid + k * NT;
+            if (u >= TOTAL) continue;
             u32x4* dst;
-            if (u < 2) {
-                src = reinterpret_cast<const u32x4*>(pt + 32) + u;
-                dst = reinterpret_cast<u32x4*>(tlw) + u;
-            } else if (u < 2 + NSR) {
-                src = reinterpret_cast<const u32x4*>(pt + kPlanSrow) + (u - 2);
-                dst = reinterpret_cast<u32x4*>(srow) + (u - 2);
-            } else if (u < 2 + NSR + nur) {
-                src = reinterpret_cast<const u32x4*>(pt + kPlanUrow) + (u - 2 - NSR);
-                dst = reinterpret_cast<u32x4*>(urow) + (u - 2 - NSR);
-            } else {
-                src = reinterpret_cast<const u32x4*>(pt + kPlanSidx) + (u - 2 - NSR - nur);
-                dst = reinterpret_cast<u32x4*>(sidx) + (u - 2 - NSR - nur);
-            }
-            *dst = *src;
+            if (u < NHD) dst = reinterpret_cast<u32x4*>(misc) + u;
+            else if (u < NHD + NTW) dst = reinterpret_cast<u32x4*>(tlw) + (u - NHD);
+            else if (u < NHD + NTW + NSR) dst = reinterpret_cast<u32x4*>(srow) + (u - NHD - NTW);
+            else if (u < NHD + NTW + NSR + NUR) dst = reinterpret_cast<u32x4*>(urow) + (u - NHD - NTW - NSR);
+            else dst = reinterpret_cast<u32x4*>(sidx) + (u - NHD - NTW - NSR - NUR);
+            *dst = pv[k];
         }
         lds_barrier();
+        U = misc[0];
+        tile_mask = (uint32_t)misc[1];
+        fast = misc[2] != 0;
     } else {
         const TileLds L{reinterpret_cast<uint32_t*>(Au), sidx, tlw, urow, srow, wsum, misc};
         tile_setup<NTAPS, NT, PD>(a, r0, L);
@@ -492,13 +499,20 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
     const int wm = wave / WN;
     const int wn = wave % WN;
 
+    // accumulators start at the bias: element 4g + e of lane l holds output
+    // channel 8g + 4(l/32) + e of its 32-column block
     floatx16 acc[FM][FN];
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+    for (int j = 0; j < FN; ++j) {
+        floatx4 b4[4];
 #pragma unroll
-        for (int j = 0; j < FN; ++j)
+        for (int g = 0; g < 4; ++g)
+            b4[g] = *reinterpret_cast<const floatx4*>(sbias + wn * WTN + j * 32 + 8 * g + 4 * (lane >> 5));
 #pragma unroll
-            for (int k = 0; k < 16; ++k) acc[i][j][k] = 0.0f;
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int k = 0; k < 16; ++k) acc[i][j][k] = b4[k / 4][k % 4];
+    }
 
     const char* xb = static_cast<const char*>(a.x);
     const u32x4 zero4 = {0u, 0u, 0u, 0u};
@@ -856,7 +870,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
                     const int cl = wn * WTN + j * 32 + 8 * g + 4 * (lane >> 5);
                     float v[4];
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * g + e] + sbias[cl + e];
+                    for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * g + e];
                     char* dst = ob + (rl - p * RPP) * OPITCH + cl * ES;
                     if constexpr (ES == 4) {
                         *reinterpret_cast<float2*>(dst) = float2{v[0], v[1]};
@@ -870,17 +884,28 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
             }
         }
         lds_barrier();
-        for (int c = tid; c < RPP * UPR; c += NT) {
+        // all LDS reads first, then the stores
+        constexpr int NU = RPP * UPR / NT;
+        static_assert(RPP * UPR % NT == 0, "store geometry");
+        int32_t tt[NU];
+        u32x4 vv[NU];
+#pragma unroll
+        for (int k = 0; k < NU; ++k) {
+            const int c = tid + k * NT;
             const int r = c / UPR;
             const int q = c - r * UPR;
-            const int32_t t = srow[p * RPP + r];
-            if (t >= 0) {
-                const char* src = ob + r * OPITCH + q * 16;
-                const u32x2 lo = *reinterpret_cast<const u32x2*>(src);
-                const u32x2 hi = *reinterpret_cast<const u32x2*>(src + 8);
-                *reinterpret_cast<u32x4*>(yb + ((int64_t)t * a.cout + co0) * ES + q * 16) =
-                    u32x4{lo.x, lo.y, hi.x, hi.y};
-            }
+            tt[k] = srow[p * RPP + r];
+            const char* src = ob + r * OPITCH + q * 16;
+            const u32x2 lo = *reinterpret_cast<const u32x2*>(src);
+            const u32x2 hi = *reinterpret_cast<const u32x2*>(src + 8);
+            vv[k] = u32x4{lo.x, lo.y, hi.x, hi.y};
+        }
+#pragma unroll
+        for (int k = 0; k < NU; ++k) {
+            const int c = tid + k * NT;
+            const int q = c % UPR;
+            if (tt[k] >= 0)
+                *reinterpret_cast<u32x4*>(yb + ((int64_t)tt[k] * a.cout + co0) * ES + q * 16) = vv[k];
         }
     }
 }
