@@ -69,6 +69,7 @@ struct ConvArgs {
     int32_t packed;
     int32_t tiles_n;
     int64_t total_tiles;
+    int64_t heavy_tiles;      // tiles of full row tiles (mapped XCD-major)
     int64_t tiles_per_xcd;
     const void* plan;         // per-row-tile setup from conv_plan_kernel, or null
 };
@@ -417,11 +418,20 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
 
-    // XCD-major tile mapping
-    const int64_t xcd = blockIdx.x & 7;
-    const int64_t local = blockIdx.x >> 3;
-    const int64_t tile = xcd * a.tiles_per_xcd + local;
-    if (local >= a.tiles_per_xcd || tile >= a.total_tiles) return;
+    // Tile mapping: the full row tiles XCD-major (workgroup b runs on XCD
+    // b % 8, each XCD gets a contiguous range), then the tiles of a partial
+    // last row tile, which run last and cost little.
+    int64_t tile;
+    const int64_t hb = a.tiles_per_xcd * 8;  // workgroups of the XCD-major part
+    if ((int64_t)blockIdx.x < hb) {
+        const int64_t xcd = blockIdx.x & 7;
+        const int64_t local = blockIdx.x >> 3;
+        tile = xcd * a.tiles_per_xcd + local;
+        if (tile >= a.heavy_tiles) return;
+    } else {
+        tile = a.heavy_tiles + ((int64_t)blockIdx.x - hb);
+        if (tile >= a.total_tiles) return;
+    }
     const int64_t tm = tile / a.tiles_n;
     const int tn = (int)(tile % a.tiles_n);
     const int64_t r0 = tm * TM;
@@ -720,94 +730,107 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
             return t == 0xff ? NTAPS : t;
         };
 
-        Slot ring[PD];
-        AFrag afr[2];
-        int sreg[2][FM];
-        // the tap words in scalar registers: tw0 holds the running group's
-        // word, the rest shift down one word per group; tw_first restores
-        // them at every chunk start
-        uint32_t tw_first[kTapWords], tw[kTapWords];
-#pragma unroll
-        for (int w = 0; w < kTapWords; ++w) tw_first[w] = __builtin_amdgcn_readfirstlane(tlw[w]);
-
-        {
-            const uint32_t w0 = tw_first[0];
-#pragma unroll
-            for (int p = 0; p < PD; ++p) load_b(b_tap(w0, p), 0, ring[p]);
-            read_slots(s_row(w0, 0), sreg[0]);
-            read_slots(s_row(w0, 1), sreg[1]);
+        // A wave none of whose rows exists (the partial last row tile) only
+        // does its share of the staging and the barriers.
+        int has_row = 0;
+        for (int k = lane; k < WTM; k += 64) has_row |= srow[wm * WTM + k] >= 0;
+        if (__builtin_amdgcn_ballot_w64(has_row != 0) == 0) {
             for (int h = 0; h < NPART; ++h) stage_part_rt(0, 0, h);
             dma_barrier<0>();
-            read_frags(0, sreg[0], afr[0]);
-        }
-
-        for (int kc = 0; kc < kch; ++kc) {
-            const int buf = kc & 1;
-            const bool more = kc + 1 < kch;
-            if (kc > 0) {
-                // chunk staged; every wave done with the other buffer.  With
-                // ngr >= NPART the last part preceded a whole group's loads.
-                if (ngr >= NPART && LPS > 0) dma_barrier<PD * LPS>();
-                else dma_barrier<0>();
-                read_frags(buf, sreg[0], afr[0]);
+            for (int kc = 0; kc + 1 < kch; ++kc) {
+                for (int h = 0; h < NPART; ++h) stage_part_rt(kc + 1, (kc & 1) ^ 1, h);
+                dma_barrier<0>();
             }
+        } else {
+            Slot ring[PD];
+            AFrag afr[2];
+            int sreg[2][FM];
+            // the tap words in scalar registers: tw0 holds the running group's
+            // word, the rest shift down one word per group; tw_first restores
+            // them at every chunk start
+            uint32_t tw_first[kTapWords], tw[kTapWords];
 #pragma unroll
-            for (int w = 0; w < kTapWords; ++w) tw[w] = tw_first[w];
-            // The last group of a chunk is peeled: its steps past the chunk's
-            // taps (padding) skip their MFMAs but keep their loads, so every
-            // step issues the same number of weight loads.
-            const int nreal = nt - PD * (ngr - 1);  // real steps of the last group
-            auto run_group = [&](int g, auto last_const) __attribute__((always_inline)) {
-                constexpr bool last_g = decltype(last_const)::value;
-                const uint32_t w0 = tw[0];
-                const uint32_t w1 = last_g ? tw_first[0] : tw[1];
-                const int kc_next = last_g ? kc + 1 : kc;  // chunk of the steps PD ahead
-                const int kc_b = min(kc_next, kch - 1);  // past the last chunk: a valid, unused panel
-                if (more && g < NPART) stage_part_rt(kc + 1, buf ^ 1, g);
-                __builtin_amdgcn_sched_barrier(0);  // the part's loads precede the group's
-                auto step = [&](auto u_const) __attribute__((always_inline)) {
-                    constexpr int u = decltype(u_const)::value;
-                    // slots of the step after next (they do not depend on the chunk)
-                    read_slots(u + 2 < PD ? s_row(w0, u + 2) : s_row(w1, u + 2 - PD), sreg[u & 1]);
-                    // A fragments of the next step; after a chunk's last step they
-                    // are re-read behind the barrier, so this read is unused
-                    read_frags(buf, sreg[(u + 1) & 1], afr[(u + 1) & 1]);
-                    if constexpr (last_g && u > 0) {
-                        if (u < nreal) mma_step(afr[u & 1], ring[u]);
-                    } else {
-                        mma_step(afr[u & 1], ring[u]);
-                    }
-                    // weights of the step PD ahead
-                    load_b(b_tap(w1, u), kc_b, ring[u]);
-                    // issue order: slot reads, then MFMAs interleaved with the
-                    // fragment reads and their address arithmetic, then the
-                    // weight loads
-                    constexpr int NMF = P::KS * FM * FN;
-                    constexpr int NFR = P::KS * FM;
-                    __builtin_amdgcn_sched_group_barrier(0x100, FM, 0);
+            for (int w = 0; w < kTapWords; ++w) tw_first[w] = __builtin_amdgcn_readfirstlane(tlw[w]);
+
+            {
+                const uint32_t w0 = tw_first[0];
 #pragma unroll
-                    for (int q = 0; q < NMF; ++q) {
-                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                        if (q < NFR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
-                    }
-                    __builtin_amdgcn_sched_group_barrier(0x020, FN * P::NG, 0);
-                    // nothing crosses a step boundary: without this fence the
-                    // scheduler sinks every weight load of the group to its
-                    // end, which leaves the next group's first steps waiting
-                    __builtin_amdgcn_sched_barrier(0);
+                for (int p = 0; p < PD; ++p) load_b(b_tap(w0, p), 0, ring[p]);
+                read_slots(s_row(w0, 0), sreg[0]);
+                read_slots(s_row(w0, 1), sreg[1]);
+                for (int h = 0; h < NPART; ++h) stage_part_rt(0, 0, h);
+                dma_barrier<0>();
+                read_frags(0, sreg[0], afr[0]);
+            }
+
+            for (int kc = 0; kc < kch; ++kc) {
+                const int buf = kc & 1;
+                const bool more = kc + 1 < kch;
+                if (kc > 0) {
+                    // chunk staged; every wave done with the other buffer.  With
+                    // ngr >= NPART the last part preceded a whole group's loads.
+                    if (ngr >= NPART && LPS > 0) dma_barrier<PD * LPS>();
+                    else dma_barrier<0>();
+                    read_frags(buf, sreg[0], afr[0]);
+                }
+#pragma unroll
+                for (int w = 0; w < kTapWords; ++w) tw[w] = tw_first[w];
+                // The last group of a chunk is peeled: its steps past the chunk's
+                // taps (padding) skip their MFMAs but keep their loads, so every
+                // step issues the same number of weight loads.
+                const int nreal = nt - PD * (ngr - 1);  // real steps of the last group
+                auto run_group = [&](int g, auto last_const) __attribute__((always_inline)) {
+                    constexpr bool last_g = decltype(last_const)::value;
+                    const uint32_t w0 = tw[0];
+                    const uint32_t w1 = last_g ? tw_first[0] : tw[1];
+                    const int kc_next = last_g ? kc + 1 : kc;  // chunk of the steps PD ahead
+                    const int kc_b = min(kc_next, kch - 1);  // past the last chunk: a valid, unused panel
+                    if (more && g < NPART) stage_part_rt(kc + 1, buf ^ 1, g);
+                    __builtin_amdgcn_sched_barrier(0);  // the part's loads precede the group's
+                    auto step = [&](auto u_const) __attribute__((always_inline)) {
+                        constexpr int u = decltype(u_const)::value;
+                        // slots of the step after next (they do not depend on the chunk)
+                        read_slots(u + 2 < PD ? s_row(w0, u + 2) : s_row(w1, u + 2 - PD), sreg[u & 1]);
+                        // A fragments of the next step; after a chunk's last step they
+                        // are re-read behind the barrier, so this read is unused
+                        read_frags(buf, sreg[(u + 1) & 1], afr[(u + 1) & 1]);
+                        if constexpr (last_g && u > 0) {
+                            if (u < nreal) mma_step(afr[u & 1], ring[u]);
+                        } else {
+                            mma_step(afr[u & 1], ring[u]);
+                        }
+                        // weights of the step PD ahead
+                        load_b(b_tap(w1, u), kc_b, ring[u]);
+                        // issue order: slot reads, then MFMAs interleaved with the
+                        // fragment reads and their address arithmetic, then the
+                        // weight loads
+                        constexpr int NMF = P::KS * FM * FN;
+                        constexpr int NFR = P::KS * FM;
+                        __builtin_amdgcn_sched_group_barrier(0x100, FM, 0);
+#pragma unroll
+                        for (int q = 0; q < NMF; ++q) {
+                            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                            if (q < NFR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                            __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+                        }
+                        __builtin_amdgcn_sched_group_barrier(0x020, FN * P::NG, 0);
+                        // nothing crosses a step boundary: without this fence the
+                        // scheduler sinks every weight load of the group to its
+                        // end, which leaves the next group's first steps waiting
+                        __builtin_amdgcn_sched_barrier(0);
+                    };
+                    step(std::integral_constant<int, 0>{});
+                    step(std::integral_constant<int, 1>{});
+                    step(std::integral_constant<int, 2>{});
+                    step(std::integral_constant<int, 3>{});
+#pragma unroll
+                    for (int w = 0; w + 1 < kTapWords; ++w) tw[w] = tw[w + 1];
                 };
-                step(std::integral_constant<int, 0>{});
-                step(std::integral_constant<int, 1>{});
-                step(std::integral_constant<int, 2>{});
-                step(std::integral_constant<int, 3>{});
-#pragma unroll
-                for (int w = 0; w + 1 < kTapWords; ++w) tw[w] = tw[w + 1];
-            };
-            for (int g = 0; g + 1 < ngr; ++g) run_group(g, std::false_type{});
-            run_group(ngr - 1, std::true_type{});
-            if (more)  // short chunks: the parts the group loop did not reach
-                for (int h = ngr; h < NPART; ++h) stage_part_rt(kc + 1, buf ^ 1, h);
+                for (int g = 0; g + 1 < ngr; ++g) run_group(g, std::false_type{});
+                run_group(ngr - 1, std::true_type{});
+                if (more)  // short chunks: the parts the group loop did not reach
+                    for (int h = ngr; h < NPART; ++h) stage_part_rt(kc + 1, buf ^ 1, h);
+            }
         }
     } else if (nt > 0) {
         // Fallback (the union does not fit the stage): each tap's 256 source
@@ -915,8 +938,9 @@ hipError_t launch_conv(hipStream_t s, ConvArgs a) {
     const int64_t tiles_m = ceil_div(a.n_out, kTM);
     a.tiles_n = a.cout / TN;
     a.total_tiles = tiles_m * a.tiles_n;
-    a.tiles_per_xcd = ceil_div(a.total_tiles, 8);
-    const int64_t grid = a.tiles_per_xcd * 8;
+    a.heavy_tiles = (a.n_out % kTM ? tiles_m - 1 : tiles_m) * a.tiles_n;
+    a.tiles_per_xcd = ceil_div(a.heavy_tiles, 8);
+    const int64_t grid = a.tiles_per_xcd * 8 + (a.total_tiles - a.heavy_tiles);
     if (grid == 0) return hipSuccess;
     conv_kernel<T, Q8, PACKED, NTAPS, TN, WM, WN, 4><<<(unsigned)grid, WM * WN * 64, 0, s>>>(a);
     return hipGetLastError();
