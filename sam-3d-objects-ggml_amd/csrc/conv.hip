@@ -1,6 +1,8 @@
 // conv.hip -- C ABI of the sparse convolution (kernel in conv_kernel.h):
 // argument checks, dispatch by dtype, the MFMA-fragment weight packer, the
 // Q8_0 block repacker and the reference-compatible spconv bridge.
+#include <atomic>
+
 #include "conv_kernel.h"
 
 namespace spc {
@@ -149,6 +151,21 @@ __global__ void q8_0_dequant_kernel(const uint8_t* __restrict__ blocks, int64_t 
     if (out_dtype == SPC_F32) static_cast<float*>(out)[i] = v;
     else if (out_dtype == SPC_F16) static_cast<uint16_t*>(out)[i] = f32_to_f16_bits(v);
     else static_cast<uint16_t*>(out)[i] = f32_to_bf16_bits(v);
+}
+
+// Compute units of the current device, queried once per device (an
+// unreadable attribute counts as 256, the MI355X figure).
+int device_cu_count() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+        cache[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
 }
 
 int check_shape(const char* fn, int64_t ntaps, int64_t cin, int64_t cout) {
@@ -331,6 +348,7 @@ int spc_sparse_conv_plan(spc_stream_t stream, int dtype, const void* x, int w_dt
         return SPC_BAD_ARG;
     }
     a.plan = plan;
+    a.num_cu = device_cu_count();
     hipError_t e = hipSuccess;
     if (w_dtype == SPC_Q8_0) {
         if (dtype != SPC_BF16) {

@@ -72,6 +72,7 @@ struct ConvArgs {
     int64_t heavy_tiles;      // tiles of full row tiles (mapped XCD-major)
     int64_t tiles_per_xcd;
     const void* plan;         // per-row-tile setup from conv_plan_kernel, or null
+    int32_t num_cu;           // compute units of the device (tile-width choice)
 };
 
 // MFMA operand traits per activation type.
@@ -946,17 +947,21 @@ hipError_t launch_conv(hipStream_t s, ConvArgs a) {
     return hipGetLastError();
 }
 
-// TN = largest of {128, 64, 32} dividing cout; 8 waves as 4x2 (64x64 wave
-// tiles), 4x2 (64x32) or 8x1 (32x32).  Q8_0 weights use 4 waves of 128x64:
-// each in-register dequantised B fragment then feeds four MFMAs instead of
-// two.
+// TN = largest of {128, 64, 32} dividing cout, halved while the narrower
+// tiles still fit on the device in one round (small row counts would leave
+// compute units idle); 8 waves as 4x2 (64x64 wave tiles), 4x2 (64x32) or
+// 8x1 (32x32).  Q8_0 weights use 4 waves of 128x64: each in-register
+// dequantised B fragment then feeds four MFMAs instead of two.
 template <typename T, bool Q8, bool PACKED, int NTAPS>
 hipError_t dispatch_tn(hipStream_t s, const ConvArgs& a) {
-    if (a.cout % 128 == 0) {
+    const int64_t tiles_m = ceil_div(a.n_out, kTM);
+    int tn = a.cout % 128 == 0 ? 128 : a.cout % 64 == 0 ? 64 : 32;
+    while (tn > 32 && tiles_m * (a.cout / (tn / 2)) <= a.num_cu) tn /= 2;
+    if (tn == 128) {
         if constexpr (Q8) return launch_conv<T, Q8, PACKED, NTAPS, 128, 2, 2>(s, a);
         else return launch_conv<T, Q8, PACKED, NTAPS, 128, 4, 2>(s, a);
     }
-    if (a.cout % 64 == 0) return launch_conv<T, Q8, PACKED, NTAPS, 64, 4, 2>(s, a);
+    if (tn == 64) return launch_conv<T, Q8, PACKED, NTAPS, 64, 4, 2>(s, a);
     return launch_conv<T, Q8, PACKED, NTAPS, 32, 8, 1>(s, a);
 }
 
