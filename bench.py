@@ -45,7 +45,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5],
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5, 6],
                     help="2 = the headline workload; others print diagnostic lines")
     ap.add_argument("--order", choices=["natural", "mask"], default="natural",
                     help="row processing order of the conv kernel")
@@ -254,6 +254,12 @@ def main():
         cin, cout = 128, 1024
         batch = 4
         workload = "stride-2 2x2x2 conv 128->128 then subm3x3x3 128->1024 at 32^3 (bf16)"
+    elif cfg == 6:
+        coords = wl.ellipsoid_batch()
+        cin = cout = 128
+        batch = 4
+        workload = ("SLAT sparse residual block (LayerNorm32, SiLU, subm3x3x3, LayerNorm, "
+                    "modulation, SiLU, subm3x3x3, + skip), bf16 C=128, 4 ellipsoid shells 64^3")
     else:
         coords = wl.sphere_shell()
         cin = cout = 64
@@ -377,6 +383,8 @@ def main():
                   "stride2_ms": ms1, "stride2_tflops": f1 / (ms1 / 1e3) / 1e12,
                   "subm_ms": ms2, "subm_tflops": f2 / (ms2 / 1e3) / 1e12,
                   "pct_peak_subm": 100 * f2 / (ms2 / 1e3) / 1e12 / PEAK_BF16_TFLOPS}
+    elif cfg == 6:
+        result = bench_res_block(spc, nat, wl, orc, coords, c_dev, dev, args, workload)
     else:
         keeps = wl.prune_masks(n)
         lv = []
@@ -401,6 +409,48 @@ def main():
             cc = oc
         result = {"metric": f"config 4: {workload}", "levels": lv, "dtype": "bf16"}
     print(json.dumps(result))
+
+
+def bench_res_block(spc, nat, wl, orc, coords, c_dev, dev, args, workload):
+    """SparseResBlock3d forward on the fused kernels against the same block
+    as separate kernels and torch elementwise ops (both with cached maps)."""
+    import torch
+
+    n = coords.shape[0]
+    torch.manual_seed(0)
+    blk = spc.blocks.SparseResBlock3d(128, 512, 128).to(dev)
+    with torch.no_grad():
+        for p in blk.conv2.parameters():
+            p.normal_(0, 0.02)
+    blk = blk.to(torch.bfloat16)
+    blk.norm1.float()
+    x, _ = bf16_dev(orc, wl.normal((n, 128), 1.0, seed=601), dev)
+    xt = spc.sparse.SparseTensor(x, c_dev)
+    emb = torch.randn(4, 512, device=dev).bfloat16()
+
+    def fused():
+        with torch.no_grad():
+            return blk(xt, emb)
+
+    def unfused():
+        with torch.no_grad():
+            emb_out = blk.emb_layers(emb).type(x.dtype)
+            scale, shift = torch.chunk(emb_out, 2, dim=1)
+            h = xt.replace(nat.layernorm_silu(xt.feats, blk.norm1.weight, blk.norm1.bias))
+            h = blk.conv1(h)
+            h = h.replace(nat.layernorm_silu(h.feats, silu=False))
+            h = h * (1 + scale) + shift
+            h = h.replace(torch.nn.functional.silu(h.feats))
+            h = blk.conv2(h)
+            return h + xt
+
+    ms_f, _ = time_gpu(fused, args.steps, args.warmup)
+    ms_u, _ = time_gpu(unfused, args.steps, args.warmup)
+    diff = float((fused().feats.float() - unfused().feats.float()).abs().max())
+    return {"metric": f"config 6: {workload}", "value": n / (ms_f / 1e3) / 1e6, "unit": "Mvoxel/s",
+            "ms_per_step": ms_f, "unfused_ms": ms_u, "speedup": ms_u / ms_f, "dtype": "bf16",
+            "max_abs_diff_fused_vs_unfused": diff,
+            "config": {"workload": workload, "n_voxels": n, "channels": 128, "batch": 4}}
 
 
 if __name__ == "__main__":

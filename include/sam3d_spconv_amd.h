@@ -262,6 +262,54 @@ int spc_scatter_mean(spc_stream_t stream, int dtype, const void* features, const
 int spc_gather_rows(spc_stream_t stream, int dtype, const void* src, const int32_t* idx,
                     void* dst, int64_t n_out, int64_t n_src, int64_t channels);
 
+/* ------------------------------------------------------------------------
+ * Residual-block prologue and epilogues (SparseResBlock3d,
+ * sam3d_objects/.../models/structured_latent_flow.py:61-74; native graph
+ * SRC/slat_flow_graph.cpp:284-380).
+ * ------------------------------------------------------------------------ */
+
+/* Row LayerNorm then SiLU over x [n, c] in dtype (SPC_F32 / SPC_F16 /
+ * SPC_BF16), as LayerNorm32 + F.silu: mean and biased variance in F32,
+ * (v - mean) / sqrt(var + eps) (* gamma + beta when gamma / beta, f32 [c],
+ * are given), rounded to dtype (LayerNorm32 casts back,
+ * modules/norm.py:6-8), then x * sigmoid(x) in F32 of that value, rounded
+ * again (silu 0 skips it).  y may be x.  c <= 2048. */
+int spc_layernorm_silu(spc_stream_t stream, int dtype, const void* x, int64_t n, int64_t c,
+                       const float* gamma, const float* beta, float eps, int silu, void* y);
+
+/* Conv epilogues, applied to the output rows before they are stored:
+ *   SPC_EPI_RESIDUAL       y = dt(dt(conv + bias) + residual[t])
+ *                          (`h = conv2(h); h = h + skip`, :72-73);
+ *   SPC_EPI_NORM_MOD_SILU  v = dt(conv + bias); u = dt(LayerNorm(v; eps))
+ *                          over the row's cout channels (no affine);
+ *                          m = dt(dt(u * dt(1 + scale[b])) + shift[b]);
+ *                          y = dt(silu(m)), b = coords[4 t] the row's batch
+ *                          (`norm2(h) * (1 + scale) + shift`, then SiLU,
+ *                          :70-71), where dt() rounds to the feature dtype.
+ * residual: [n_out, cout] in dtype.  scale / shift: f32 [n_batch, cout]
+ * holding dtype values (emb_out.type(x.dtype)).  NORM_MOD_SILU needs
+ * cout <= 128 (one tile covers a whole output row). */
+typedef enum { SPC_EPI_NONE = 0, SPC_EPI_RESIDUAL = 1, SPC_EPI_NORM_MOD_SILU = 2 } spc_epilogue_mode;
+typedef struct {
+    int32_t mode;
+    float eps;
+    const void* residual;
+    const float* scale;
+    const float* shift;
+    const int32_t* coords;
+    int64_t n_batch;
+} spc_conv_epilogue;
+
+/* spc_sparse_conv_plan with an epilogue (epi NULL or mode SPC_EPI_NONE:
+ * identical to spc_sparse_conv_plan).  No reference counterpart as one
+ * call: it fuses the reference's separate conv, norm, modulation,
+ * activation and residual nodes. */
+int spc_sparse_conv_fused(spc_stream_t stream, int dtype, const void* x, int w_dtype,
+                          int w_layout, const void* w, const void* w_scale, const void* bias,
+                          void* y, const int32_t* idx, int idx_layout, const int32_t* row_perm,
+                          const void* plan, int64_t ntaps, int64_t n_out, int64_t n_in,
+                          int64_t cin, int64_t cout, const spc_conv_epilogue* epi);
+
 #ifdef __cplusplus
 }
 #endif

@@ -8,7 +8,8 @@ HIP product path never imports it.
 the reference's sparse-conv path); `ref` wraps _ref/libref_tables.so, the
 reference's own cpp_ggml/src/sparse_ops.cpp compiled by the Makefile here
 (present only where the reference tree was available at build time).
-Citations for every function live in spconv_oracle.cpp.
+Citations for the compiled functions live in spconv_oracle.cpp; the numpy
+residual-block pieces at the end of this file carry their own.
 """
 from __future__ import annotations
 
@@ -296,3 +297,70 @@ def cpu_threads() -> int:
         return len(os.sched_getaffinity(0))
     except AttributeError:  # pragma: no cover
         return os.cpu_count() or 1
+
+
+# ---------------------------------------------------------------------------
+# SLAT sparse residual block (structured_latent_flow.py:61-74), numpy.
+# Pinned in tests/test_oracle_block.py against torch's CPU layer_norm / silu
+# and closed forms.
+# ---------------------------------------------------------------------------
+
+def round_to(o: "_Oracle", a: np.ndarray, dtype: int) -> np.ndarray:
+    """Round float32 values to the feature dtype and back (RNE)."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    if dtype == F32:
+        return a
+    if dtype == BF16:
+        return (o.f32_to_bf16(a).astype(np.uint32) << 16).view(np.float32)
+    return o.f32_to_f16(a).view(np.float16).astype(np.float32)
+
+
+def layernorm(a: np.ndarray, gamma=None, beta=None, eps: float = 1e-6) -> np.ndarray:
+    """Row LayerNorm in F32 (torch.nn.LayerNorm as LayerNorm32 runs it,
+    modules/norm.py:6-8): biased variance, eps inside the square root."""
+    a = np.asarray(a, dtype=np.float32)
+    mean = a.mean(axis=1, dtype=np.float64, keepdims=True)
+    var = ((a - mean) ** 2).mean(axis=1, dtype=np.float64, keepdims=True)
+    y = ((a - mean) / np.sqrt(var + eps)).astype(np.float32)
+    if gamma is not None:
+        y = y * np.asarray(gamma, np.float32)
+    if beta is not None:
+        y = y + np.asarray(beta, np.float32)
+    return y.astype(np.float32)
+
+
+def silu(a: np.ndarray) -> np.ndarray:
+    """x * sigmoid(x) in F32 (F.silu)."""
+    a = np.asarray(a, dtype=np.float32)
+    return (a / (np.float32(1.0) + np.exp(-a))).astype(np.float32)
+
+
+def res_block(o: "_Oracle", x: np.ndarray, table: np.ndarray, p: dict, scale: np.ndarray,
+              shift: np.ndarray, batch: np.ndarray, dtype: int = BF16) -> np.ndarray:
+    """SparseResBlock3d.forward without up/down sampling
+    (structured_latent_flow.py:61-74), every intermediate rounded to the
+    feature dtype where the reference's tensors are:
+        h = dt(silu(dt(LN(x) * g + b)));  h = dt(conv1(h))
+        h = dt(silu(dt(dt(dt(LN(h)) * dt(1 + scale)) + shift)))
+        out = dt(dt(conv2(h)) + skip(x)),  skip = x or dt(x W^T + b).
+    x: float32 feature values (already in dtype); table: token-major
+    [N*27] map; p: float32 arrays norm1_w, norm1_b, conv1_w [Co,27,Ci],
+    conv1_b, conv2_w, conv2_b, optional skip_w [Co,Ci], skip_b; scale /
+    shift: [B, Co] dtype values; batch: [N] batch index of each row."""
+    n = x.shape[0]
+    r = lambda a: round_to(o, a, dtype)  # noqa: E731
+
+    def conv(h, w, b):
+        bits = {F32: lambda a: a, BF16: o.f32_to_bf16, F16: o.f32_to_f16}[dtype]
+        y = o.sparse_conv(bits(h), bits(w), bits(b), table, ntaps=27, n_out=n, idx_layout=1,
+                          out_dtype=F32, x_dtype=dtype, w_dtype=dtype, b_dtype=dtype)
+        return r(y)
+
+    h = r(silu(r(layernorm(x, p["norm1_w"], p["norm1_b"]))))
+    h = conv(h, p["conv1_w"], p["conv1_b"])
+    u = r(layernorm(h))
+    m = r(r(u * r(1.0 + scale[batch])) + shift[batch])
+    h = r(silu(m))
+    h = conv(h, p["conv2_w"], p["conv2_b"])
+    skip = x if "skip_w" not in p else r(x @ p["skip_w"].T.astype(np.float32) + p["skip_b"])
+    return r(h + skip)

@@ -6,7 +6,8 @@ SparseConv3d, SparseDownsample, SparseUpsample, SparseSubdivide) on top of
 hand-written gfx950 HIP kernels reached through the C ABI of
 lib/libsam3d_spconv_amd.so (include/sam3d_spconv_amd.h).  `tables` builds
 the reference's SlatTables / MeshTables index structs on the GPU; `gguf`
-reads converted checkpoints and attaches their conv weights.
+reads converted checkpoints and attaches their conv weights; `blocks` has
+the SLAT sparse residual block on the fused norm / conv-epilogue kernels.
 
 The directory name is not a Python identifier; load it with
 `__graft_entry__.load()` (registered as the module `sam3d_amd`).
@@ -19,7 +20,7 @@ BACKEND = "hip"
 def __getattr__(name):
     # the torch.nn modules import lazily so that the map/oracle tooling does
     # not pay for them
-    if name in ("sparse", "tables", "gguf"):
+    if name in ("sparse", "tables", "gguf", "blocks"):
         import importlib
 
         return importlib.import_module(f".{name}", __name__)

@@ -85,8 +85,22 @@ def lib() -> ctypes.CDLL:
     L.spc_scatter_mean_workspace_bytes.argtypes = [_I64, _I64]
     L.spc_scatter_mean.argtypes = [_P, _INT, _P, _P, _P, _P, _I64, _I64, _I64, _P, _SZ]
     L.spc_gather_rows.argtypes = [_P, _INT, _P, _P, _P, _I64, _I64, _I64]
+    L.spc_layernorm_silu.argtypes = [_P, _INT, _P, _I64, _I64, _P, _P, ctypes.c_float, _INT, _P]
+    L.spc_sparse_conv_fused.argtypes = [_P, _INT, _P, _INT, _INT, _P, _P, _P, _P, _P, _INT, _P,
+                                        _P, _I64, _I64, _I64, _I64, _I64,
+                                        ctypes.POINTER(ConvEpilogue)]
     _lib = L
     return L
+
+
+EPI_NONE, EPI_RESIDUAL, EPI_NORM_MOD_SILU = 0, 1, 2
+
+
+class ConvEpilogue(ctypes.Structure):
+    """spc_conv_epilogue (include/sam3d_spconv_amd.h)."""
+    _fields_ = [("mode", ctypes.c_int32), ("eps", ctypes.c_float), ("residual", ctypes.c_void_p),
+                ("scale", ctypes.c_void_p), ("shift", ctypes.c_void_p),
+                ("coords", ctypes.c_void_p), ("n_batch", ctypes.c_int64)]
 
 
 def _check(fn: str, status: int) -> None:
@@ -324,12 +338,17 @@ def sparse_conv(x: torch.Tensor, weight, bias: torch.Tensor | None,
                 idx: torch.Tensor | None, *, ntaps: int, n_out: int,
                 idx_layout: int = IDX_TOKEN_MAJOR, row_perm: torch.Tensor | None = None,
                 w_scale: torch.Tensor | None = None, out: torch.Tensor | None = None,
-                cout: int | None = None, plan: torch.Tensor | None = None) -> torch.Tensor:
-    """y = conv(x) through spc_sparse_conv.  `weight` is a PackedWeights, a
-    [Cout, ntaps, Cin] tensor in the feature dtype, or int8 Q8_0 quants with
-    w_scale (fp16 block scales).  idx None with ntaps 1 is the identity map
-    (the dense 1x1x1 conv)."""
-    _need_gpu(x, bias, idx, row_perm, w_scale)
+                cout: int | None = None, plan: torch.Tensor | None = None,
+                residual: torch.Tensor | None = None,
+                norm_mod: tuple | None = None) -> torch.Tensor:
+    """y = conv(x) through spc_sparse_conv_fused.  `weight` is a
+    PackedWeights, a [Cout, ntaps, Cin] tensor in the feature dtype, or int8
+    Q8_0 quants with w_scale (fp16 block scales).  idx None with ntaps 1 is
+    the identity map (the dense 1x1x1 conv).  Epilogues: `residual`
+    ([n_out, Cout], feature dtype) is added to the rounded output;
+    `norm_mod` = (scale, shift, coords, eps) with f32 [n_batch, Cout] scale
+    and shift gives silu(norm(y) * (1 + scale[b]) + shift[b])."""
+    _need_gpu(x, bias, idx, row_perm, w_scale, residual)
     x = x.contiguous()
     dt = dtype_code(x.dtype)
     cin = x.shape[1]
@@ -357,10 +376,53 @@ def sparse_conv(x: torch.Tensor, weight, bias: torch.Tensor | None,
         bias = bias.contiguous()
     if out is None:
         out = torch.empty((n_out, cout), dtype=x.dtype, device=x.device)
-    st = lib().spc_sparse_conv_plan(_stream(x.device), dt, _ptr(x), wdt, layout, wptr, sptr,
-                                    _ptr(bias), _ptr(out), _ptr(idx), idx_layout, _ptr(row_perm),
-                                    _ptr(plan), ntaps, n_out, x.shape[0], cin, cout)
+    epi = ConvEpilogue(EPI_NONE, 0.0, None, None, None, None, 0)
+    keep = []
+    if residual is not None and norm_mod is not None:
+        raise ValueError("one epilogue at a time")
+    if residual is not None:
+        residual = residual.contiguous()
+        if residual.shape != (n_out, cout) or residual.dtype != x.dtype:
+            raise ValueError("residual must be [n_out, cout] in the feature dtype")
+        epi.mode, epi.residual = EPI_RESIDUAL, _ptr(residual)
+        keep.append(residual)
+    if norm_mod is not None:
+        scale, shift, coords, eps = norm_mod
+        _need_gpu(scale, shift, coords)
+        scale = scale.to(torch.float32).contiguous()
+        shift = shift.to(torch.float32).contiguous()
+        coords = coords.contiguous()
+        if scale.shape != shift.shape or scale.dim() != 2 or scale.shape[1] != cout:
+            raise ValueError("scale / shift must be [n_batch, cout]")
+        if coords.dtype != torch.int32 or coords.shape != (n_out, 4):
+            raise ValueError("coords must be int32 [n_out, 4]")
+        epi.mode, epi.eps = EPI_NORM_MOD_SILU, float(eps)
+        epi.scale, epi.shift, epi.coords = _ptr(scale), _ptr(shift), _ptr(coords)
+        epi.n_batch = scale.shape[0]
+        keep += [scale, shift, coords]
+    st = lib().spc_sparse_conv_fused(_stream(x.device), dt, _ptr(x), wdt, layout, wptr, sptr,
+                                     _ptr(bias), _ptr(out), _ptr(idx), idx_layout, _ptr(row_perm),
+                                     _ptr(plan), ntaps, n_out, x.shape[0], cin, cout,
+                                     ctypes.byref(epi))
     _check("spc_sparse_conv", st)
+    return out
+
+
+def layernorm_silu(x: torch.Tensor, weight: torch.Tensor | None = None,
+                   bias: torch.Tensor | None = None, eps: float = 1e-6, silu: bool = True,
+                   out: torch.Tensor | None = None) -> torch.Tensor:
+    """silu(LayerNorm32(x)) over the rows of x [n, c] (spc_layernorm_silu);
+    weight / bias the optional affine parameters."""
+    _need_gpu(x, weight, bias)
+    x = x.contiguous()
+    n, c = x.shape
+    w = None if weight is None else weight.detach().to(torch.float32).contiguous()
+    b = None if bias is None else bias.detach().to(torch.float32).contiguous()
+    if out is None:
+        out = torch.empty_like(x)
+    st = lib().spc_layernorm_silu(_stream(x.device), dtype_code(x.dtype), _ptr(x), n, c, _ptr(w),
+                                  _ptr(b), float(eps), int(bool(silu)), _ptr(out))
+    _check("spc_layernorm_silu", st)
     return out
 
 

@@ -309,6 +309,15 @@ int spc_sparse_conv_plan(spc_stream_t stream, int dtype, const void* x, int w_dt
                          void* y, const int32_t* idx, int idx_layout, const int32_t* row_perm,
                          const void* plan, int64_t ntaps, int64_t n_out, int64_t n_in,
                          int64_t cin, int64_t cout) {
+    return spc_sparse_conv_fused(stream, dtype, x, w_dtype, w_layout, w, w_scale, bias, y, idx,
+                                 idx_layout, row_perm, plan, ntaps, n_out, n_in, cin, cout, nullptr);
+}
+
+int spc_sparse_conv_fused(spc_stream_t stream, int dtype, const void* x, int w_dtype,
+                          int w_layout, const void* w, const void* w_scale, const void* bias,
+                          void* y, const int32_t* idx, int idx_layout, const int32_t* row_perm,
+                          const void* plan, int64_t ntaps, int64_t n_out, int64_t n_in,
+                          int64_t cin, int64_t cout, const spc_conv_epilogue* epi) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int st = check_shape("spc_sparse_conv", ntaps, cin, cout);
     if (st != SPC_OK) return st;
@@ -349,6 +358,36 @@ int spc_sparse_conv_plan(spc_stream_t stream, int dtype, const void* x, int w_dt
     }
     a.plan = plan;
     a.num_cu = device_cu_count();
+    if (epi && epi->mode != SPC_EPI_NONE) {
+        a.epi_mode = epi->mode;
+        if (epi->mode == SPC_EPI_RESIDUAL) {
+            if (!epi->residual || !aligned16(epi->residual)) {
+                set_last_error("spc_sparse_conv_fused: residual must be a 16-byte aligned pointer");
+                return SPC_BAD_ARG;
+            }
+            a.residual = epi->residual;
+        } else if (epi->mode == SPC_EPI_NORM_MOD_SILU) {
+            if (cout > 128) {
+                set_last_error("spc_sparse_conv_fused: the norm epilogue needs cout <= 128 (got %lld)",
+                               (long long)cout);
+                return SPC_BAD_SHAPE;
+            }
+            if (!epi->scale || !epi->shift || !epi->coords || !aligned16(epi->scale) ||
+                !aligned16(epi->shift) || epi->n_batch < 1 || !(epi->eps >= 0.0f)) {
+                set_last_error("spc_sparse_conv_fused: norm epilogue needs 16-byte aligned scale and "
+                               "shift, coords, n_batch >= 1 and eps >= 0");
+                return SPC_BAD_ARG;
+            }
+            a.epi_eps = epi->eps;
+            a.epi_scale = epi->scale;
+            a.epi_shift = epi->shift;
+            a.coords = epi->coords;
+            a.n_batch = epi->n_batch;
+        } else {
+            set_last_error("spc_sparse_conv_fused: unknown epilogue mode %d", epi->mode);
+            return SPC_BAD_ARG;
+        }
+    }
     hipError_t e = hipSuccess;
     if (w_dtype == SPC_Q8_0) {
         if (dtype != SPC_BF16) {

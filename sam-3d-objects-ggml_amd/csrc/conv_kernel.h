@@ -73,6 +73,14 @@ struct ConvArgs {
     int64_t tiles_per_xcd;
     const void* plan;         // per-row-tile setup from conv_plan_kernel, or null
     int32_t num_cu;           // compute units of the device (tile-width choice)
+    // fused epilogue (spc_conv_epilogue): SPC_EPI_NONE / _RESIDUAL / _NORM_MOD_SILU
+    int32_t epi_mode;
+    float epi_eps;
+    const void* residual;     // [n_out, cout] in the feature dtype
+    const float* epi_scale;   // [n_batch, cout]
+    const float* epi_shift;   // [n_batch, cout]
+    const int32_t* coords;    // [n_out, 4]: batch of each output row
+    int64_t n_batch;          // rows of epi_scale / epi_shift
 };
 
 // MFMA operand traits per activation type.
@@ -91,6 +99,8 @@ struct Mfma<__bf16> {
     __device__ static float ld(const void* p, int64_t i) {
         return bf16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
     }
+    __device__ static float round(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
+    __device__ static float unpack(uint32_t w, int h) { return __uint_as_float(h ? w & 0xffff0000u : w << 16); }
 };
 
 template <>
@@ -105,6 +115,8 @@ struct Mfma<_Float16> {
     __device__ static float ld(const void* p, int64_t i) {
         return f16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
     }
+    __device__ static float round(float v) { return f16_bits_to_f32(f32_to_f16_bits(v)); }
+    __device__ static float unpack(uint32_t w, int h) { return f16_bits_to_f32((uint16_t)(h ? w >> 16 : w)); }
 };
 
 template <>
@@ -119,6 +131,7 @@ struct Mfma<float> {
     __device__ static float ld(const void* p, int64_t i) {
         return static_cast<const float*>(p)[i];
     }
+    __device__ static float round(float v) { return v; }
 };
 
 // Weight-panel geometry shared by the packer and the kernel.  One panel =
@@ -869,6 +882,94 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
         }
     }
 
+    // ---- epilogue LayerNorm -> modulation -> SiLU over whole output rows
+    // (TN == cout: the tile holds every channel of its rows).  The rounded
+    // conv outputs go to an F32 LDS tile; groups of TN/4 lanes then take one
+    // row each (four channels per lane, four rows in flight per lane group),
+    // with group-local shuffles for the mean and the biased variance.
+    if (a.epi_mode == SPC_EPI_NORM_MOD_SILU) {
+        constexpr int FP = TN + 4;           // f32 row pitch (16-byte multiple)
+        static_assert(TM * FP * 4 <= 2 * STAGE * 16, "f32 output tile fits the A stage");
+        constexpr int G = TN / 4;            // lanes per row
+        constexpr int RW = 64 / G;           // rows per wave at a time
+        constexpr int RB = 4;                // row groups in flight per lane
+        static_assert(TM % (NW * RW * RB) == 0, "norm epilogue geometry");
+        float* of = reinterpret_cast<float*>(Au);
+        lds_barrier();  // every wave is done with the A stage
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            const int rl = wm * WTM + i * 32 + (lane & 31);
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int cl = wn * WTN + j * 32 + 8 * g + 4 * (lane >> 5);
+                    *reinterpret_cast<floatx4*>(of + rl * FP + cl) =
+                        floatx4{M::round(acc[i][j][4 * g]), M::round(acc[i][j][4 * g + 1]),
+                                M::round(acc[i][j][4 * g + 2]), M::round(acc[i][j][4 * g + 3])};
+                }
+        }
+        lds_barrier();
+        const int gl = lane % G;
+        const int c0 = 4 * gl;
+        char* yb = static_cast<char*>(a.y);
+        for (int it = 0; it < TM / (NW * RW * RB); ++it) {
+            float v[RB][4];
+            int32_t t[RB];
+            float s[RB], q[RB];
+#pragma unroll
+            for (int k = 0; k < RB; ++k) {
+                const int r = ((it * RB + k) * NW + wave) * RW + lane / G;
+                t[k] = srow[r];
+                const floatx4 f = *reinterpret_cast<const floatx4*>(of + r * FP + c0);
+                v[k][0] = f.x; v[k][1] = f.y; v[k][2] = f.z; v[k][3] = f.w;
+                s[k] = (v[k][0] + v[k][1]) + (v[k][2] + v[k][3]);
+            }
+#pragma unroll
+            for (int off = G / 2; off > 0; off >>= 1)
+#pragma unroll
+                for (int k = 0; k < RB; ++k) s[k] += __shfl_xor(s[k], off);
+#pragma unroll
+            for (int k = 0; k < RB; ++k) {
+                const float mean = s[k] / (float)TN;
+                q[k] = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    v[k][e] -= mean;
+                    q[k] += v[k][e] * v[k][e];
+                }
+            }
+#pragma unroll
+            for (int off = G / 2; off > 0; off >>= 1)
+#pragma unroll
+                for (int k = 0; k < RB; ++k) q[k] += __shfl_xor(q[k], off);
+#pragma unroll
+            for (int k = 0; k < RB; ++k) {
+                if (t[k] < 0) continue;
+                const float rstd = 1.0f / sqrtf(q[k] / (float)TN + a.epi_eps);
+                const int64_t b = min(max((int64_t)a.coords[(int64_t)t[k] * 4], (int64_t)0), a.n_batch - 1);
+                const floatx4 sc = *reinterpret_cast<const floatx4*>(a.epi_scale + b * a.cout + c0);
+                const floatx4 sh = *reinterpret_cast<const floatx4*>(a.epi_shift + b * a.cout + c0);
+                float o[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float u = M::round(v[k][e] * rstd);           // norm2 (LayerNorm32)
+                    const float m = M::round(M::round(u * M::round(1.0f + sc[e])) + sh[e]);
+                    o[e] = m / (1.0f + expf(-m));                        // SiLU
+                }
+                char* dst = yb + ((int64_t)t[k] * a.cout + c0) * ES;
+                if constexpr (ES == 4) {
+                    *reinterpret_cast<floatx4*>(dst) = floatx4{o[0], o[1], o[2], o[3]};
+                } else {
+                    *reinterpret_cast<u32x2*>(dst) =
+                        u32x2{(uint32_t)M::cvt(o[0]) | ((uint32_t)M::cvt(o[1]) << 16),
+                              (uint32_t)M::cvt(o[2]) | ((uint32_t)M::cvt(o[3]) << 16)};
+                }
+            }
+        }
+        return;
+    }
+
     // ---- epilogue: + bias in F32, one rounding.  Each lane holds four runs
     // of four consecutive channels of one row; they go to an LDS output
     // tile (8-byte writes, 16 in f32), then whole rows leave with coalesced
@@ -924,6 +1025,34 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
             const u32x2 hi = *reinterpret_cast<const u32x2*>(src + 8);
             vv[k] = u32x4{lo.x, lo.y, hi.x, hi.y};
         }
+        if (a.epi_mode == SPC_EPI_RESIDUAL) {
+            // y = dt(dt(conv + bias) + residual): the rounded conv output
+            // plus the residual row, added in F32 and rounded once more
+            u32x4 rv[NU];
+#pragma unroll
+            for (int k = 0; k < NU; ++k) {
+                const int q = (tid + k * NT) % UPR;
+                rv[k] = tt[k] >= 0 ? *reinterpret_cast<const u32x4*>(
+                                         static_cast<const char*>(a.residual) +
+                                         ((int64_t)tt[k] * a.cout + co0) * ES + q * 16)
+                                   : vv[k];
+            }
+#pragma unroll
+            for (int k = 0; k < NU; ++k) {
+                if constexpr (ES == 4) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        vv[k][e] = __float_as_uint(__uint_as_float(vv[k][e]) + __uint_as_float(rv[k][e]));
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float lo = M::unpack(vv[k][e], 0) + M::unpack(rv[k][e], 0);
+                        const float hi = M::unpack(vv[k][e], 1) + M::unpack(rv[k][e], 1);
+                        vv[k][e] = (uint32_t)M::cvt(lo) | ((uint32_t)M::cvt(hi) << 16);
+                    }
+                }
+            }
+        }
 #pragma unroll
         for (int k = 0; k < NU; ++k) {
             const int c = tid + k * NT;
@@ -957,6 +1086,10 @@ hipError_t dispatch_tn(hipStream_t s, const ConvArgs& a) {
     const int64_t tiles_m = ceil_div(a.n_out, kTM);
     int tn = a.cout % 128 == 0 ? 128 : a.cout % 64 == 0 ? 64 : 32;
     while (tn > 32 && tiles_m * (a.cout / (tn / 2)) <= a.num_cu) tn /= 2;
+    if (a.epi_mode == SPC_EPI_NORM_MOD_SILU) {
+        if (a.cout > 128) return hipErrorInvalidValue;  // rows wider than one tile
+        tn = a.cout;                                    // one tile covers the row
+    }
     if (tn == 128) {
         if constexpr (Q8) return launch_conv<T, Q8, PACKED, NTAPS, 128, 2, 2>(s, a);
         else return launch_conv<T, Q8, PACKED, NTAPS, 128, 4, 2>(s, a);

@@ -42,7 +42,7 @@ from . import _native as nat
 __all__ = [
     "SparseTensor", "SparseTensorData", "sparse_batch_broadcast", "sparse_batch_op",
     "sparse_cat", "sparse_unbind", "SparseConv3d", "SparseInverseConv3d",
-    "SparseDownsample", "SparseUpsample", "SparseSubdivide",
+    "SparseDownsample", "SparseUpsample", "SparseSubdivide", "SparseLinear",
 ]
 
 BACKEND = "hip"
@@ -551,11 +551,14 @@ class _ConvCore:
         return b.contiguous()
 
     def _conv(self, feats: torch.Tensor, idx: Optional[torch.Tensor], n_out: int,
-              plan: Optional[torch.Tensor] = None) -> torch.Tensor:
+              plan: Optional[torch.Tensor] = None, residual: Optional[torch.Tensor] = None,
+              norm_mod: Optional[tuple] = None) -> torch.Tensor:
         c = self.conv
         if feats.dim() != 2 or feats.shape[1] != c.in_channels:
             raise ValueError(f"expected feats [N, {c.in_channels}], got {tuple(feats.shape)}")
         nat._need_gpu(feats)
+        if (residual is not None or norm_mod is not None) and c.out_channels % 32:
+            raise ValueError("fused epilogues need out_channels a multiple of 32")
 
         def run():
             x = feats.detach().contiguous()
@@ -564,7 +567,9 @@ class _ConvCore:
                 x = torch.nn.functional.pad(x, (0, cin_p - c.in_channels))
             w = self._weight_operand(x.dtype, x.device)
             b = self._bias_operand(x.dtype, x.device)
-            y = nat.sparse_conv(x, w, b, idx, ntaps=self._ntaps, n_out=n_out, plan=plan)
+            r = None if residual is None else residual.detach().to(x.dtype)
+            y = nat.sparse_conv(x, w, b, idx, ntaps=self._ntaps, n_out=n_out, plan=plan,
+                                residual=r, norm_mod=norm_mod)
             if y.shape[1] != c.out_channels:
                 y = y[:, : c.out_channels].contiguous()
             return y
@@ -603,17 +608,34 @@ class SparseConv3d(nn.Module, _ConvCore):
         self._init_core(ntaps, raw_view=(kind == "subm1"))
 
     def forward(self, x: SparseTensor) -> SparseTensor:
+        return self.forward_fused(x)
+
+    def forward_fused(self, x: SparseTensor, residual: Optional[torch.Tensor] = None,
+                      norm_mod: Optional[tuple] = None) -> SparseTensor:
+        """forward() with a fused epilogue on the output rows (submanifold
+        convs only): `residual` [N, Cout] is added to the rounded output
+        (`h = conv2(h); h = h + skip`), `norm_mod` = (scale, shift, eps) with
+        per-batch [B, Cout] scale / shift gives silu(norm(y) * (1 + scale)
+        + shift) (structured_latent_flow.py:69-71; Cout <= 128)."""
         spatial_changed = any(s != 1 for s in self.stride) or (self.padding is not None)
         new_shape = torch.Size([x.shape[0], self.conv.out_channels])
         scale = tuple(s * k for s, k in zip(x._scale, self.stride))
+        nm = None
+        if norm_mod is not None:
+            sc, sh, eps = norm_mod
+            nm = (sc, sh, x.coords, eps)
+        if (residual is not None or nm is not None) and self._kind not in ("subm3", "subm1"):
+            raise ValueError("fused epilogues apply to submanifold convs")
         if self._kind == "subm3":
             m = _subm_map(x)
             n = x.feats.shape[0]
-            feats = self._conv(x.feats, m.token_major, n, _plan(x, "subm3", m.token_major, 27, n, n))
+            feats = self._conv(x.feats, m.token_major, n, _plan(x, "subm3", m.token_major, 27, n, n),
+                               residual=residual, norm_mod=nm)
             data = x.data.replace_feature(feats)
         elif self._kind == "subm1":
             n = x.feats.shape[0]
-            feats = self._conv(x.feats, None, n, _plan(x, "dense1", None, 1, n, n))
+            feats = self._conv(x.feats, None, n, _plan(x, "dense1", None, 1, n, n),
+                               residual=residual, norm_mod=nm)
             data = x.data.replace_feature(feats)
         else:
             d = _downsample_map(x)
@@ -674,6 +696,13 @@ class SparseInverseConv3d(nn.Module, _ConvCore):
 # ---------------------------------------------------------------------------
 # spatial ops (SP/spatial.py)
 # ---------------------------------------------------------------------------
+class SparseLinear(nn.Linear):
+    """nn.Linear over the feats of a SparseTensor (SP/linear.py:9-15)."""
+
+    def forward(self, input: SparseTensor) -> SparseTensor:
+        return input.replace(super().forward(input.feats))
+
+
 def _factor3(f) -> Tuple[int, int, int]:
     return tuple(f) if isinstance(f, (list, tuple)) else (f,) * 3
 
