@@ -93,13 +93,10 @@ __device__ __forceinline__ void dma_barrier() {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-// Round-to-nearest-even float -> bf16 / f16 bits (device), from the formats'
-// definitions; NaN payloads are quieted.
+// Round-to-nearest-even float -> bf16 / f16 bits (device): the gfx950
+// hardware converts (v_cvt_pk_bf16_f32, v_cvt_f16_f32); NaNs stay NaNs.
 __device__ inline uint16_t f32_to_bf16_bits(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
+    return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 __device__ inline float bf16_bits_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 
@@ -109,6 +106,13 @@ __device__ inline uint16_t f32_to_f16_bits(float f) {
 }
 __device__ inline float f16_bits_to_f32(uint16_t h) {
     return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// x * sigmoid(x) = x / (1 + e^-x) with the hardware exp2 and reciprocal
+// (each within a few F32 ulps; the results are rounded to bf16 / f16 or
+// compared with a tolerance).
+__device__ inline float silu_f32(float x) {
+    return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x));
 }
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }

@@ -955,7 +955,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
                 for (int e = 0; e < 4; ++e) {
                     const float u = M::round(v[k][e] * rstd);           // norm2 (LayerNorm32)
                     const float m = M::round(M::round(u * M::round(1.0f + sc[e])) + sh[e]);
-                    o[e] = m / (1.0f + expf(-m));                        // SiLU
+                    o[e] = silu_f32(m);                                  // SiLU
                 }
                 char* dst = yb + ((int64_t)t[k] * a.cout + c0) * ES;
                 if constexpr (ES == 4) {

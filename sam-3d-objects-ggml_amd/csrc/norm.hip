@@ -63,8 +63,9 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
-// G lanes per row, NV runs of 4 per lane (c <= 4 * G * NV)
-template <int DT, int G, int NV>
+// G lanes per row, NV runs of 4 per lane (c <= 4 * G * NV), R rows per lane
+// group (rows r, r + groups, ...: R independent reductions in flight)
+template <int DT, int G, int NV, int R>
 __global__ __launch_bounds__(256) void layernorm_silu_kernel(const void* __restrict__ x, int64_t n,
                                                              int c, const float* __restrict__ gamma,
                                                              const float* __restrict__ beta,
@@ -72,75 +73,112 @@ __global__ __launch_bounds__(256) void layernorm_silu_kernel(const void* __restr
                                                              void* __restrict__ y) {
     using E = Elem<DT>;
     const int lane = threadIdx.x & 63;
-    const int64_t row = ((int64_t)blockIdx.x * 256 + threadIdx.x) / G;
-    const int gl = lane % G;  // lane within the row's group
-    const bool live = row < n;
-    float v[NV][4];
-    float s = 0.0f;
+    constexpr int GPB = 256 / G;  // row groups per block
+    const int64_t row0 = (int64_t)blockIdx.x * GPB * R + threadIdx.x / G;
+    const int gl = lane % G;      // lane within the row's group
+    float v[R][NV][4];
+    float gv[NV][4], bv[NV][4];
+    float s[R], q[R];
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
         const int c0 = 4 * (gl + G * k);
-        if (live && c0 < c) E::ld4(x, row * c + c0, v[k]);
-        else v[k][0] = v[k][1] = v[k][2] = v[k][3] = 0.0f;
-        s += (v[k][0] + v[k][1]) + (v[k][2] + v[k][3]);
+        const bool in = c0 < c;
+        const floatx4 g4 = gamma && in ? *reinterpret_cast<const floatx4*>(gamma + c0)
+                                       : floatx4{1.f, 1.f, 1.f, 1.f};
+        const floatx4 b4 = beta && in ? *reinterpret_cast<const floatx4*>(beta + c0)
+                                      : floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            gv[k][e] = g4[e];
+            bv[k][e] = b4[e];
+        }
     }
-    const float mean = group_sum<G>(s) / (float)c;
-    float q = 0.0f;
 #pragma unroll
-    for (int k = 0; k < NV; ++k) {
-        if (4 * (gl + G * k) < c) {
+    for (int r = 0; r < R; ++r) {
+        const int64_t row = row0 + (int64_t)r * GPB;
+        s[r] = 0.0f;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float d = v[k][e] - mean;
-                q += d * d;
+        for (int k = 0; k < NV; ++k) {
+            const int c0 = 4 * (gl + G * k);
+            if (row < n && c0 < c) E::ld4(x, row * c + c0, v[r][k]);
+            else v[r][k][0] = v[r][k][1] = v[r][k][2] = v[r][k][3] = 0.0f;
+            s[r] += (v[r][k][0] + v[r][k][1]) + (v[r][k][2] + v[r][k][3]);
+        }
+    }
+#pragma unroll
+    for (int off = G / 2; off > 0; off >>= 1)
+#pragma unroll
+        for (int r = 0; r < R; ++r) s[r] += __shfl_xor(s[r], off);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const float mean = s[r] / (float)c;
+        q[r] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            if (4 * (gl + G * k) < c) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    v[r][k][e] -= mean;
+                    q[r] += v[r][k][e] * v[r][k][e];
+                }
             }
         }
     }
-    const float rstd = 1.0f / sqrtf(group_sum<G>(q) / (float)c + eps);
-    if (!live) return;
 #pragma unroll
-    for (int k = 0; k < NV; ++k) {
-        const int c0 = 4 * (gl + G * k);
-        if (c0 >= c) continue;
-        float o[4];
+    for (int off = G / 2; off > 0; off >>= 1)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            float u = (v[k][e] - mean) * rstd;
-            if (gamma) u *= gamma[c0 + e];
-            if (beta) u += beta[c0 + e];
-            u = E::round(u);  // LayerNorm32 casts back to the feature dtype
-            if (silu) u = u / (1.0f + expf(-u));
-            o[e] = u;
+        for (int r = 0; r < R; ++r) q[r] += __shfl_xor(q[r], off);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int64_t row = row0 + (int64_t)r * GPB;
+        if (row >= n) continue;
+        const float rstd = 1.0f / sqrtf(q[r] / (float)c + eps);
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const int c0 = 4 * (gl + G * k);
+            if (c0 >= c) continue;
+            float o[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float u = v[r][k][e] * rstd;
+                if (gamma) u *= gv[k][e];
+                if (beta) u += bv[k][e];
+                u = E::round(u);  // LayerNorm32 casts back to the feature dtype
+                if (silu) u = silu_f32(u);
+                o[e] = u;
+            }
+            E::st4(y, row * c + c0, o);
         }
-        E::st4(y, row * c + c0, o);
     }
+}
+
+template <int DT, int G, int NV, int R>
+void launch_g(hipStream_t s, const void* x, int64_t n, int c, const float* gamma, const float* beta,
+              float eps, int silu, void* y) {
+    const dim3 grid((unsigned)ceil_div(n, (int64_t)(256 / G) * R));
+    layernorm_silu_kernel<DT, G, NV, R><<<grid, dim3(256), 0, s>>>(x, n, c, gamma, beta, eps, silu, y);
 }
 
 template <int DT>
 hipError_t launch_norm(hipStream_t s, const void* x, int64_t n, int c, const float* gamma,
                        const float* beta, float eps, int silu, void* y) {
     const int runs = c / 4;
-    const dim3 block(256);
     if (runs <= 64) {
         // G = smallest power of two >= runs: several rows per wave
         int g = 1;
         while (g < runs) g <<= 1;
-        const int64_t rows_per_block = 256 / g;
-        const dim3 grid((unsigned)ceil_div(n, rows_per_block));
         switch (g) {
-            case 1: layernorm_silu_kernel<DT, 1, 1><<<grid, block, 0, s>>>(x, n, c, gamma, beta, eps, silu, y); break;
-            case 2: layernorm_silu_kernel<DT, 2, 1><<<grid, block, 0, s>>>(x, n, c, gamma, beta, eps, silu, y); break;
-            case 4: layernorm_silu_kernel<DT, 4, 1><<<grid, block, 0, s>>>(x, n, c, gamma, beta, eps, silu, y); break;
-            case 8: layernorm_silu_kernel<DT, 8, 1><<<grid, block, 0, s>>>(x, n, c, gamma, beta, eps, silu, y); break;
-            case 16: layernorm_silu_kernel<DT, 16, 1><<<grid, block, 0, s>>>(x, n, c, gamma, beta, eps, silu, y); break;
-            case 32: layernorm_silu_kernel<DT, 32, 1><<<grid, block, 0, s>>>(x, n, c, gamma, beta, eps, silu, y); break;
-            default: layernorm_silu_kernel<DT, 64, 1><<<grid, block, 0, s>>>(x, n, c, gamma, beta, eps, silu, y); break;
+            case 1: launch_g<DT, 1, 1, 1>(s, x, n, c, gamma, beta, eps, silu, y); break;
+            case 2: launch_g<DT, 2, 1, 1>(s, x, n, c, gamma, beta, eps, silu, y); break;
+            case 4: launch_g<DT, 4, 1, 1>(s, x, n, c, gamma, beta, eps, silu, y); break;
+            case 8: launch_g<DT, 8, 1, 1>(s, x, n, c, gamma, beta, eps, silu, y); break;
+            case 16: launch_g<DT, 16, 1, 1>(s, x, n, c, gamma, beta, eps, silu, y); break;
+            case 32: launch_g<DT, 32, 1, 1>(s, x, n, c, gamma, beta, eps, silu, y); break;
+            default: launch_g<DT, 64, 1, 1>(s, x, n, c, gamma, beta, eps, silu, y); break;
         }
     } else {
         // one row per wave, up to 8 runs of 4 per lane
-        const dim3 grid((unsigned)ceil_div(n, 4));
-        layernorm_silu_kernel<DT, 64, kNormMaxC / 256><<<grid, block, 0, s>>>(x, n, c, gamma, beta, eps,
-                                                                             silu, y);
+        launch_g<DT, 64, kNormMaxC / 256, 1>(s, x, n, c, gamma, beta, eps, silu, y);
     }
     return hipGetLastError();
 }
@@ -163,8 +201,9 @@ int spc_layernorm_silu(spc_stream_t stream, int dtype, const void* x, int64_t n,
     }
     if (n == 0) return SPC_OK;
     const size_t align = dtype == SPC_F32 ? 16 : 8;
-    if (!x || !y || ((uintptr_t)x % align) || ((uintptr_t)y % align)) {
-        set_last_error("spc_layernorm_silu: null or misaligned pointer");
+    if (!x || !y || ((uintptr_t)x % align) || ((uintptr_t)y % align) || ((uintptr_t)gamma % 16) ||
+        ((uintptr_t)beta % 16)) {
+        set_last_error("spc_layernorm_silu: null or misaligned pointer (gamma / beta 16-byte aligned)");
         return SPC_BAD_ARG;
     }
     hipError_t e;
