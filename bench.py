@@ -45,7 +45,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5, 6],
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5, 6, 7],
                     help="2 = the headline workload; others print diagnostic lines")
     ap.add_argument("--order", choices=["natural", "mask"], default="natural",
                     help="row processing order of the conv kernel")
@@ -260,6 +260,13 @@ def main():
         batch = 4
         workload = ("SLAT sparse residual block (LayerNorm32, SiLU, subm3x3x3, LayerNorm, "
                     "modulation, SiLU, subm3x3x3, + skip), bf16 C=128, 4 ellipsoid shells 64^3")
+    elif cfg == 7:
+        coords = wl.sphere_shell()
+        cin, cout = 768, 192
+        batch = 1
+        workload = ("mesh-decoder upsample block (GroupNorm32, SiLU, subdivide, subm3x3x3 "
+                    "768->192, GroupNorm32, SiLU, subm3x3x3, + 1x1x1 skip), bf16, sphere shell "
+                    "64^3 -> 128^3")
     else:
         coords = wl.sphere_shell()
         cin = cout = 64
@@ -385,6 +392,8 @@ def main():
                   "pct_peak_subm": 100 * f2 / (ms2 / 1e3) / 1e12 / PEAK_BF16_TFLOPS}
     elif cfg == 6:
         result = bench_res_block(spc, nat, wl, orc, coords, c_dev, dev, args, workload)
+    elif cfg == 7:
+        result = bench_subdivide_block(spc, nat, wl, orc, coords, c_dev, dev, args, workload)
     else:
         keeps = wl.prune_masks(n)
         lv = []
@@ -451,6 +460,57 @@ def bench_res_block(spc, nat, wl, orc, coords, c_dev, dev, args, workload):
             "ms_per_step": ms_f, "unfused_ms": ms_u, "speedup": ms_u / ms_f, "dtype": "bf16",
             "max_abs_diff_fused_vs_unfused": diff,
             "config": {"workload": workload, "n_voxels": n, "channels": 128, "batch": 4}}
+
+
+def bench_subdivide_block(spc, nat, wl, orc, coords, c_dev, dev, args, workload):
+    """SparseSubdivideBlock3d forward (768 -> 192, the first mesh-decoder
+    upsample block) on the fused path against the same block with separate
+    GroupNorm, SiLU, gather and residual passes.  Both include the child
+    map build, as the block builds it on every call."""
+    import torch
+
+    sp = spc.sparse
+    n = coords.shape[0]
+    torch.manual_seed(0)
+    blk = spc.blocks.SparseSubdivideBlock3d(768, 64, 192).to(dev)
+    with torch.no_grad():
+        for p in blk.out_layers[3].parameters():
+            p.normal_(0, 0.02)
+    blk = blk.to(torch.bfloat16)
+    blk.act_layers[0].float()
+    blk.out_layers[1].float()
+    x, _ = bf16_dev(orc, wl.normal((n, 768), 1.0, seed=701), dev)
+    xt = sp.SparseTensor(x, c_dev)
+    gn0, gn1 = blk.act_layers[0], blk.out_layers[1]
+
+    def fused():
+        with torch.no_grad():
+            return blk(xt)
+
+    def unfused():
+        with torch.no_grad():
+            coords, parent = blk.sub.map(xt)
+            h = nat.group_norm_silu(xt.feats, sp.batch_offsets(xt), 32, gn0.weight, gn0.bias,
+                                    gn0.eps, silu=False)
+            h = torch.nn.functional.silu(h)
+            h = blk.sub.assemble(xt, coords, nat.gather_rows(h, parent))
+            xs = blk.sub.assemble(xt, coords, nat.gather_rows(xt.feats, parent))
+            h = blk.out_layers[0](h)
+            h = h.replace(torch.nn.functional.silu(nat.group_norm_silu(
+                h.feats, sp.batch_offsets(h), 32, gn1.weight, gn1.bias, gn1.eps, silu=False)))
+            h = blk.out_layers[3](h)
+            return h + blk.skip_connection(xs)
+
+    ms_f, _ = time_gpu(fused, args.steps, args.warmup)
+    ms_u, _ = time_gpu(unfused, args.steps, args.warmup)
+    yf = fused()
+    nc = yf.feats.shape[0]
+    diff = float((yf.feats.float() - unfused().feats.float()).abs().max())
+    return {"metric": f"config 7: {workload}", "value": nc / (ms_f / 1e3) / 1e6, "unit": "Mvoxel/s",
+            "ms_per_step": ms_f, "unfused_ms": ms_u, "speedup": ms_u / ms_f, "dtype": "bf16",
+            "max_abs_diff_fused_vs_unfused": diff,
+            "config": {"workload": workload, "n_parents": n, "n_children": nc, "cin": 768,
+                       "cout": 192}}
 
 
 if __name__ == "__main__":

@@ -131,6 +131,17 @@ int spc_stride2_inverse_taps(spc_stream_t stream, const int32_t* coords,
                              const int32_t* fine_to_coarse, int64_t nf, int64_t nc,
                              int32_t* taps);
 
+/* Index composition: out[i] = rows[idx[i]] for idx[i] in [0, n_rows), else
+ * -1 (idx and out 16-byte aligned).  With idx a neighbour table over
+ * subdivided children and rows the children's parent rows (the `parent`
+ * output of spc_subdivide_map), a conv on the composed table reads the
+ * parents' features directly: SparseSubdivide's child features are copies
+ * of the parent rows (SP/spatial.py:120-127), so the result equals the conv
+ * over the copied rows exactly, without writing the copies.  No reference
+ * counterpart: the reference materialises the copies. */
+int spc_compose_rows(spc_stream_t stream, const int32_t* idx, int64_t n, const int32_t* rows,
+                     int64_t n_rows, int32_t* out);
+
 /* ------------------------------------------------------------------------
  * Subdivide map.  Replaces subdivide_mesh_level (SRC/sparse_ops.cpp:
  * 348-371) and SparseSubdivide's coordinates (SP/spatial.py:108-124).
@@ -277,6 +288,30 @@ int spc_gather_rows(spc_stream_t stream, int dtype, const void* src, const int32
 int spc_layernorm_silu(spc_stream_t stream, int dtype, const void* x, int64_t n, int64_t c,
                        const float* gamma, const float* beta, float eps, int silu, void* y);
 
+/* GroupNorm over each batch item's rows (SparseGroupNorm32,
+ * modules/sparse/norm.py:15-55: per item, the statistics of each group of
+ * c / groups channels over all of the item's rows; biased variance, eps
+ * inside the square root; computed in F32 and cast back).  Rows of item b
+ * are [offsets[b], offsets[b+1]) (offsets: device int64 [n_batch + 1],
+ * ascending); max_rows bounds the rows of one item.
+ *   spc_group_norm_stats: stats (device f32 [n_batch, groups, 2]) =
+ *     (mean, 1 / sqrt(var + eps)); F64 partial sums in a fixed order
+ *     (deterministic), workspace of spc_group_norm_workspace_bytes.
+ *   spc_group_norm_silu: y[i] = dt(silu(dt((x[r] - mean) * rstd * gamma +
+ *     beta))) with r = rows[i] (rows NULL: r = i) -- the norm, SiLU and
+ *     SparseSubdivide's parent gather of SparseSubdivideBlock3d's act_layers
+ *     (decoder_mesh.py:69-73) in one pass; silu 0 skips the activation;
+ *     gamma / beta f32 [c] or NULL.
+ * c <= 1024, a multiple of 4 and of groups. */
+size_t spc_group_norm_workspace_bytes(int64_t n_batch, int64_t max_rows, int64_t groups);
+int spc_group_norm_stats(spc_stream_t stream, int dtype, const void* x, int64_t c, int64_t groups,
+                         const int64_t* offsets, int64_t n_batch, int64_t max_rows, float eps,
+                         float* stats, void* workspace, size_t workspace_bytes);
+int spc_group_norm_silu(spc_stream_t stream, int dtype, const void* x, int64_t n_src, int64_t c,
+                        int64_t groups, const int64_t* offsets, int64_t n_batch, const float* stats,
+                        const float* gamma, const float* beta, int silu, const int32_t* rows,
+                        int64_t n_out, void* y);
+
 /* Conv epilogues, applied to the output rows before they are stored:
  *   SPC_EPI_RESIDUAL       y = dt(dt(conv + bias) + residual[t])
  *                          (`h = conv2(h); h = h + skip`, :72-73);
@@ -286,7 +321,10 @@ int spc_layernorm_silu(spc_stream_t stream, int dtype, const void* x, int64_t n,
  *                          y = dt(silu(m)), b = coords[4 t] the row's batch
  *                          (`norm2(h) * (1 + scale) + shift`, then SiLU,
  *                          :70-71), where dt() rounds to the feature dtype.
- * residual: [n_out, cout] in dtype.  scale / shift: f32 [n_batch, cout]
+ * residual: [n_out, cout] in dtype, or, with residual_rows set, [n_residual,
+ * cout] read at row residual_rows[t] (entries outside [0, n_residual) add
+ * nothing): the subdivide block adds its skip computed on the parent rows
+ * (decoder_mesh.py:82).  scale / shift: f32 [n_batch, cout]
  * holding dtype values (emb_out.type(x.dtype)).  NORM_MOD_SILU needs
  * cout <= 128 (one tile covers a whole output row). */
 typedef enum { SPC_EPI_NONE = 0, SPC_EPI_RESIDUAL = 1, SPC_EPI_NORM_MOD_SILU = 2 } spc_epilogue_mode;
@@ -298,6 +336,8 @@ typedef struct {
     const float* shift;
     const int32_t* coords;
     int64_t n_batch;
+    const int32_t* residual_rows;
+    int64_t n_residual;
 } spc_conv_epilogue;
 
 /* spc_sparse_conv_plan with an epilogue (epi NULL or mode SPC_EPI_NONE:

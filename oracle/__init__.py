@@ -364,3 +364,74 @@ def res_block(o: "_Oracle", x: np.ndarray, table: np.ndarray, p: dict, scale: np
     h = conv(h, p["conv2_w"], p["conv2_b"])
     skip = x if "skip_w" not in p else r(x @ p["skip_w"].T.astype(np.float32) + p["skip_b"])
     return r(h + skip)
+
+
+def batch_offsets(batch: np.ndarray, n_batch: int | None = None) -> np.ndarray:
+    """Row offsets [B + 1] of rows sorted by batch index."""
+    batch = np.asarray(batch)
+    nb = int(batch.max()) + 1 if n_batch is None else n_batch
+    return np.concatenate([[0], np.cumsum(np.bincount(batch, minlength=nb))]).astype(np.int64)
+
+
+def group_norm_items(a: np.ndarray, offsets: np.ndarray, groups: int, gamma=None, beta=None,
+                     eps: float = 1e-5) -> np.ndarray:
+    """SparseGroupNorm (modules/sparse/norm.py:15-46): per batch item (rows
+    offsets[b] .. offsets[b+1]), nn.GroupNorm over [1, C, rows]: each group
+    of C / groups channels normalised with the mean and biased variance of
+    all its values in the item, then the per-channel affine.  F32 result."""
+    a = np.asarray(a, dtype=np.float32)
+    out = np.zeros_like(a)
+    c = a.shape[1]
+    cpg = c // groups
+    for b in range(len(offsets) - 1):
+        blk = a[offsets[b]:offsets[b + 1]]
+        if blk.shape[0] == 0:
+            continue
+        g = blk.reshape(blk.shape[0], groups, cpg).astype(np.float64)
+        mean = g.mean(axis=(0, 2), keepdims=True)
+        var = ((g - mean) ** 2).mean(axis=(0, 2), keepdims=True)
+        y = ((g - mean) / np.sqrt(var + eps)).reshape(blk.shape).astype(np.float32)
+        if gamma is not None:
+            y = y * np.asarray(gamma, np.float32)
+        if beta is not None:
+            y = y + np.asarray(beta, np.float32)
+        out[offsets[b]:offsets[b + 1]] = y
+    return out
+
+
+def subdivide_block(o: "_Oracle", x: np.ndarray, coords: np.ndarray, p: dict, groups: int,
+                    dtype: int = BF16):
+    """SparseSubdivideBlock3d.forward (decoder_mesh.py:69-83): h =
+    dt(silu(dt(GN(x)))) gathered to the children (SparseSubdivide order,
+    spatial.py:108-130), conv1, dt(silu(dt(GN))), conv2, + skip(subdivide(x))
+    with skip the 1x1x1 conv (the spconv raw view W[co][ci] = buf[ci*Cout +
+    co], SRC/mesh_decoder_graph.cpp:349-384) or the identity.  p: float32
+    gn0_w, gn0_b, conv1_w [Co,27,Ci], conv1_b, gn1_w, gn1_b, conv2_w,
+    conv2_b, optional skip_w (the [Co,1,1,1,Ci] buffer) and skip_b.
+    Returns (child coords, features)."""
+    r = lambda a: round_to(o, a, dtype)  # noqa: E731
+    bits = {F32: lambda a: np.ascontiguousarray(a, np.float32), BF16: o.f32_to_bf16,
+            F16: o.f32_to_f16}[dtype]
+
+    def conv(h, w, b, table, ntaps):
+        y = o.sparse_conv(bits(h), bits(w), bits(b), table, ntaps=ntaps, n_out=h.shape[0],
+                          idx_layout=1, out_dtype=F32, x_dtype=dtype, w_dtype=dtype, b_dtype=dtype)
+        return r(y)
+
+    child, parent = o.subdivide(coords)
+    offs_p = batch_offsets(coords[:, 0])
+    h = r(silu(r(group_norm_items(x, offs_p, groups, p["gn0_w"], p["gn0_b"]))))[parent]
+    table = o.conv_table_slat(child)
+    h = conv(h, p["conv1_w"], p["conv1_b"], table, 27)
+    offs_c = batch_offsets(child[:, 0])
+    h = r(silu(r(group_norm_items(h, offs_c, groups, p["gn1_w"], p["gn1_b"]))))
+    h = conv(h, p["conv2_w"], p["conv2_b"], table, 27)
+    xs = x[parent]
+    if "skip_w" in p:
+        co, ci = p["conv2_w"].shape[0], x.shape[1]
+        w_eff = p["skip_w"].reshape(-1).reshape(ci, co).T.reshape(co, 1, ci)
+        ident = np.arange(xs.shape[0], dtype=np.int32)
+        skip = conv(xs, w_eff, p["skip_b"], ident, 1)
+    else:
+        skip = xs
+    return child, r(h + skip)

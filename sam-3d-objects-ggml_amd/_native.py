@@ -63,6 +63,7 @@ def lib() -> ctypes.CDLL:
     L.spc_downsample_workspace_bytes.argtypes = [_I64]
     L.spc_downsample_map.argtypes = [_P, _P, _I64, _I64, _I32, _P, _P, _P, _P, _P, _P, _P, _SZ]
     L.spc_stride2_inverse_taps.argtypes = [_P, _P, _P, _I64, _I64, _P]
+    L.spc_compose_rows.argtypes = [_P, _P, _I64, _P, _I64, _P]
     L.spc_subdivide_workspace_bytes.restype = _SZ
     L.spc_subdivide_workspace_bytes.argtypes = [_I64]
     L.spc_subdivide_map.argtypes = [_P, _P, _I64, _P, _P, _P, _P, _P, _SZ]
@@ -86,6 +87,12 @@ def lib() -> ctypes.CDLL:
     L.spc_scatter_mean.argtypes = [_P, _INT, _P, _P, _P, _P, _I64, _I64, _I64, _P, _SZ]
     L.spc_gather_rows.argtypes = [_P, _INT, _P, _P, _P, _I64, _I64, _I64]
     L.spc_layernorm_silu.argtypes = [_P, _INT, _P, _I64, _I64, _P, _P, ctypes.c_float, _INT, _P]
+    L.spc_group_norm_workspace_bytes.restype = _SZ
+    L.spc_group_norm_workspace_bytes.argtypes = [_I64, _I64, _I64]
+    L.spc_group_norm_stats.argtypes = [_P, _INT, _P, _I64, _I64, _P, _I64, _I64, ctypes.c_float,
+                                       _P, _P, _SZ]
+    L.spc_group_norm_silu.argtypes = [_P, _INT, _P, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _INT,
+                                      _P, _I64, _P]
     L.spc_sparse_conv_fused.argtypes = [_P, _INT, _P, _INT, _INT, _P, _P, _P, _P, _P, _INT, _P,
                                         _P, _I64, _I64, _I64, _I64, _I64,
                                         ctypes.POINTER(ConvEpilogue)]
@@ -100,7 +107,8 @@ class ConvEpilogue(ctypes.Structure):
     """spc_conv_epilogue (include/sam3d_spconv_amd.h)."""
     _fields_ = [("mode", ctypes.c_int32), ("eps", ctypes.c_float), ("residual", ctypes.c_void_p),
                 ("scale", ctypes.c_void_p), ("shift", ctypes.c_void_p),
-                ("coords", ctypes.c_void_p), ("n_batch", ctypes.c_int64)]
+                ("coords", ctypes.c_void_p), ("n_batch", ctypes.c_int64),
+                ("residual_rows", ctypes.c_void_p), ("n_residual", ctypes.c_int64)]
 
 
 def _check(fn: str, status: int) -> None:
@@ -145,10 +153,10 @@ class SubmMap:
 
     n: int
     token_major: torch.Tensor   # [n*27] int32, sentinel n
-    offset_major: torch.Tensor  # [27*n] int32, -1 missing
-    mask_sorted: torch.Tensor   # [n] int32
-    argsort: torch.Tensor       # [n] int32
-    mask_natural: torch.Tensor  # [n] int32
+    offset_major: torch.Tensor | None  # [27*n] int32, -1 missing (outputs "all")
+    mask_sorted: torch.Tensor | None   # [n] int32 (outputs "all")
+    argsort: torch.Tensor | None       # [n] int32 (outputs "all")
+    mask_natural: torch.Tensor | None  # [n] int32 (outputs "all")
     _plan: torch.Tensor | None = None
 
     @property
@@ -165,7 +173,8 @@ class SubmMap:
 def map_build(coords: torch.Tensor, *, mesh_resolution: int | None = None,
               outputs: str = "all", sync: bool = True, workspace: torch.Tensor | None = None):
     """spc_map_build on int32 [N,4] device coords.  mesh_resolution selects the
-    build_mesh_conv_table semantics (range + uniqueness checks)."""
+    build_mesh_conv_table semantics (range + uniqueness checks).  outputs
+    "token" builds the token-major table only (no mask sort)."""
     _need_gpu(coords)
     coords = coords.contiguous()
     if coords.dtype != torch.int32 or coords.dim() != 2 or coords.shape[1] != 4:
@@ -176,8 +185,10 @@ def map_build(coords: torch.Tensor, *, mesh_resolution: int | None = None,
     ws = workspace if workspace is not None else _workspace(L.spc_map_workspace_bytes(n), dev)
     e = lambda k: torch.empty(k, dtype=torch.int32, device=dev)  # noqa: E731
     tm = e(27 * n)
-    om = e(27 * n) if outputs == "all" else None
-    ms, ar, mn = e(n), e(n), e(n)
+    full = outputs == "all"
+    om = e(27 * n) if full else None
+    # the mask sort runs only when its outputs are asked for
+    ms, ar, mn = (e(n), e(n), e(n)) if full else (None, None, None)
     flags = (MAP_MESH if mesh_resolution is not None else 0) | (MAP_SYNC if sync else 0)
     st = L.spc_map_build(_stream(dev), _ptr(coords), n, int(mesh_resolution or 0), flags,
                          _ptr(tm), _ptr(om), _ptr(ms), _ptr(ar), _ptr(mn), _ptr(ws), ws.numel())
@@ -217,6 +228,20 @@ def downsample_map(coords: torch.Tensor, n_batch: int, resolution: int,
     k = nc.value
     return DownsampleMap(nf, k, f2c, cc[:k], ch[: 8 * k], cnt[:k],
                          None if taps is None else taps[: 8 * k])
+
+
+def compose_rows(idx: torch.Tensor, rows: torch.Tensor) -> torch.Tensor:
+    """out[i] = rows[idx[i]] for idx[i] in [0, len(rows)), else -1
+    (spc_compose_rows): a neighbour table over subdivided children composed
+    with their parent rows."""
+    _need_gpu(idx, rows)
+    idx = idx.to(torch.int32).contiguous()
+    rows = rows.to(torch.int32).contiguous()
+    out = torch.empty_like(idx)
+    st = lib().spc_compose_rows(_stream(idx.device), _ptr(idx), idx.numel(), _ptr(rows),
+                                rows.numel(), _ptr(out))
+    _check("spc_compose_rows", st)
+    return out
 
 
 def stride2_inverse_taps(fine_coords: torch.Tensor, fine_to_coarse: torch.Tensor,
@@ -340,15 +365,18 @@ def sparse_conv(x: torch.Tensor, weight, bias: torch.Tensor | None,
                 w_scale: torch.Tensor | None = None, out: torch.Tensor | None = None,
                 cout: int | None = None, plan: torch.Tensor | None = None,
                 residual: torch.Tensor | None = None,
-                norm_mod: tuple | None = None) -> torch.Tensor:
+                norm_mod: tuple | None = None,
+                residual_rows: torch.Tensor | None = None) -> torch.Tensor:
     """y = conv(x) through spc_sparse_conv_fused.  `weight` is a
     PackedWeights, a [Cout, ntaps, Cin] tensor in the feature dtype, or int8
     Q8_0 quants with w_scale (fp16 block scales).  idx None with ntaps 1 is
     the identity map (the dense 1x1x1 conv).  Epilogues: `residual`
-    ([n_out, Cout], feature dtype) is added to the rounded output;
+    ([n_out, Cout], feature dtype) is added to the rounded output -- with
+    `residual_rows` (int32 [n_out]) residual is [R, Cout] and output row t
+    adds residual[residual_rows[t]];
     `norm_mod` = (scale, shift, coords, eps) with f32 [n_batch, Cout] scale
     and shift gives silu(norm(y) * (1 + scale[b]) + shift[b])."""
-    _need_gpu(x, bias, idx, row_perm, w_scale, residual)
+    _need_gpu(x, bias, idx, row_perm, w_scale, residual, residual_rows)
     x = x.contiguous()
     dt = dtype_code(x.dtype)
     cin = x.shape[1]
@@ -376,13 +404,21 @@ def sparse_conv(x: torch.Tensor, weight, bias: torch.Tensor | None,
         bias = bias.contiguous()
     if out is None:
         out = torch.empty((n_out, cout), dtype=x.dtype, device=x.device)
-    epi = ConvEpilogue(EPI_NONE, 0.0, None, None, None, None, 0)
+    epi = ConvEpilogue(EPI_NONE, 0.0, None, None, None, None, 0, None, 0)
     keep = []
     if residual is not None and norm_mod is not None:
         raise ValueError("one epilogue at a time")
     if residual is not None:
         residual = residual.contiguous()
-        if residual.shape != (n_out, cout) or residual.dtype != x.dtype:
+        if residual_rows is not None:
+            residual_rows = residual_rows.to(torch.int32).contiguous()
+            if residual_rows.shape != (n_out,) or residual.dim() != 2 or residual.shape[1] != cout \
+                    or residual.shape[0] < 1 or residual.dtype != x.dtype:
+                raise ValueError("residual_rows must be int32 [n_out] and residual [R >= 1, cout] "
+                                 "in the feature dtype")
+            epi.residual_rows, epi.n_residual = _ptr(residual_rows), residual.shape[0]
+            keep.append(residual_rows)
+        elif residual.shape != (n_out, cout) or residual.dtype != x.dtype:
             raise ValueError("residual must be [n_out, cout] in the feature dtype")
         epi.mode, epi.residual = EPI_RESIDUAL, _ptr(residual)
         keep.append(residual)
@@ -507,4 +543,38 @@ def gather_rows(src: torch.Tensor, idx: torch.Tensor) -> torch.Tensor:
     st = lib().spc_gather_rows(_stream(src.device), dtype_code(src.dtype), _ptr(src), _ptr(idx),
                                _ptr(out), idx.numel(), n_src, channels)
     _check("spc_gather_rows", st)
+    return out
+
+
+def group_norm_silu(x: torch.Tensor, offsets: torch.Tensor, groups: int, weight=None, bias=None,
+                    eps: float = 1e-5, silu: bool = True, rows: torch.Tensor | None = None,
+                    max_rows: int | None = None) -> torch.Tensor:
+    """silu(GroupNorm32(x)) with per-batch-item statistics (rows of item b:
+    offsets[b] .. offsets[b+1], device int64), optionally gathered:
+    out[i] = f(x)[rows[i]] (spc_group_norm_stats + spc_group_norm_silu)."""
+    _need_gpu(x, offsets, weight, bias, rows)
+    x = x.contiguous()
+    n, c = x.shape
+    offsets = offsets.to(torch.int64).contiguous()
+    nb = offsets.numel() - 1
+    if max_rows is None:
+        max_rows = int((offsets[1:] - offsets[:-1]).max().item()) if nb > 0 else 0
+    L = lib()
+    ws = torch.empty(max(8, L.spc_group_norm_workspace_bytes(nb, max_rows, groups)), dtype=torch.uint8,
+                     device=x.device)
+    stats = torch.empty((nb, groups, 2), dtype=torch.float32, device=x.device)
+    st = L.spc_group_norm_stats(_stream(x.device), dtype_code(x.dtype), _ptr(x), c, groups,
+                                _ptr(offsets), nb, max_rows, float(eps), _ptr(stats), _ptr(ws),
+                                ws.numel())
+    _check("spc_group_norm_stats", st)
+    w = None if weight is None else weight.detach().to(torch.float32).contiguous()
+    b = None if bias is None else bias.detach().to(torch.float32).contiguous()
+    if rows is not None:
+        rows = rows.to(torch.int32).contiguous()
+    n_out = n if rows is None else rows.numel()
+    out = torch.empty((n_out, c), dtype=x.dtype, device=x.device)
+    st = L.spc_group_norm_silu(_stream(x.device), dtype_code(x.dtype), _ptr(x), n, c, groups,
+                               _ptr(offsets), nb, _ptr(stats), _ptr(w), _ptr(b), int(bool(silu)),
+                               _ptr(rows), n_out, _ptr(out))
+    _check("spc_group_norm_silu", st)
     return out

@@ -25,9 +25,10 @@ import torch
 import torch.nn as nn
 
 from . import _native as nat
-from .sparse import SparseConv3d, SparseDownsample, SparseLinear, SparseTensor, SparseUpsample
+from .sparse import (SparseConv3d, SparseDownsample, SparseGroupNorm32, SparseLinear, SparseSiLU,
+                     SparseSubdivide, SparseTensor, SparseUpsample, batch_offsets)
 
-__all__ = ["LayerNorm32", "SparseResBlock3d"]
+__all__ = ["LayerNorm32", "SparseResBlock3d", "SparseSubdivideBlock3d"]
 
 
 class LayerNorm32(nn.LayerNorm):
@@ -87,3 +88,69 @@ class SparseResBlock3d(nn.Module):
         if self.out_channels % 32 == 0:
             return self.conv2.forward_fused(h, residual=skip.feats)
         return self.conv2(h) + skip
+
+
+class SparseSubdivideBlock3d(nn.Module):
+    """The mesh decoder's upsampling block (decoder_mesh.py:17-83;
+    SRC/mesh_decoder_graph.cpp:399-437):
+
+        h = out_layers(subdivide(silu(groupnorm(x))))
+        out = h + skip(subdivide(x))
+
+    with out_layers = [conv 3x3x3, GroupNorm32, SiLU, conv 3x3x3] and skip a
+    1x1x1 conv when the channel count changes.  Runs as: GroupNorm
+    statistics + norm / SiLU / parent gather in one pass, conv1, GroupNorm
+    statistics + norm / SiLU, conv2 with the residual epilogue.  State-dict
+    keys are the reference's (act_layers.0.*, out_layers.0.conv.*,
+    out_layers.1.*, out_layers.3.conv.*, skip_connection.conv.*)."""
+
+    def __init__(self, channels: int, resolution: int, out_channels: Optional[int] = None,
+                 num_groups: int = 32):
+        super().__init__()
+        self.channels = channels
+        self.resolution = resolution
+        self.out_resolution = resolution * 2
+        self.out_channels = out_channels or channels
+        self.act_layers = nn.Sequential(SparseGroupNorm32(num_groups, channels), SparseSiLU())
+        self.sub = SparseSubdivide()
+        conv2 = SparseConv3d(self.out_channels, self.out_channels, 3,
+                             indice_key=f"res_{self.out_resolution}")
+        for p in conv2.parameters():  # zero_module (modules/utils.py)
+            p.detach().zero_()
+        self.out_layers = nn.Sequential(
+            SparseConv3d(channels, self.out_channels, 3, indice_key=f"res_{self.out_resolution}"),
+            SparseGroupNorm32(num_groups, self.out_channels),
+            SparseSiLU(),
+            conv2,
+        )
+        if self.out_channels == channels:
+            self.skip_connection = nn.Identity()
+        else:
+            self.skip_connection = SparseConv3d(channels, self.out_channels, 1,
+                                                indice_key=f"res_{self.out_resolution}")
+
+    def forward(self, x: SparseTensor) -> SparseTensor:
+        gn0, gn1 = self.act_layers[0], self.out_layers[1]
+        conv1, conv2 = self.out_layers[0], self.out_layers[3]
+        coords, parent = self.sub.map(x)
+        nc = coords.shape[0]
+        # silu(GroupNorm(x)) on the parent rows only: the children's features
+        # are copies of them, so conv1 reads the parents through the child
+        # neighbour table composed with the parent rows (bit-identical to the
+        # conv over the copies, without writing 8x the rows)
+        h_par = nat.group_norm_silu(x.feats, batch_offsets(x), gn0.num_groups, gn0.weight,
+                                    gn0.bias, gn0.eps, silu=True)
+        cm = nat.map_build(coords.contiguous(), outputs="token")
+        composed = nat.compose_rows(cm.token_major, parent)
+        plan1 = nat.conv_plan(composed, ntaps=27, n_out=nc, n_in=x.feats.shape[0])
+        h = self.sub.assemble(x, coords, conv1._conv(h_par, composed, nc, plan1))
+        h.data.cached("subm3", lambda c: cm)  # conv2's map: the same child coordinates
+        h = h.replace(nat.group_norm_silu(h.feats, batch_offsets(h), gn1.num_groups, gn1.weight,
+                                          gn1.bias, gn1.eps, silu=True))
+        # the skip on the parent rows (a 1x1x1 conv is row-wise), added to
+        # child t from row parent[t] in conv2's epilogue
+        skip = x.feats if isinstance(self.skip_connection, nn.Identity) \
+            else self.skip_connection(x).feats
+        if self.out_channels % 32 == 0:
+            return conv2.forward_fused(h, residual=skip, residual_rows=parent)
+        return conv2(h) + h.replace(nat.gather_rows(skip, parent))

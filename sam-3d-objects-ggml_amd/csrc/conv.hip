@@ -366,6 +366,15 @@ int spc_sparse_conv_fused(spc_stream_t stream, int dtype, const void* x, int w_d
                 return SPC_BAD_ARG;
             }
             a.residual = epi->residual;
+            if (epi->residual_rows) {
+                if (epi->n_residual < 1 || epi->n_residual > INT32_MAX) {
+                    set_last_error("spc_sparse_conv_fused: residual_rows needs 1 <= n_residual <= "
+                                   "INT32_MAX (got %lld)", (long long)epi->n_residual);
+                    return SPC_BAD_ARG;
+                }
+                a.residual_rows = epi->residual_rows;
+                a.n_residual = epi->n_residual;
+            }
         } else if (epi->mode == SPC_EPI_NORM_MOD_SILU) {
             if (cout > 128) {
                 set_last_error("spc_sparse_conv_fused: the norm epilogue needs cout <= 128 (got %lld)",

@@ -76,7 +76,9 @@ struct ConvArgs {
     // fused epilogue (spc_conv_epilogue): SPC_EPI_NONE / _RESIDUAL / _NORM_MOD_SILU
     int32_t epi_mode;
     float epi_eps;
-    const void* residual;     // [n_out, cout] in the feature dtype
+    const void* residual;     // [n_out, cout] in the feature dtype, or [n_residual, cout]
+    const int32_t* residual_rows;  // optional residual row of each output row
+    int64_t n_residual;
     const float* epi_scale;   // [n_batch, cout]
     const float* epi_shift;   // [n_batch, cout]
     const int32_t* coords;    // [n_out, 4]: batch of each output row
@@ -1029,13 +1031,22 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
             // y = dt(dt(conv + bias) + residual): the rounded conv output
             // plus the residual row, added in F32 and rounded once more
             u32x4 rv[NU];
+            int32_t rr[NU];
+#pragma unroll
+            for (int k = 0; k < NU; ++k) {
+                rr[k] = tt[k];
+                if (a.residual_rows && tt[k] >= 0) {
+                    const int32_t v = a.residual_rows[tt[k]];
+                    rr[k] = (v >= 0 && v < a.n_residual) ? v : -1;
+                }
+            }
 #pragma unroll
             for (int k = 0; k < NU; ++k) {
                 const int q = (tid + k * NT) % UPR;
-                rv[k] = tt[k] >= 0 ? *reinterpret_cast<const u32x4*>(
+                rv[k] = rr[k] >= 0 ? *reinterpret_cast<const u32x4*>(
                                          static_cast<const char*>(a.residual) +
-                                         ((int64_t)tt[k] * a.cout + co0) * ES + q * 16)
-                                   : vv[k];
+                                         ((int64_t)rr[k] * a.cout + co0) * ES + q * 16)
+                                   : u32x4{0u, 0u, 0u, 0u};
             }
 #pragma unroll
             for (int k = 0; k < NU; ++k) {

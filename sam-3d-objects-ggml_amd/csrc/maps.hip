@@ -319,6 +319,23 @@ __global__ void subdivide_kernel(const int4* __restrict__ coords, int64_t n,
     parent[dst] = (int32_t)p;
 }
 
+// out[i] = rows[idx[i]] for idx[i] in [0, n_rows), else -1; four entries per
+// lane (n4 = n / 4 vector steps, then the tail)
+__global__ void compose_rows_kernel(const int32_t* __restrict__ idx, int64_t n,
+                                    const int32_t* __restrict__ rows, int64_t n_rows,
+                                    int32_t* __restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t n4 = n / 4;
+    auto one = [&](int32_t v) { return (v >= 0 && v < n_rows) ? rows[v] : -1; };
+    if (i < n4) {
+        const int4 v = reinterpret_cast<const int4*>(idx)[i];
+        reinterpret_cast<int4*>(out)[i] = int4{one(v.x), one(v.y), one(v.z), one(v.w)};
+    } else if (i - n4 < n - 4 * n4) {
+        const int64_t j = 4 * n4 + (i - n4);
+        out[j] = one(idx[j]);
+    }
+}
+
 inline unsigned grid_for(int64_t n, int threads) { return (unsigned)((n + threads - 1) / threads); }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -538,6 +555,25 @@ int spc_stride2_inverse_taps(spc_stream_t stream, const int32_t* coords,
     }
     stride2_inverse_kernel<<<grid_for(nf, 256), 256, 0, s>>>(
         reinterpret_cast<const int4*>(coords), fine_to_coarse, nf, (int32_t)nc, taps);
+    SPC_HIP(hipGetLastError());
+    return SPC_OK;
+}
+
+int spc_compose_rows(spc_stream_t stream, const int32_t* idx, int64_t n, const int32_t* rows,
+                     int64_t n_rows, int32_t* out) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (n < 0 || n_rows < 0 || n_rows > INT32_MAX) {
+        set_last_error("spc_compose_rows: n=%lld n_rows=%lld out of range", (long long)n,
+                       (long long)n_rows);
+        return SPC_BAD_SHAPE;
+    }
+    if (n == 0) return SPC_OK;
+    if (!idx || !out || (!rows && n_rows > 0) || !aligned16(idx) || !aligned16(out)) {
+        set_last_error("spc_compose_rows: null or misaligned argument (idx / out 16-byte aligned)");
+        return SPC_BAD_ARG;
+    }
+    const int64_t lanes = n / 4 + (n % 4);
+    compose_rows_kernel<<<grid_for(lanes, 256), 256, 0, s>>>(idx, n, rows, n_rows, out);
     SPC_HIP(hipGetLastError());
     return SPC_OK;
 }

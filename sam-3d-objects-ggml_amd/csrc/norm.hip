@@ -6,6 +6,8 @@
 // per wave), every lane holding runs of 4 consecutive channels (one 8- or
 // 16-byte load).  Mean and biased variance are formed in F32 with two
 // passes over the registers and group-local shuffles.
+#include <algorithm>
+
 #include "common.h"
 
 namespace spc {
@@ -183,6 +185,219 @@ hipError_t launch_norm(hipStream_t s, const void* x, int64_t n, int c, const flo
     return hipGetLastError();
 }
 
+// ---- GroupNorm over each batch item's rows (SparseGroupNorm32) ----------
+// Statistics per (item, group) over the item's rows x the group's channels:
+// a partial kernel (one block per (chunk of R rows, item)) writes F64 sums
+// and sums of squares per group; a finalize kernel (one wave per (item,
+// group)) adds an item's chunks in a fixed lane-strided order and a fixed
+// shuffle tree.  R depends only on the shape (gn_chunk_rows), so results
+// are deterministic.
+constexpr int kGnMaxC = 1024;
+constexpr int64_t kGnTargetBlocks = 2048;  // about 8 blocks per CU
+
+// rows per chunk: enough chunks to fill the device, at least 16 rows
+__host__ __device__ inline int64_t gn_chunk_rows(int64_t n_batch, int64_t max_rows) {
+    int64_t r = (n_batch * max_rows + kGnTargetBlocks - 1) / kGnTargetBlocks;
+    r = (r + 15) / 16 * 16;
+    return r < 16 ? 16 : (r > 1024 ? 1024 : r);
+}
+
+inline int64_t gn_chunks(int64_t n_batch, int64_t max_rows) {
+    const int64_t r = gn_chunk_rows(n_batch, max_rows);
+    return std::max<int64_t>(1, (max_rows + r - 1) / r);
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void gn_partial_kernel(const void* __restrict__ x, int c, int groups,
+                                                         const int64_t* __restrict__ off, int rows_per,
+                                                         double* __restrict__ part, int chunks) {
+    using E = Elem<DT>;
+    __shared__ float ls[2 * kGnMaxC];     // [row lane][c] sums, then squares
+    __shared__ double cs[2 * kGnMaxC];
+    const int b = blockIdx.y;
+    const int64_t r0 = off[b] + (int64_t)blockIdx.x * rows_per;
+    const int64_t r1 = min(off[b + 1], r0 + rows_per);
+    const int nvec = c / 4;
+    int np = 1;
+    while (np < nvec) np <<= 1;
+    const int rl_n = 256 / np;  // row lanes: rl_n * c <= 1024
+    const int tid = threadIdx.x;
+    const int v = tid % np, rl = tid / np;
+    float s[4] = {0.f, 0.f, 0.f, 0.f}, q[4] = {0.f, 0.f, 0.f, 0.f};
+    if (v < nvec) {
+        int64_t r = r0 + rl;
+        // four rows in flight per lane
+        for (; r + 3 * rl_n < r1; r += 4 * rl_n) {
+            float t[4][4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) E::ld4(x, (r + u * rl_n) * c + 4 * v, t[u]);
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    s[e] += t[u][e];
+                    q[e] += t[u][e] * t[u][e];
+                }
+        }
+        for (; r < r1; r += rl_n) {
+            float t[4];
+            E::ld4(x, r * c + 4 * v, t);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                s[e] += t[e];
+                q[e] += t[e] * t[e];
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            ls[rl * c + 4 * v + e] = s[e];
+            ls[kGnMaxC + rl * c + 4 * v + e] = q[e];
+        }
+    }
+    __syncthreads();
+    for (int ch = tid; ch < c; ch += 256) {
+        double a = 0.0, aa = 0.0;
+        for (int k = 0; k < rl_n; ++k) {
+            a += ls[k * c + ch];
+            aa += ls[kGnMaxC + k * c + ch];
+        }
+        cs[ch] = a;
+        cs[kGnMaxC + ch] = aa;
+    }
+    __syncthreads();
+    const int cpg = c / groups;
+    for (int g = tid; g < groups; g += 256) {
+        double a = 0.0, aa = 0.0;
+        for (int k = 0; k < cpg; ++k) {
+            a += cs[g * cpg + k];
+            aa += cs[kGnMaxC + g * cpg + k];
+        }
+        double* p = part + (((int64_t)b * chunks + blockIdx.x) * groups + g) * 2;
+        p[0] = a;
+        p[1] = aa;
+    }
+}
+
+// one 64-lane block per (item, group)
+__global__ __launch_bounds__(64) void gn_finalize_kernel(const double* __restrict__ part,
+                                                         const int64_t* __restrict__ off, int groups,
+                                                         int chunks, int rows_per, int cpg, float eps,
+                                                         float* __restrict__ stats) {
+    const int i = blockIdx.x;
+    const int b = i / groups, g = i % groups;
+    const int lane = threadIdx.x;
+    const int64_t rows = off[b + 1] - off[b];
+    // never past the partials written (callers pass max_rows >= every item's rows)
+    const int used = (int)min<int64_t>((rows + rows_per - 1) / rows_per, chunks);
+    double a = 0.0, aa = 0.0;
+    for (int k = lane; k < used; k += 64) {
+        const double* p = part + (((int64_t)b * chunks + k) * groups + g) * 2;
+        a += p[0];
+        aa += p[1];
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        a += __shfl_xor(a, o);
+        aa += __shfl_xor(aa, o);
+    }
+    if (lane == 0) {
+        const double cnt = (double)rows * cpg;
+        const double mean = cnt > 0 ? a / cnt : 0.0;
+        const double var = cnt > 0 ? fmax(aa / cnt - mean * mean, 0.0) : 0.0;
+        stats[2 * i] = (float)mean;
+        stats[2 * i + 1] = (float)(1.0 / sqrt(var + (double)eps));
+    }
+}
+
+// y[i] = dt(silu(dt((x[src] - mean) * rstd * gamma + beta))), src = rows[i]
+// (or i); the batch item of src by a binary search over the row offsets.
+// Each lane handles a run of 4 * NV channels (16 bytes for 2-byte types
+// with NV = 2).
+template <int DT, int NV>
+__global__ __launch_bounds__(256) void gn_apply_kernel(const void* __restrict__ x, int64_t n_src, int c,
+                                                       int groups, const int64_t* __restrict__ off,
+                                                       int n_batch, const float* __restrict__ stats,
+                                                       const float* __restrict__ gamma,
+                                                       const float* __restrict__ beta, int silu,
+                                                       const int32_t* __restrict__ rows,
+                                                       int64_t n_out, void* __restrict__ y) {
+    using E = Elem<DT>;
+    constexpr int W = 4 * NV;
+    const int nrun = c / W;
+    const int cpg = c / groups;
+    const int64_t total = n_out * nrun;
+    for (int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; id < total;
+         id += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t i = id / nrun;
+        const int c0 = W * (int)(id - i * nrun);
+        const int64_t src = rows ? rows[i] : i;
+        float o[W];
+#pragma unroll
+        for (int e = 0; e < W; ++e) o[e] = 0.f;
+        if (src >= 0 && src < n_src) {
+            int lo = 0, hi = n_batch;  // last b with off[b] <= src
+            while (hi - lo > 1) {
+                const int mid = (lo + hi) >> 1;
+                if (off[mid] <= src) lo = mid;
+                else hi = mid;
+            }
+            float t[W];
+#pragma unroll
+            for (int h = 0; h < NV; ++h) E::ld4(x, src * c + c0 + 4 * h, t + 4 * h);
+            const float* st = stats + 2 * (int64_t)lo * groups;
+            int g = c0 / cpg, rem = c0 - g * cpg;
+#pragma unroll
+            for (int h = 0; h < NV; ++h) {
+                const floatx4 g4 = gamma ? *reinterpret_cast<const floatx4*>(gamma + c0 + 4 * h)
+                                         : floatx4{1.f, 1.f, 1.f, 1.f};
+                const floatx4 b4 = beta ? *reinterpret_cast<const floatx4*>(beta + c0 + 4 * h)
+                                        : floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float mean = st[2 * g], rstd = st[2 * g + 1];
+                    float u = (t[4 * h + e] - mean) * rstd * g4[e] + b4[e];
+                    u = E::round(u);  // GroupNorm32 casts back to the feature dtype
+                    o[4 * h + e] = silu ? silu_f32(u) : u;
+                    if (++rem == cpg) {
+                        rem = 0;
+                        ++g;
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < NV; ++h) E::st4(y, i * c + c0 + 4 * h, o + 4 * h);
+    }
+}
+
+template <int DT>
+hipError_t launch_gn_stats(hipStream_t s, const void* x, int c, int groups, const int64_t* off,
+                           int n_batch, int64_t max_rows, double* part, float eps, float* stats) {
+    const int rows_per = (int)gn_chunk_rows(n_batch, max_rows);
+    const int chunks = (int)gn_chunks(n_batch, max_rows);
+    gn_partial_kernel<DT><<<dim3(chunks, n_batch), 256, 0, s>>>(x, c, groups, off, rows_per, part,
+                                                                chunks);
+    gn_finalize_kernel<<<n_batch * groups, 64, 0, s>>>(part, off, groups, chunks, rows_per,
+                                                      c / groups, eps, stats);
+    return hipGetLastError();
+}
+
+template <int DT>
+hipError_t launch_gn_apply(hipStream_t s, const void* x, int64_t n_src, int c, int groups,
+                           const int64_t* off, int n_batch, const float* stats, const float* gamma,
+                           const float* beta, int silu, const int32_t* rows, int64_t n_out, void* y) {
+    const bool wide = DT != SPC_F32 && c % 8 == 0;
+    const int64_t total = n_out * (c / (wide ? 8 : 4));
+    const unsigned grid = (unsigned)std::min<int64_t>(ceil_div(total, 256), 65536);
+    if (wide)
+        gn_apply_kernel<DT, 2><<<grid, 256, 0, s>>>(x, n_src, c, groups, off, n_batch, stats, gamma,
+                                                    beta, silu, rows, n_out, y);
+    else
+        gn_apply_kernel<DT, 1><<<grid, 256, 0, s>>>(x, n_src, c, groups, off, n_batch, stats, gamma,
+                                                    beta, silu, rows, n_out, y);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 }  // namespace spc
@@ -216,6 +431,84 @@ int spc_layernorm_silu(spc_stream_t stream, int dtype, const void* x, int64_t n,
     }
     if (e != hipSuccess) {
         set_last_error("spc_layernorm_silu: launch failed: %s", hipGetErrorString(e));
+        return SPC_HIP_ERROR;
+    }
+    return SPC_OK;
+}
+
+size_t spc_group_norm_workspace_bytes(int64_t n_batch, int64_t max_rows, int64_t groups) {
+    if (n_batch <= 0 || max_rows < 0 || groups <= 0) return 0;
+    return (size_t)(n_batch * gn_chunks(n_batch, max_rows) * groups * 2 * sizeof(double));
+}
+
+int spc_group_norm_stats(spc_stream_t stream, int dtype, const void* x, int64_t c, int64_t groups,
+                         const int64_t* offsets, int64_t n_batch, int64_t max_rows, float eps,
+                         float* stats, void* workspace, size_t workspace_bytes) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (c <= 0 || c > kGnMaxC || c % 4 != 0 || groups <= 0 || c % groups != 0 || n_batch <= 0 ||
+        n_batch > 65535 || max_rows < 0 || !(eps >= 0.0f)) {
+        set_last_error("spc_group_norm_stats: unsupported shape c=%lld groups=%lld n_batch=%lld "
+                       "(c a multiple of 4 and of groups, at most %d)", (long long)c,
+                       (long long)groups, (long long)n_batch, kGnMaxC);
+        return SPC_BAD_SHAPE;
+    }
+    if (workspace_bytes < spc_group_norm_workspace_bytes(n_batch, max_rows, groups)) {
+        set_last_error("spc_group_norm_stats: workspace too small");
+        return SPC_BAD_ARG;
+    }
+    const size_t align = dtype == SPC_F32 ? 16 : 8;
+    if (!x || !offsets || !stats || !workspace || ((uintptr_t)x % align) ||
+        ((uintptr_t)workspace % 8)) {
+        set_last_error("spc_group_norm_stats: null or misaligned pointer");
+        return SPC_BAD_ARG;
+    }
+    hipError_t e;
+    double* part = static_cast<double*>(workspace);
+    if (dtype == SPC_BF16) e = launch_gn_stats<SPC_BF16>(s, x, (int)c, (int)groups, offsets, (int)n_batch, max_rows, part, eps, stats);
+    else if (dtype == SPC_F16) e = launch_gn_stats<SPC_F16>(s, x, (int)c, (int)groups, offsets, (int)n_batch, max_rows, part, eps, stats);
+    else if (dtype == SPC_F32) e = launch_gn_stats<SPC_F32>(s, x, (int)c, (int)groups, offsets, (int)n_batch, max_rows, part, eps, stats);
+    else {
+        set_last_error("spc_group_norm_stats: unknown dtype %d", dtype);
+        return SPC_BAD_ARG;
+    }
+    if (e != hipSuccess) {
+        set_last_error("spc_group_norm_stats: launch failed: %s", hipGetErrorString(e));
+        return SPC_HIP_ERROR;
+    }
+    return SPC_OK;
+}
+
+int spc_group_norm_silu(spc_stream_t stream, int dtype, const void* x, int64_t n_src, int64_t c,
+                        int64_t groups, const int64_t* offsets, int64_t n_batch, const float* stats,
+                        const float* gamma, const float* beta, int silu, const int32_t* rows,
+                        int64_t n_out, void* y) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (n_src < 0 || n_out < 0 || c <= 0 || c > kGnMaxC || c % 4 != 0 || groups <= 0 ||
+        c % groups != 0 || n_batch <= 0) {
+        set_last_error("spc_group_norm_silu: unsupported shape");
+        return SPC_BAD_SHAPE;
+    }
+    if (n_out == 0) return SPC_OK;
+    if (!rows && n_out != n_src) {
+        set_last_error("spc_group_norm_silu: rows may be NULL only when n_out == n_src");
+        return SPC_BAD_ARG;
+    }
+    const size_t align = dtype == SPC_F32 ? 16 : 8;
+    if (!x || !y || !offsets || !stats || ((uintptr_t)x % align) || ((uintptr_t)y % align) ||
+        ((uintptr_t)gamma % 16) || ((uintptr_t)beta % 16)) {
+        set_last_error("spc_group_norm_silu: null or misaligned pointer");
+        return SPC_BAD_ARG;
+    }
+    hipError_t e;
+    if (dtype == SPC_BF16) e = launch_gn_apply<SPC_BF16>(s, x, n_src, (int)c, (int)groups, offsets, (int)n_batch, stats, gamma, beta, silu, rows, n_out, y);
+    else if (dtype == SPC_F16) e = launch_gn_apply<SPC_F16>(s, x, n_src, (int)c, (int)groups, offsets, (int)n_batch, stats, gamma, beta, silu, rows, n_out, y);
+    else if (dtype == SPC_F32) e = launch_gn_apply<SPC_F32>(s, x, n_src, (int)c, (int)groups, offsets, (int)n_batch, stats, gamma, beta, silu, rows, n_out, y);
+    else {
+        set_last_error("spc_group_norm_silu: unknown dtype %d", dtype);
+        return SPC_BAD_ARG;
+    }
+    if (e != hipSuccess) {
+        set_last_error("spc_group_norm_silu: launch failed: %s", hipGetErrorString(e));
         return SPC_HIP_ERROR;
     }
     return SPC_OK;

@@ -43,6 +43,7 @@ __all__ = [
     "SparseTensor", "SparseTensorData", "sparse_batch_broadcast", "sparse_batch_op",
     "sparse_cat", "sparse_unbind", "SparseConv3d", "SparseInverseConv3d",
     "SparseDownsample", "SparseUpsample", "SparseSubdivide", "SparseLinear",
+    "SparseGroupNorm32", "SparseSiLU",
 ]
 
 BACKEND = "hip"
@@ -552,7 +553,8 @@ class _ConvCore:
 
     def _conv(self, feats: torch.Tensor, idx: Optional[torch.Tensor], n_out: int,
               plan: Optional[torch.Tensor] = None, residual: Optional[torch.Tensor] = None,
-              norm_mod: Optional[tuple] = None) -> torch.Tensor:
+              norm_mod: Optional[tuple] = None,
+              residual_rows: Optional[torch.Tensor] = None) -> torch.Tensor:
         c = self.conv
         if feats.dim() != 2 or feats.shape[1] != c.in_channels:
             raise ValueError(f"expected feats [N, {c.in_channels}], got {tuple(feats.shape)}")
@@ -569,7 +571,7 @@ class _ConvCore:
             b = self._bias_operand(x.dtype, x.device)
             r = None if residual is None else residual.detach().to(x.dtype)
             y = nat.sparse_conv(x, w, b, idx, ntaps=self._ntaps, n_out=n_out, plan=plan,
-                                residual=r, norm_mod=norm_mod)
+                                residual=r, norm_mod=norm_mod, residual_rows=residual_rows)
             if y.shape[1] != c.out_channels:
                 y = y[:, : c.out_channels].contiguous()
             return y
@@ -611,10 +613,13 @@ class SparseConv3d(nn.Module, _ConvCore):
         return self.forward_fused(x)
 
     def forward_fused(self, x: SparseTensor, residual: Optional[torch.Tensor] = None,
-                      norm_mod: Optional[tuple] = None) -> SparseTensor:
+                      norm_mod: Optional[tuple] = None,
+                      residual_rows: Optional[torch.Tensor] = None) -> SparseTensor:
         """forward() with a fused epilogue on the output rows (submanifold
         convs only): `residual` [N, Cout] is added to the rounded output
-        (`h = conv2(h); h = h + skip`), `norm_mod` = (scale, shift, eps) with
+        (`h = conv2(h); h = h + skip`) -- or, with `residual_rows` [N],
+        residual[residual_rows[t]] from a [R, Cout] residual --
+        `norm_mod` = (scale, shift, eps) with
         per-batch [B, Cout] scale / shift gives silu(norm(y) * (1 + scale)
         + shift) (structured_latent_flow.py:69-71; Cout <= 128)."""
         spatial_changed = any(s != 1 for s in self.stride) or (self.padding is not None)
@@ -630,12 +635,12 @@ class SparseConv3d(nn.Module, _ConvCore):
             m = _subm_map(x)
             n = x.feats.shape[0]
             feats = self._conv(x.feats, m.token_major, n, _plan(x, "subm3", m.token_major, 27, n, n),
-                               residual=residual, norm_mod=nm)
+                               residual=residual, norm_mod=nm, residual_rows=residual_rows)
             data = x.data.replace_feature(feats)
         elif self._kind == "subm1":
             n = x.feats.shape[0]
             feats = self._conv(x.feats, None, n, _plan(x, "dense1", None, 1, n, n),
-                               residual=residual, norm_mod=nm)
+                               residual=residual, norm_mod=nm, residual_rows=residual_rows)
             data = x.data.replace_feature(feats)
         else:
             d = _downsample_map(x)
@@ -703,6 +708,36 @@ class SparseLinear(nn.Linear):
         return input.replace(super().forward(input.feats))
 
 
+def batch_offsets(x: SparseTensor) -> torch.Tensor:
+    """Row offsets [B + 1] (int64, on the feature device) of the batch
+    items' contiguous row ranges (the tensor's layout)."""
+    lay = x.layout
+    offs = [lay[0].start] + [sl.stop for sl in lay]
+    for a, sl in zip(offs, lay):
+        if sl.start != a:
+            raise ValueError("batch items must occupy contiguous, ascending row ranges")
+    return torch.tensor(offs, dtype=torch.int64).to(x.feats.device, non_blocking=True)
+
+
+class SparseGroupNorm32(nn.GroupNorm):
+    """GroupNorm over each batch item's rows, computed in F32 and cast back
+    (SP/norm.py:15-55), on spc_group_norm_stats / spc_group_norm_silu."""
+
+    def __init__(self, num_groups, num_channels, eps=1e-5, affine=True):
+        super().__init__(num_groups, num_channels, eps, affine)
+
+    def forward(self, input: SparseTensor) -> SparseTensor:
+        return input.replace(nat.group_norm_silu(input.feats, batch_offsets(input), self.num_groups,
+                                                 self.weight, self.bias, self.eps, silu=False))
+
+
+class SparseSiLU(nn.SiLU):
+    """SiLU on the feats (SP/nonlinearity.py:14-16)."""
+
+    def forward(self, input: SparseTensor) -> SparseTensor:
+        return input.replace(super().forward(input.feats))
+
+
 def _factor3(f) -> Tuple[int, int, int]:
     return tuple(f) if isinstance(f, (list, tuple)) else (f,) * 3
 
@@ -765,8 +800,17 @@ class SparseSubdivide(nn.Module):
     repetition), so spatial-cache keys match the reference's."""
 
     def forward(self, input: SparseTensor) -> SparseTensor:
-        coords, parent = nat.subdivide_map(input.coords.contiguous())
-        feats = nat.gather_rows(input.feats, parent)
+        coords, parent = self.map(input)
+        return self.assemble(input, coords, nat.gather_rows(input.feats, parent))
+
+    @staticmethod
+    def map(input: SparseTensor):
+        """(child coords, parent row of every child)."""
+        return nat.subdivide_map(input.coords.contiguous())
+
+    @staticmethod
+    def assemble(input: SparseTensor, coords: torch.Tensor, feats: torch.Tensor) -> SparseTensor:
+        """The subdivided tensor with the given child features."""
         data = SparseTensorData(feats, coords, [2 * s for s in input.data.spatial_shape],
                                 input.data.batch_size)
         out = SparseTensor(data, shape=input.shape)

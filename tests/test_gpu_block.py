@@ -164,3 +164,128 @@ def test_res_block(spc, orc, dev, cin, cout):
     got = from_dev(y.feats)
     assert got.shape == ref.shape
     assert max_rel(got, ref) <= MAXREL
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f32"])
+@pytest.mark.parametrize("c,groups,gather", [(64, 32, True), (32, 32, False), (768, 32, True),
+                                             (128, 8, False)])
+def test_group_norm_silu(spc, orc, dev, dt, c, groups, gather):
+    import oracle
+    import torch
+
+    _case(f"group_norm_silu {dt} c={c} groups={groups} gather={gather}")
+    nat = spc._native
+    rng = np.random.default_rng(c + groups)
+    sizes = [300, 1021, 2, 700]
+    n = sum(sizes)
+    offs = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
+    x = (rng.standard_normal((n, c)) * 1.5 + 0.2).astype(np.float32)
+    code = {"bf16": oracle.BF16, "f32": oracle.F32}[dt]
+    xr = oracle.round_to(orc, x, code)
+    g = rng.standard_normal(c).astype(np.float32)
+    b = rng.standard_normal(c).astype(np.float32)
+    rows = rng.integers(0, n, size=3000).astype(np.int32) if gather else None
+    y = nat.group_norm_silu(_dev_feats(orc, x, dt, dev), torch.from_numpy(offs).to(dev), groups,
+                            torch.from_numpy(g).to(dev), torch.from_numpy(b).to(dev), eps=1e-5,
+                            silu=True, rows=None if rows is None else torch.from_numpy(rows).to(dev))
+    ref = oracle.round_to(orc, oracle.silu(oracle.round_to(
+        orc, oracle.group_norm_items(xr, offs, groups, g, b, 1e-5), code)), code)
+    if rows is not None:
+        ref = ref[rows]
+    got = from_dev(y)
+    if dt == "f32":
+        assert np.allclose(got, ref, rtol=1e-4, atol=1e-5)
+    else:
+        assert max_rel(got, ref) <= 1e-2
+        assert np.mean(got == ref) >= 0.98
+
+
+def test_compose_rows(spc, dev):
+    import torch
+
+    _case("compose_rows n=4099 (ragged tail), sentinels and out-of-range entries")
+    nat = spc._native
+    rng = np.random.default_rng(5)
+    rows = rng.integers(0, 500, size=800).astype(np.int32)
+    idx = rng.integers(-3, 820, size=4099).astype(np.int32)
+    got = nat.compose_rows(torch.from_numpy(idx).to(dev), torch.from_numpy(rows).to(dev))
+    ok = (idx >= 0) & (idx < 800)
+    ref = np.where(ok, rows[np.clip(idx, 0, 799)], -1)
+    assert np.array_equal(got.cpu().numpy(), ref)
+
+
+def test_conv_residual_rows_epilogue(spc, orc, dev):
+    """residual[residual_rows[t]] added in the epilogue: bit-exact with the
+    gathered two-step sum; entries outside [0, R) add nothing."""
+    import torch
+
+    coords, n, x, xt, conv = _subm_setup(spc, orc, dev, 3000, 20, 2, 64, 96, 35)
+    _case(f"conv residual-rows epilogue bf16 N={n} 64->96")
+    r = _dev_feats(orc, spc.workloads.normal((700, 96), 1.0, seed=36), "bf16", dev)
+    rng = np.random.default_rng(37)
+    rows = rng.integers(0, 700, size=n).astype(np.int32)
+    rows[::97] = -1
+    rows[5::101] = 700
+    rows_d = torch.from_numpy(rows).to(dev)
+    with torch.no_grad():
+        y = conv(xt).feats
+        yf = conv.forward_fused(xt, residual=r, residual_rows=rows_d).feats
+    valid = torch.from_numpy((rows >= 0) & (rows < 700)).to(dev)
+    add = torch.where(valid[:, None], r[rows_d.clamp(0, 699).long()], torch.zeros_like(r[:1]))
+    assert torch.equal(yf, y + add)
+
+
+@pytest.mark.parametrize("cin,cout", [(64, 32), (32, 32)])
+def test_subdivide_block(spc, orc, dev, cin, cout):
+    """SparseSubdivideBlock3d (GroupNorm/SiLU/gather pass, conv, GroupNorm/
+    SiLU, conv with the residual epilogue) against the oracle's block."""
+    import oracle
+    import torch
+
+    blocks = spc.blocks
+    coords = spc.workloads.random_voxels(1500, 16, batches=2, seed=71 + cin)
+    n = coords.shape[0]
+    _case(f"SparseSubdivideBlock3d bf16 N={n} {cin}->{cout}")
+    torch.manual_seed(cin)
+    blk = blocks.SparseSubdivideBlock3d(cin, 16, cout).to(dev)
+    with torch.no_grad():
+        for prm in blk.out_layers[3].parameters():  # the reference zero-initialises it
+            prm.normal_(0, 0.02)
+        for gn in (blk.act_layers[0], blk.out_layers[1]):
+            gn.weight.normal_(1, 0.1)
+            gn.bias.normal_(0, 0.1)
+    blk = blk.to(torch.bfloat16)
+    blk.act_layers[0].float()
+    blk.out_layers[1].float()
+    x = spc.workloads.normal((n, cin), 1.0, seed=72)
+    xt = spc.sparse.SparseTensor(_dev_feats(orc, x, "bf16", dev), torch.from_numpy(coords).to(dev))
+    with torch.no_grad():
+        y = blk(xt)
+    f = lambda t: t.detach().float().cpu().numpy()  # noqa: E731
+    p = {"gn0_w": f(blk.act_layers[0].weight), "gn0_b": f(blk.act_layers[0].bias),
+         "conv1_w": f(blk.out_layers[0].conv.weight).reshape(cout, 27, cin),
+         "conv1_b": f(blk.out_layers[0].conv.bias),
+         "gn1_w": f(blk.out_layers[1].weight), "gn1_b": f(blk.out_layers[1].bias),
+         "conv2_w": f(blk.out_layers[3].conv.weight).reshape(cout, 27, cout),
+         "conv2_b": f(blk.out_layers[3].conv.bias)}
+    if cin != cout:
+        p["skip_w"] = f(blk.skip_connection.conv.weight)
+        p["skip_b"] = f(blk.skip_connection.conv.bias)
+    child, ref = oracle.subdivide_block(orc, oracle.round_to(orc, x, oracle.BF16), coords, p, 32,
+                                        oracle.BF16)
+    assert np.array_equal(y.coords.cpu().numpy(), child)
+    assert max_rel(from_dev(y.feats), ref) <= MAXREL
+    # the block reads parent rows through composed tables; the same block
+    # over materialised child copies gives the same bits
+    nat, sp = spc._native, spc.sparse
+    with torch.no_grad():
+        cc, par = blk.sub.map(xt)
+        gn0, gn1 = blk.act_layers[0], blk.out_layers[1]
+        h = blk.sub.assemble(xt, cc, nat.group_norm_silu(
+            xt.feats, sp.batch_offsets(xt), 32, gn0.weight, gn0.bias, gn0.eps, rows=par))
+        xs = blk.sub.assemble(xt, cc, nat.gather_rows(xt.feats, par))
+        h = blk.out_layers[0](h)
+        h = h.replace(nat.group_norm_silu(h.feats, sp.batch_offsets(h), 32, gn1.weight, gn1.bias,
+                                          gn1.eps))
+        want = blk.out_layers[3](h) + blk.skip_connection(xs)
+    assert torch.equal(y.feats, want.feats)

@@ -43,3 +43,27 @@ def test_round_to_matches_torch_casts(orc, dt):
     tdt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[dt]
     want = torch.from_numpy(x).to(tdt).float().numpy()
     assert np.array_equal(oracle.round_to(orc, x, code), want)
+
+
+def test_group_norm_items_matches_torch():
+    """Per batch item, torch's group_norm over [1, C, rows] -- what the
+    reference's SparseGroupNorm runs (modules/sparse/norm.py:19-31)."""
+    import oracle
+    import torch
+
+    rng = np.random.default_rng(3)
+    sizes = [37, 120, 5]
+    a = (rng.standard_normal((sum(sizes), 64)) * 2 + 0.3).astype(np.float32)
+    offs = np.concatenate([[0], np.cumsum(sizes)])
+    g = rng.standard_normal(64).astype(np.float32)
+    b = rng.standard_normal(64).astype(np.float32)
+    got = oracle.group_norm_items(a, offs, 32, g, b, 1e-5)
+    for k in range(3):
+        blk = torch.from_numpy(a[offs[k]:offs[k + 1]]).T.reshape(1, 64, -1)
+        ref = torch.nn.functional.group_norm(blk, 32, torch.from_numpy(g), torch.from_numpy(b),
+                                             eps=1e-5).reshape(64, -1).T.numpy()
+        assert np.allclose(got[offs[k]:offs[k + 1]], ref, rtol=1e-5, atol=1e-5)
+    # closed form: a constant group normalises to 0 (then + beta)
+    z = oracle.group_norm_items(np.ones((4, 64), np.float32), np.array([0, 4]), 32, None, b)
+    assert np.allclose(z, np.broadcast_to(b, z.shape))
+    assert np.array_equal(oracle.batch_offsets(np.array([0, 0, 1, 3, 3])), [0, 2, 3, 3, 5])
