@@ -131,6 +131,18 @@ int spc_stride2_inverse_taps(spc_stream_t stream, const int32_t* coords,
                              const int32_t* fine_to_coarse, int64_t nf, int64_t nc,
                              int32_t* taps);
 
+/* Token-major table [8 n_parent * 27] of a tensor subdivided without
+ * `keep` (child c = 8p + d, spc_subdivide_map), derived from the parents'
+ * token-major table [n_parent * 27] (spc_map_build, not SPC_MAP_MESH):
+ * the child at 2x + d + delta(o) is child e of the parent at x + j, per
+ * axis j = floor((d + delta) / 2), e = d + delta - 2j, and exists exactly
+ * when that parent does.  Bit-exact with spc_map_build's token_major on the
+ * child coordinates (sentinel 8 n_parent), without the hash build.  No
+ * reference counterpart: the reference rebuilds the table from the
+ * subdivided coordinates (SRC/sparse_ops.cpp:312-371). */
+int spc_subdivide_neighbors(spc_stream_t stream, const int32_t* parent_token_major,
+                            int64_t n_parent, int32_t* child_token_major);
+
 /* Index composition: out[i] = rows[idx[i]] for idx[i] in [0, n_rows), else
  * -1 (idx and out 16-byte aligned).  With idx a neighbour table over
  * subdivided children and rows the children's parent rows (the `parent`

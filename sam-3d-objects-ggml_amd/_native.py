@@ -64,6 +64,7 @@ def lib() -> ctypes.CDLL:
     L.spc_downsample_map.argtypes = [_P, _P, _I64, _I64, _I32, _P, _P, _P, _P, _P, _P, _P, _SZ]
     L.spc_stride2_inverse_taps.argtypes = [_P, _P, _P, _I64, _I64, _P]
     L.spc_compose_rows.argtypes = [_P, _P, _I64, _P, _I64, _P]
+    L.spc_subdivide_neighbors.argtypes = [_P, _P, _I64, _P]
     L.spc_subdivide_workspace_bytes.restype = _SZ
     L.spc_subdivide_workspace_bytes.argtypes = [_I64]
     L.spc_subdivide_map.argtypes = [_P, _P, _I64, _P, _P, _P, _P, _P, _SZ]
@@ -228,6 +229,21 @@ def downsample_map(coords: torch.Tensor, n_batch: int, resolution: int,
     k = nc.value
     return DownsampleMap(nf, k, f2c, cc[:k], ch[: 8 * k], cnt[:k],
                          None if taps is None else taps[: 8 * k])
+
+
+def subdivide_neighbors(parent_token_major: torch.Tensor, n_parent: int) -> SubmMap:
+    """Token-major map of the children of a subdivision without pruning,
+    derived from the parents' token-major table (spc_subdivide_neighbors);
+    equal to map_build(child coords, outputs="token")."""
+    _need_gpu(parent_token_major)
+    ptm = parent_token_major.to(torch.int32).contiguous()
+    if ptm.numel() != 27 * n_parent:
+        raise ValueError("parent table must hold 27 * n_parent entries")
+    nc = 8 * n_parent
+    ctm = torch.empty(27 * nc, dtype=torch.int32, device=ptm.device)
+    st = lib().spc_subdivide_neighbors(_stream(ptm.device), _ptr(ptm), n_parent, _ptr(ctm))
+    _check("spc_subdivide_neighbors", st)
+    return SubmMap(nc, ctm, None, None, None, None)
 
 
 def compose_rows(idx: torch.Tensor, rows: torch.Tensor) -> torch.Tensor:

@@ -26,7 +26,8 @@ import torch.nn as nn
 
 from . import _native as nat
 from .sparse import (SparseConv3d, SparseDownsample, SparseGroupNorm32, SparseLinear, SparseSiLU,
-                     SparseSubdivide, SparseTensor, SparseUpsample, batch_offsets)
+                     SparseSubdivide, SparseTensor, SparseUpsample, _subm_map, batch_offsets,
+                     max_item_rows)
 
 __all__ = ["LayerNorm32", "SparseResBlock3d", "SparseSubdivideBlock3d"]
 
@@ -134,19 +135,21 @@ class SparseSubdivideBlock3d(nn.Module):
         conv1, conv2 = self.out_layers[0], self.out_layers[3]
         coords, parent = self.sub.map(x)
         nc = coords.shape[0]
+        offs, rows_max = batch_offsets(x), max_item_rows(x)
         # silu(GroupNorm(x)) on the parent rows only: the children's features
         # are copies of them, so conv1 reads the parents through the child
         # neighbour table composed with the parent rows (bit-identical to the
         # conv over the copies, without writing 8x the rows)
-        h_par = nat.group_norm_silu(x.feats, batch_offsets(x), gn0.num_groups, gn0.weight,
-                                    gn0.bias, gn0.eps, silu=True)
-        cm = nat.map_build(coords.contiguous(), outputs="token")
+        h_par = nat.group_norm_silu(x.feats, offs, gn0.num_groups, gn0.weight, gn0.bias, gn0.eps,
+                                    silu=True, max_rows=rows_max)
+        # the child table follows from the parents' one (no hash build)
+        cm = nat.subdivide_neighbors(_subm_map(x).token_major, x.feats.shape[0])
         composed = nat.compose_rows(cm.token_major, parent)
         plan1 = nat.conv_plan(composed, ntaps=27, n_out=nc, n_in=x.feats.shape[0])
         h = self.sub.assemble(x, coords, conv1._conv(h_par, composed, nc, plan1))
         h.data.cached("subm3", lambda c: cm)  # conv2's map: the same child coordinates
-        h = h.replace(nat.group_norm_silu(h.feats, batch_offsets(h), gn1.num_groups, gn1.weight,
-                                          gn1.bias, gn1.eps, silu=True))
+        h = h.replace(nat.group_norm_silu(h.feats, 8 * offs, gn1.num_groups, gn1.weight, gn1.bias,
+                                          gn1.eps, silu=True, max_rows=8 * rows_max))
         # the skip on the parent rows (a 1x1x1 conv is row-wise), added to
         # child t from row parent[t] in conv2's epilogue
         skip = x.feats if isinstance(self.skip_connection, nn.Identity) \

@@ -336,6 +336,34 @@ __global__ void compose_rows_kernel(const int32_t* __restrict__ idx, int64_t n,
     }
 }
 
+// Child table of a fully subdivided tensor from the parents' table: child
+// c = 8p + d (d = dx*4 + dy*2 + dz) at 2*x_p + d; its neighbour at offset
+// delta(o) is child e of parent p + j, per axis s = d + delta, j = floor(s/2),
+// e = s - 2j.  Non-owning (duplicate) parents give children with no
+// neighbours, as the hash table's first-row rule gives for their copies.
+__global__ __launch_bounds__(256) void subdivide_neighbors_kernel(const int32_t* __restrict__ ptm,
+                                                                  int64_t np,
+                                                                  int32_t* __restrict__ ctm) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t nc = 8 * np;
+    if (e >= nc * 27) return;
+    const int64_t c = e / 27;
+    const int o = (int)(e - c * 27);
+    const int64_t p = c >> 3;
+    const int d = (int)(c & 7);
+    const int32_t* pr = ptm + p * 27;
+    int32_t out = (int32_t)nc;
+    if (pr[13] == (int32_t)p) {
+        const int sx = (d >> 2) + o / 9 - 1, sy = ((d >> 1) & 1) + (o / 3) % 3 - 1,
+                  sz = (d & 1) + o % 3 - 1;
+        const int jx = sx >> 1, jy = sy >> 1, jz = sz >> 1;  // floor division (arithmetic shift)
+        const int q = pr[(jx + 1) * 9 + (jy + 1) * 3 + (jz + 1)];
+        if (q >= 0 && q < np)
+            out = q * 8 + (sx - 2 * jx) * 4 + (sy - 2 * jy) * 2 + (sz - 2 * jz);
+    }
+    ctm[e] = out;
+}
+
 inline unsigned grid_for(int64_t n, int threads) { return (unsigned)((n + threads - 1) / threads); }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -555,6 +583,24 @@ int spc_stride2_inverse_taps(spc_stream_t stream, const int32_t* coords,
     }
     stride2_inverse_kernel<<<grid_for(nf, 256), 256, 0, s>>>(
         reinterpret_cast<const int4*>(coords), fine_to_coarse, nf, (int32_t)nc, taps);
+    SPC_HIP(hipGetLastError());
+    return SPC_OK;
+}
+
+int spc_subdivide_neighbors(spc_stream_t stream, const int32_t* parent_token_major,
+                            int64_t n_parent, int32_t* child_token_major) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (n_parent < 0 || n_parent > INT32_MAX / (8 * 27)) {
+        set_last_error("spc_subdivide_neighbors: n_parent = %lld out of range", (long long)n_parent);
+        return SPC_BAD_SHAPE;
+    }
+    if (n_parent == 0) return SPC_OK;
+    if (!parent_token_major || !child_token_major) {
+        set_last_error("spc_subdivide_neighbors: null table");
+        return SPC_BAD_ARG;
+    }
+    subdivide_neighbors_kernel<<<grid_for(n_parent * 8 * 27, 256), 256, 0, s>>>(
+        parent_token_major, n_parent, child_token_major);
     SPC_HIP(hipGetLastError());
     return SPC_OK;
 }

@@ -719,6 +719,11 @@ def batch_offsets(x: SparseTensor) -> torch.Tensor:
     return torch.tensor(offs, dtype=torch.int64).to(x.feats.device, non_blocking=True)
 
 
+def max_item_rows(x: SparseTensor) -> int:
+    """Rows of the largest batch item (from the layout, no device sync)."""
+    return max((sl.stop - sl.start for sl in x.layout), default=0)
+
+
 class SparseGroupNorm32(nn.GroupNorm):
     """GroupNorm over each batch item's rows, computed in F32 and cast back
     (SP/norm.py:15-55), on spc_group_norm_stats / spc_group_norm_silu."""
@@ -728,7 +733,8 @@ class SparseGroupNorm32(nn.GroupNorm):
 
     def forward(self, input: SparseTensor) -> SparseTensor:
         return input.replace(nat.group_norm_silu(input.feats, batch_offsets(input), self.num_groups,
-                                                 self.weight, self.bias, self.eps, silu=False))
+                                                 self.weight, self.bias, self.eps, silu=False,
+                                                 max_rows=max_item_rows(input)))
 
 
 class SparseSiLU(nn.SiLU):
@@ -813,7 +819,11 @@ class SparseSubdivide(nn.Module):
         """The subdivided tensor with the given child features."""
         data = SparseTensorData(feats, coords, [2 * s for s in input.data.spatial_shape],
                                 input.data.batch_size)
-        out = SparseTensor(data, shape=input.shape)
+        layout = None
+        if coords.shape[0] == 8 * input.coords.shape[0]:
+            # no pruning: item b's children are rows 8 * (its parent rows)
+            layout = [slice(8 * sl.start, 8 * sl.stop) for sl in input.layout]
+        out = SparseTensor(data, shape=input.shape, layout=layout)
         out._scale = input._scale * 2
         out._spatial_cache = input._spatial_cache
         return out

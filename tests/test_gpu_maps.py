@@ -128,3 +128,25 @@ def test_downsample_map_matches_oracle(spc, orc, dev, name):
     assert np.array_equal(d.children.cpu().numpy(), ref["children"])
     assert np.array_equal(d.counts.cpu().numpy(), ref["counts"])
     assert np.array_equal(d.stride2_taps.cpu().numpy(), taps_ref)
+
+
+@pytest.mark.parametrize("name", ["sphere64", "ellipsoids4", "random_dups_unsorted", "single",
+                                  "ragged_193"])
+def test_subdivide_neighbors_matches_child_map(spc, orc, dev, name):
+    """The child table derived from the parents' table equals the hash-built
+    table of the subdivided coordinates and the oracle's table, duplicates
+    (first-row rule) and batch boundaries included."""
+    import torch
+
+    nat = spc._native
+    coords = _coord_sets(spc)[name]
+    n = coords.shape[0]
+    _case(f"subdivide_neighbors {name} np={n}")
+    c = torch.from_numpy(coords).to(dev)
+    pm = nat.map_build(c, outputs="token")
+    child, par = nat.subdivide_map(c)
+    got = nat.subdivide_neighbors(pm.token_major, n).token_major
+    want = nat.map_build(child.contiguous(), outputs="token").token_major
+    assert torch.equal(got, want)
+    ref = orc.conv_table_slat(child.cpu().numpy())
+    assert np.array_equal(got.cpu().numpy().reshape(-1), ref.reshape(-1))
