@@ -143,6 +143,24 @@ int spc_stride2_inverse_taps(spc_stream_t stream, const int32_t* coords,
 int spc_subdivide_neighbors(spc_stream_t stream, const int32_t* parent_token_major,
                             int64_t n_parent, int32_t* child_token_major);
 
+/* Merged-tap form of the 3x3x3 submanifold conv over a tensor subdivided
+ * without `keep`, whose child features are copies of the parent rows
+ * (SparseSubdivide, SP/spatial.py:120-127): child c = 8p + d (d = dx*4 +
+ * dy*2 + dz) has a neighbour at offset k exactly when the parent at
+ * floor((d + k) / 2) exists, so its 27 taps read only 8 parent rows, at
+ * offsets j with j_a in {d_a - 1, d_a}.  y[c] = b + sum_t W'(d, t) h[q_t]
+ * with W'(d, t) the sum of the W_k that land on parent offset t.  Writes
+ * idx [64 n_parent] (idx[c*8 + t], t = ix*4 + iy*2 + iz at j_a = d_a - 1 +
+ * i_a; -1 when missing) and the class-major row order row_perm
+ * [8 class_rows] (perm[d*class_rows + i] = 8i + d, -1 for i >= n_parent),
+ * class_rows a multiple of 256 and >= n_parent.  With spc_sparse_conv_
+ * classes (ntaps 8, n_classes 8, n_in n_parent, n_out 8 class_rows) this
+ * runs the child conv on the parent features with 8 instead of 27 taps.
+ * No reference counterpart. */
+int spc_subdivide_tap_classes(spc_stream_t stream, const int32_t* parent_token_major,
+                              int64_t n_parent, int64_t class_rows, int32_t* idx,
+                              int32_t* row_perm);
+
 /* Index composition: out[i] = rows[idx[i]] for idx[i] in [0, n_rows), else
  * -1 (idx and out 16-byte aligned).  With idx a neighbour table over
  * subdivided children and rows the children's parent rows (the `parent`
@@ -361,6 +379,20 @@ int spc_sparse_conv_fused(spc_stream_t stream, int dtype, const void* x, int w_d
                           void* y, const int32_t* idx, int idx_layout, const int32_t* row_perm,
                           const void* plan, int64_t ntaps, int64_t n_out, int64_t n_in,
                           int64_t cin, int64_t cout, const spc_conv_epilogue* epi);
+
+/* spc_sparse_conv_fused with weight classes: the rows of tile order
+ * [c * class_rows, (c + 1) * class_rows) (class_rows a multiple of 256)
+ * use taps c * ntaps .. c * ntaps + ntaps - 1 of packed weights holding
+ * n_classes * ntaps taps (spc_conv_pack_weights with that tap count, in the
+ * feature dtype; no Q8_0).  n_out <= class_rows * n_classes counts tile
+ * rows; with row_perm each tile row writes output row row_perm[v] (-1 =
+ * none), so y holds max(row_perm) + 1 rows.  No reference counterpart (the
+ * merged-tap child conv of spc_subdivide_tap_classes). */
+int spc_sparse_conv_classes(spc_stream_t stream, int dtype, const void* x, const void* w,
+                            const void* bias, void* y, const int32_t* idx, int idx_layout,
+                            const int32_t* row_perm, const void* plan, int64_t ntaps,
+                            int64_t n_out, int64_t n_in, int64_t cin, int64_t cout,
+                            int64_t class_rows, int64_t n_classes, const spc_conv_epilogue* epi);
 
 #ifdef __cplusplus
 }

@@ -65,6 +65,9 @@ def lib() -> ctypes.CDLL:
     L.spc_stride2_inverse_taps.argtypes = [_P, _P, _P, _I64, _I64, _P]
     L.spc_compose_rows.argtypes = [_P, _P, _I64, _P, _I64, _P]
     L.spc_subdivide_neighbors.argtypes = [_P, _P, _I64, _P]
+    L.spc_subdivide_tap_classes.argtypes = [_P, _P, _I64, _I64, _P, _P]
+    L.spc_sparse_conv_classes.argtypes = [_P, _INT, _P, _P, _P, _P, _P, _INT, _P, _P, _I64, _I64,
+                                          _I64, _I64, _I64, _I64, _I64, _P]
     L.spc_subdivide_workspace_bytes.restype = _SZ
     L.spc_subdivide_workspace_bytes.argtypes = [_I64]
     L.spc_subdivide_map.argtypes = [_P, _P, _I64, _P, _P, _P, _P, _P, _SZ]
@@ -246,6 +249,23 @@ def subdivide_neighbors(parent_token_major: torch.Tensor, n_parent: int) -> Subm
     return SubmMap(nc, ctm, None, None, None, None)
 
 
+def subdivide_tap_classes(parent_token_major: torch.Tensor, n_parent: int):
+    """(idx [64 n_parent], row_perm [8 class_rows], class_rows) of the
+    merged-tap child conv (spc_subdivide_tap_classes), class_rows = n_parent
+    rounded up to 256."""
+    _need_gpu(parent_token_major)
+    ptm = parent_token_major.to(torch.int32).contiguous()
+    if ptm.numel() != 27 * n_parent:
+        raise ValueError("parent table must hold 27 * n_parent entries")
+    class_rows = (n_parent + 255) // 256 * 256
+    idx = torch.empty(64 * n_parent, dtype=torch.int32, device=ptm.device)
+    perm = torch.empty(8 * class_rows, dtype=torch.int32, device=ptm.device)
+    st = lib().spc_subdivide_tap_classes(_stream(ptm.device), _ptr(ptm), n_parent, class_rows,
+                                         _ptr(idx), _ptr(perm))
+    _check("spc_subdivide_tap_classes", st)
+    return idx, perm, class_rows
+
+
 def compose_rows(idx: torch.Tensor, rows: torch.Tensor) -> torch.Tensor:
     """out[i] = rows[idx[i]] for idx[i] in [0, len(rows)), else -1
     (spc_compose_rows): a neighbour table over subdivided children composed
@@ -382,7 +402,8 @@ def sparse_conv(x: torch.Tensor, weight, bias: torch.Tensor | None,
                 cout: int | None = None, plan: torch.Tensor | None = None,
                 residual: torch.Tensor | None = None,
                 norm_mod: tuple | None = None,
-                residual_rows: torch.Tensor | None = None) -> torch.Tensor:
+                residual_rows: torch.Tensor | None = None,
+                class_rows: int = 0, n_classes: int = 1) -> torch.Tensor:
     """y = conv(x) through spc_sparse_conv_fused.  `weight` is a
     PackedWeights, a [Cout, ntaps, Cin] tensor in the feature dtype, or int8
     Q8_0 quants with w_scale (fp16 block scales).  idx None with ntaps 1 is
@@ -391,7 +412,9 @@ def sparse_conv(x: torch.Tensor, weight, bias: torch.Tensor | None,
     `residual_rows` (int32 [n_out]) residual is [R, Cout] and output row t
     adds residual[residual_rows[t]];
     `norm_mod` = (scale, shift, coords, eps) with f32 [n_batch, Cout] scale
-    and shift gives silu(norm(y) * (1 + scale[b]) + shift[b])."""
+    and shift gives silu(norm(y) * (1 + scale[b]) + shift[b]).  class_rows >
+    0 selects weight classes (spc_sparse_conv_classes): `weight` is then a
+    PackedWeights of n_classes * ntaps taps."""
     _need_gpu(x, bias, idx, row_perm, w_scale, residual, residual_rows)
     x = x.contiguous()
     dt = dtype_code(x.dtype)
@@ -400,7 +423,7 @@ def sparse_conv(x: torch.Tensor, weight, bias: torch.Tensor | None,
         _need_gpu(weight.data)
         wdt, layout, wptr, sptr = weight.w_dtype, W_PACKED, _ptr(weight.data), None
         cout = weight.cout
-        if weight.ntaps != ntaps or weight.cin != cin:
+        if weight.ntaps != ntaps * (n_classes if class_rows else 1) or weight.cin != cin:
             raise ValueError("packed weights do not match ntaps / cin")
     else:
         _need_gpu(weight)
@@ -452,6 +475,15 @@ def sparse_conv(x: torch.Tensor, weight, bias: torch.Tensor | None,
         epi.scale, epi.shift, epi.coords = _ptr(scale), _ptr(shift), _ptr(coords)
         epi.n_batch = scale.shape[0]
         keep += [scale, shift, coords]
+    if class_rows:
+        if not isinstance(weight, PackedWeights):
+            raise ValueError("weight classes need PackedWeights")
+        st = lib().spc_sparse_conv_classes(_stream(x.device), dt, _ptr(x), wptr, _ptr(bias),
+                                           _ptr(out), _ptr(idx), idx_layout, _ptr(row_perm),
+                                           _ptr(plan), ntaps, n_out, x.shape[0], cin, cout,
+                                           int(class_rows), int(n_classes), ctypes.byref(epi))
+        _check("spc_sparse_conv_classes", st)
+        return out
     st = lib().spc_sparse_conv_fused(_stream(x.device), dt, _ptr(x), wdt, layout, wptr, sptr,
                                      _ptr(bias), _ptr(out), _ptr(idx), idx_layout, _ptr(row_perm),
                                      _ptr(plan), ntaps, n_out, x.shape[0], cin, cout,

@@ -26,10 +26,27 @@ import torch.nn as nn
 
 from . import _native as nat
 from .sparse import (SparseConv3d, SparseDownsample, SparseGroupNorm32, SparseLinear, SparseSiLU,
-                     SparseSubdivide, SparseTensor, SparseUpsample, _subm_map, batch_offsets,
-                     max_item_rows)
+                     SparseSubdivide, SparseTensor, SparseUpsample, _run, _subm_map,
+                     batch_offsets, max_item_rows)
 
 __all__ = ["LayerNorm32", "SparseResBlock3d", "SparseSubdivideBlock3d"]
+
+
+def _tap_merge_matrix() -> torch.Tensor:
+    """[64, 27] 0/1 (F64): row d*8 + t (child class d = dx*4 + dy*2 + dz,
+    parent tap t = ix*4 + iy*2 + iz at offset j_a = d_a - 1 + i_a) has a 1 at
+    child tap o (offset k = (o//9 - 1, (o//3)%3 - 1, o%3 - 1)) when
+    floor((d_a + k_a) / 2) = j_a on every axis."""
+    m = torch.zeros(64, 27, dtype=torch.float64)
+    for d in range(8):
+        da = (d >> 2, (d >> 1) & 1, d & 1)
+        for t in range(8):
+            ja = tuple(da[a] - 1 + ((t >> (2 - a)) & 1) for a in range(3))
+            for o in range(27):
+                ka = (o // 9 - 1, (o // 3) % 3 - 1, o % 3 - 1)
+                if all((da[a] + ka[a]) // 2 == ja[a] for a in range(3)):
+                    m[d * 8 + t, o] = 1.0
+    return m
 
 
 class LayerNorm32(nn.LayerNorm):
@@ -100,10 +117,18 @@ class SparseSubdivideBlock3d(nn.Module):
 
     with out_layers = [conv 3x3x3, GroupNorm32, SiLU, conv 3x3x3] and skip a
     1x1x1 conv when the channel count changes.  Runs as: GroupNorm
-    statistics + norm / SiLU / parent gather in one pass, conv1, GroupNorm
-    statistics + norm / SiLU, conv2 with the residual epilogue.  State-dict
-    keys are the reference's (act_layers.0.*, out_layers.0.conv.*,
-    out_layers.1.*, out_layers.3.conv.*, skip_connection.conv.*)."""
+    statistics + norm / SiLU on the parent rows, conv1 on the parents' rows
+    (the children's features are copies of them), GroupNorm statistics +
+    norm / SiLU, conv2 with the skip (computed on the parent rows) added in
+    its epilogue.  conv1 runs in merged-tap form by default (`merged_taps`):
+    a child's 27 taps land on 8 parent rows, so it runs as 8 taps with
+    summed weights per child class (spc_subdivide_tap_classes) -- 8 / 27 of
+    the MFMA work; the summed weights are rounded once to the feature
+    dtype, so the result agrees with the 27-tap conv to that rounding.
+    `merged_taps = False` runs the 27 taps over the composed child table
+    (bit-identical to the conv over the copied rows).  State-dict keys are
+    the reference's (act_layers.0.*, out_layers.0.conv.*, out_layers.1.*,
+    out_layers.3.conv.*, skip_connection.conv.*)."""
 
     def __init__(self, channels: int, resolution: int, out_channels: Optional[int] = None,
                  num_groups: int = 32):
@@ -129,6 +154,34 @@ class SparseSubdivideBlock3d(nn.Module):
         else:
             self.skip_connection = SparseConv3d(channels, self.out_channels, 1,
                                                 indice_key=f"res_{self.out_resolution}")
+        self.merged_taps = True
+        self._merged = None
+        self._merged_key = None
+
+    def _merged_weights(self, dtype: torch.dtype, device) -> nat.PackedWeights:
+        """conv1's weights summed per (child class d, parent tap t): W'[d*8 + t]
+        = sum of W_k over the child taps k with floor((d + k) / 2) = j(d, t),
+        formed in F64 and rounded once to the feature dtype; packed as 64
+        taps (cached per weight version)."""
+        conv1 = self.out_layers[0]
+        c = conv1.conv
+        key = (dtype, device, c.weight.data_ptr(), c.weight._version,
+               None if conv1._q8 is None else conv1._q8[0].data_ptr())
+        if self._merged is not None and self._merged_key == key:
+            return self._merged
+        cin, cout = c.in_channels, c.out_channels
+        if conv1._q8 is not None:
+            blocks, layout = conv1._q8
+            w = nat.q8_0_dequant(blocks.to(device), torch.float32)
+            w = (w.view(27, cout, cin).permute(1, 0, 2) if layout == "mesh"
+                 else w.view(cout, 27, cin))
+        else:
+            w = c.weight.detach().to(device=device).reshape(cout, 27, cin)
+        w = w.to(torch.float64).permute(1, 0, 2).reshape(27, cout * cin)
+        wm = torch.matmul(_tap_merge_matrix().to(device), w).reshape(64, cout, cin)
+        self._merged = nat.pack_weights(wm.to(dtype).contiguous(), layout=nat.W_TCK)
+        self._merged_key = key
+        return self._merged
 
     def forward(self, x: SparseTensor) -> SparseTensor:
         gn0, gn1 = self.act_layers[0], self.out_layers[1]
@@ -143,10 +196,23 @@ class SparseSubdivideBlock3d(nn.Module):
         h_par = nat.group_norm_silu(x.feats, offs, gn0.num_groups, gn0.weight, gn0.bias, gn0.eps,
                                     silu=True, max_rows=rows_max)
         # the child table follows from the parents' one (no hash build)
-        cm = nat.subdivide_neighbors(_subm_map(x).token_major, x.feats.shape[0])
-        composed = nat.compose_rows(cm.token_major, parent)
-        plan1 = nat.conv_plan(composed, ntaps=27, n_out=nc, n_in=x.feats.shape[0])
-        h = self.sub.assemble(x, coords, conv1._conv(h_par, composed, nc, plan1))
+        n_par = x.feats.shape[0]
+        pm = _subm_map(x).token_major
+        cm = nat.subdivide_neighbors(pm, n_par)
+        c1 = conv1.conv
+        if self.merged_taps and c1.in_channels % 32 == 0 and c1.out_channels % 32 == 0:
+            idx8, perm, crows = nat.subdivide_tap_classes(pm, n_par)
+            plan8 = nat.conv_plan(idx8, ntaps=8, n_out=8 * crows, n_in=n_par, row_perm=perm)
+            hp = h_par.detach()
+            y1 = _run(lambda: nat.sparse_conv(
+                hp, self._merged_weights(hp.dtype, hp.device), conv1._bias_operand(hp.dtype, hp.device),
+                idx8, ntaps=8, n_out=8 * crows, row_perm=perm, plan=plan8, class_rows=crows,
+                n_classes=8)[:nc], h_par, c1.weight, c1.bias)
+        else:
+            composed = nat.compose_rows(cm.token_major, parent)
+            plan1 = nat.conv_plan(composed, ntaps=27, n_out=nc, n_in=n_par)
+            y1 = conv1._conv(h_par, composed, nc, plan1)
+        h = self.sub.assemble(x, coords, y1)
         h.data.cached("subm3", lambda c: cm)  # conv2's map: the same child coordinates
         h = h.replace(nat.group_norm_silu(h.feats, 8 * offs, gn1.num_groups, gn1.weight, gn1.bias,
                                           gn1.eps, silu=True, max_rows=8 * rows_max))

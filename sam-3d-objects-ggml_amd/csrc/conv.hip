@@ -168,8 +168,9 @@ int device_cu_count() {
     return n;
 }
 
-int check_shape(const char* fn, int64_t ntaps, int64_t cin, int64_t cout) {
-    if ((ntaps != 27 && ntaps != 8 && ntaps != 1) || cin <= 0 || cout <= 0 || cin % 32 != 0 ||
+int check_shape(const char* fn, int64_t ntaps, int64_t cin, int64_t cout, bool any_taps = false) {
+    const bool taps_ok = any_taps ? (ntaps >= 1 && ntaps <= 4096) : (ntaps == 27 || ntaps == 8 || ntaps == 1);
+    if (!taps_ok || cin <= 0 || cout <= 0 || cin % 32 != 0 ||
         cout % 32 != 0 || cin > (1 << 16) || cout > (1 << 16) ||
         ntaps * cin * cout * 4 >= ((int64_t)1 << 31)) {
         set_last_error("%s: unsupported shape ntaps=%lld cin=%lld cout=%lld (ntaps 27, 8 or 1, "
@@ -204,7 +205,8 @@ int spc_conv_pack_weights(spc_stream_t stream, int w_dtype, int w_layout, const 
                           const void* w_scale, int64_t ntaps, int64_t cin, int64_t cout,
                           void* packed) {
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const int st = check_shape("spc_conv_pack_weights", ntaps, cin, cout);
+    // any tap count: weight classes pack n_classes * ntaps taps
+    const int st = check_shape("spc_conv_pack_weights", ntaps, cin, cout, true);
     if (st != SPC_OK) return st;
     if (!w || !packed || !aligned16(packed) || (w_dtype == SPC_Q8_0 && !w_scale)) {
         set_last_error("spc_conv_pack_weights: null / misaligned pointer");
@@ -313,11 +315,13 @@ int spc_sparse_conv_plan(spc_stream_t stream, int dtype, const void* x, int w_dt
                                  idx_layout, row_perm, plan, ntaps, n_out, n_in, cin, cout, nullptr);
 }
 
-int spc_sparse_conv_fused(spc_stream_t stream, int dtype, const void* x, int w_dtype,
-                          int w_layout, const void* w, const void* w_scale, const void* bias,
-                          void* y, const int32_t* idx, int idx_layout, const int32_t* row_perm,
-                          const void* plan, int64_t ntaps, int64_t n_out, int64_t n_in,
-                          int64_t cin, int64_t cout, const spc_conv_epilogue* epi) {
+namespace {
+
+int conv_entry(spc_stream_t stream, int dtype, const void* x, int w_dtype, int w_layout,
+               const void* w, const void* w_scale, const void* bias, void* y, const int32_t* idx,
+               int idx_layout, const int32_t* row_perm, const void* plan, int64_t ntaps,
+               int64_t n_out, int64_t n_in, int64_t cin, int64_t cout, int64_t class_rows,
+               int64_t n_classes, const spc_conv_epilogue* epi) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int st = check_shape("spc_sparse_conv", ntaps, cin, cout);
     if (st != SPC_OK) return st;
@@ -352,6 +356,19 @@ int spc_sparse_conv_fused(spc_stream_t stream, int dtype, const void* x, int w_d
     a.cin = (int32_t)cin;
     a.cout = (int32_t)cout;
     a.packed = w_layout == SPC_W_PACKED;
+    if (class_rows > 0) {
+        if (class_rows % kTM != 0 || n_classes < 1 || n_classes * ntaps > 4096 ||
+            n_classes * ntaps * cin * cout * 4 >= ((int64_t)1 << 31) ||
+            n_out > class_rows * n_classes || !a.packed || w_dtype != dtype || w_dtype == SPC_Q8_0) {
+            set_last_error("spc_sparse_conv_classes: class_rows must be a positive multiple of %d "
+                           "with n_out <= class_rows * n_classes, weights packed in the feature "
+                           "dtype (got class_rows=%lld n_classes=%lld n_out=%lld)",
+                           kTM, (long long)class_rows, (long long)n_classes, (long long)n_out);
+            return SPC_BAD_ARG;
+        }
+        a.class_rows = class_rows;
+        a.n_classes = (int32_t)n_classes;
+    }
     if (plan && ((uintptr_t)plan & 255u) != 0) {
         set_last_error("spc_sparse_conv_plan: plan must be 256-byte aligned");
         return SPC_BAD_ARG;
@@ -426,6 +443,30 @@ int spc_sparse_conv_fused(spc_stream_t stream, int dtype, const void* x, int w_d
     }
     if (e != hipSuccess) return hip_status(e, "conv_kernel launch");
     return SPC_OK;
+}
+
+}  // namespace
+
+int spc_sparse_conv_fused(spc_stream_t stream, int dtype, const void* x, int w_dtype,
+                          int w_layout, const void* w, const void* w_scale, const void* bias,
+                          void* y, const int32_t* idx, int idx_layout, const int32_t* row_perm,
+                          const void* plan, int64_t ntaps, int64_t n_out, int64_t n_in,
+                          int64_t cin, int64_t cout, const spc_conv_epilogue* epi) {
+    return conv_entry(stream, dtype, x, w_dtype, w_layout, w, w_scale, bias, y, idx, idx_layout,
+                      row_perm, plan, ntaps, n_out, n_in, cin, cout, 0, 1, epi);
+}
+
+int spc_sparse_conv_classes(spc_stream_t stream, int dtype, const void* x, const void* w,
+                            const void* bias, void* y, const int32_t* idx, int idx_layout,
+                            const int32_t* row_perm, const void* plan, int64_t ntaps,
+                            int64_t n_out, int64_t n_in, int64_t cin, int64_t cout,
+                            int64_t class_rows, int64_t n_classes, const spc_conv_epilogue* epi) {
+    if (class_rows <= 0) {
+        set_last_error("spc_sparse_conv_classes: class_rows must be positive");
+        return SPC_BAD_ARG;
+    }
+    return conv_entry(stream, dtype, x, dtype, SPC_W_PACKED, w, nullptr, bias, y, idx, idx_layout,
+                      row_perm, plan, ntaps, n_out, n_in, cin, cout, class_rows, n_classes, epi);
 }
 
 void sam3d_spconv_f16_forward(spc_stream_t stream, const void* input, const void* weight,

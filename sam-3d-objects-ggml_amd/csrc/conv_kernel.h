@@ -70,6 +70,8 @@ struct ConvArgs {
     int32_t tiles_n;
     int64_t total_tiles;
     int64_t heavy_tiles;      // tiles of full row tiles (mapped XCD-major)
+    int64_t class_rows;       // > 0: rows [c * class_rows, (c + 1) * class_rows) use weight
+    int32_t n_classes;        //   taps c * ntaps .. (packed weights of n_classes * ntaps taps)
     int64_t tiles_per_xcd;
     const void* plan;         // per-row-tile setup from conv_plan_kernel, or null
     int32_t num_cu;           // compute units of the device (tile-width choice)
@@ -551,7 +553,10 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
     // Packed weights through a buffer resource: the panel offset is a scalar,
     // the lane offset a constant register, so a fragment load costs no vector
     // address arithmetic (and reads past the packed size return zeros).
-    const uint32_t wbytes = (uint32_t)((int64_t)a.ntaps * a.cin * a.cout * P::WB);
+    const uint32_t wbytes =
+        (uint32_t)((int64_t)a.ntaps * max(1, a.n_classes) * a.cin * a.cout * P::WB);
+    // weight class of the tile: its first packed tap (class_rows is a multiple of the tile height)
+    const uint32_t wtap0 = a.class_rows > 0 ? (uint32_t)(r0 / a.class_rows) * NTAPS : 0u;
     const __amdgpu_buffer_rsrc_t wrsrc =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a.w), (short)0, (int)wbytes, 0x00020000);
     // B operands of (tap o, chunk kc) for this wave's FN column blocks
@@ -561,8 +566,8 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
             const int c32 = (co0 + wn * WTN) / 32 + j;  // wave-uniform
             const int co = c32 * 32 + (lane & 31);
             if constexpr (PACKED) {
-                const uint32_t panel = ((uint32_t)o * (uint32_t)kch + (uint32_t)kc) * (uint32_t)ncol32 +
-                                       (uint32_t)c32;
+                const uint32_t panel =
+                    ((wtap0 + (uint32_t)o) * (uint32_t)kch + (uint32_t)kc) * (uint32_t)ncol32 + (uint32_t)c32;
                 const int poff = (int)(panel * (uint32_t)(P::NG * 1024));
 #pragma unroll
                 for (int g = 0; g < P::NG; ++g)

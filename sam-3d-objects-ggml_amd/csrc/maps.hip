@@ -16,6 +16,8 @@
 // sort of sort.hip.
 #include <climits>
 
+#include <algorithm>
+
 #include "common.h"
 
 namespace spc {
@@ -364,6 +366,38 @@ __global__ __launch_bounds__(256) void subdivide_neighbors_kernel(const int32_t*
     ctm[e] = out;
 }
 
+// Merged-tap tables of the 3x3x3 conv over a fully subdivided tensor, read
+// from the parents.  Child c = 8p + d sees, per axis, parent offsets
+// {d_a - 1, d_a}: tap t = ix*4 + iy*2 + iz at j_a = d_a - 1 + i_a.
+// idx[c*8 + t] = the parent row at x_p + j (or -1); perm is class-major:
+// perm[d*class_rows + i] = 8i + d for i < np, -1 for the padding rows.
+__global__ __launch_bounds__(256) void subdivide_tap_classes_kernel(const int32_t* __restrict__ ptm,
+                                                                    int64_t np, int64_t class_rows,
+                                                                    int32_t* __restrict__ idx,
+                                                                    int32_t* __restrict__ perm) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e < 64 * np) {
+        const int64_t c = e >> 3;
+        const int t = (int)(e & 7);
+        const int64_t p = c >> 3;
+        const int d = (int)(c & 7);
+        const int32_t* pr = ptm + p * 27;
+        int32_t out = -1;
+        if (pr[13] == (int32_t)p) {  // a duplicate parent's children have no neighbours
+            const int jx = (d >> 2) - 1 + (t >> 2), jy = ((d >> 1) & 1) - 1 + ((t >> 1) & 1),
+                      jz = (d & 1) - 1 + (t & 1);
+            const int32_t q = pr[(jx + 1) * 9 + (jy + 1) * 3 + (jz + 1)];
+            if (q >= 0 && q < np) out = q;
+        }
+        idx[e] = out;
+    }
+    if (e < 8 * class_rows) {
+        const int64_t d = e / class_rows;
+        const int64_t i = e - d * class_rows;
+        perm[e] = i < np ? (int32_t)(8 * i + d) : -1;
+    }
+}
+
 inline unsigned grid_for(int64_t n, int threads) { return (unsigned)((n + threads - 1) / threads); }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -601,6 +635,28 @@ int spc_subdivide_neighbors(spc_stream_t stream, const int32_t* parent_token_maj
     }
     subdivide_neighbors_kernel<<<grid_for(n_parent * 8 * 27, 256), 256, 0, s>>>(
         parent_token_major, n_parent, child_token_major);
+    SPC_HIP(hipGetLastError());
+    return SPC_OK;
+}
+
+int spc_subdivide_tap_classes(spc_stream_t stream, const int32_t* parent_token_major,
+                              int64_t n_parent, int64_t class_rows, int32_t* idx,
+                              int32_t* row_perm) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (n_parent < 0 || n_parent > INT32_MAX / 64 || class_rows < n_parent || class_rows % 256 != 0 ||
+        class_rows > INT32_MAX / 8) {
+        set_last_error("spc_subdivide_tap_classes: n_parent=%lld class_rows=%lld (a multiple of "
+                       "256, >= n_parent)", (long long)n_parent, (long long)class_rows);
+        return SPC_BAD_SHAPE;
+    }
+    if (class_rows == 0) return SPC_OK;
+    if (!parent_token_major || !idx || !row_perm) {
+        set_last_error("spc_subdivide_tap_classes: null argument");
+        return SPC_BAD_ARG;
+    }
+    const int64_t work = std::max<int64_t>(64 * n_parent, 8 * class_rows);
+    subdivide_tap_classes_kernel<<<grid_for(work, 256), 256, 0, s>>>(parent_token_major, n_parent,
+                                                                     class_rows, idx, row_perm);
     SPC_HIP(hipGetLastError());
     return SPC_OK;
 }

@@ -275,8 +275,17 @@ def test_subdivide_block(spc, orc, dev, cin, cout):
                                         oracle.BF16)
     assert np.array_equal(y.coords.cpu().numpy(), child)
     assert max_rel(from_dev(y.feats), ref) <= MAXREL
-    # the block reads parent rows through composed tables; the same block
-    # over materialised child copies gives the same bits
+    # merged taps: the same block with the 27-tap conv1 agrees to the
+    # rounding of the summed weights; the 27-tap form reads parent rows
+    # through composed tables and gives the same bits as the block over
+    # materialised child copies
+    assert blk.merged_taps
+    blk.merged_taps = False
+    with torch.no_grad():
+        y27 = blk(xt)
+    blk.merged_taps = True
+    assert max_rel(from_dev(y.feats), from_dev(y27.feats)) <= 1e-2
+    y = y27
     nat, sp = spc._native, spc.sparse
     with torch.no_grad():
         cc, par = blk.sub.map(xt)
@@ -289,3 +298,37 @@ def test_subdivide_block(spc, orc, dev, cin, cout):
                                           gn1.eps))
         want = blk.out_layers[3](h) + blk.skip_connection(xs)
     assert torch.equal(y.feats, want.feats)
+
+
+def test_subdivide_block_merged_taps_f32(spc, orc, dev):
+    """F32 features: the merged-tap conv1 (weights summed in F64, rounded to
+    F32) against the 27-tap conv1, and both against the oracle's block."""
+    import oracle
+    import torch
+
+    blocks = spc.blocks
+    coords = spc.workloads.random_voxels(1200, 14, batches=2, seed=81)
+    n = coords.shape[0]
+    _case(f"SparseSubdivideBlock3d f32 merged vs 27 taps N={n} 64->32")
+    torch.manual_seed(5)
+    blk = blocks.SparseSubdivideBlock3d(64, 14, 32).to(dev)
+    with torch.no_grad():
+        for prm in blk.out_layers[3].parameters():
+            prm.normal_(0, 0.05)
+    x = spc.workloads.normal((n, 64), 1.0, seed=82)
+    xt = spc.sparse.SparseTensor(torch.from_numpy(x).to(dev), torch.from_numpy(coords).to(dev))
+    with torch.no_grad():
+        ym = blk(xt).feats
+        blk.merged_taps = False
+        y27 = blk(xt).feats
+    assert torch.allclose(ym, y27, rtol=1e-4, atol=1e-5)
+    f = lambda t: t.detach().float().cpu().numpy()  # noqa: E731
+    p = {"gn0_w": f(blk.act_layers[0].weight), "gn0_b": f(blk.act_layers[0].bias),
+         "conv1_w": f(blk.out_layers[0].conv.weight).reshape(32, 27, 64),
+         "conv1_b": f(blk.out_layers[0].conv.bias),
+         "gn1_w": f(blk.out_layers[1].weight), "gn1_b": f(blk.out_layers[1].bias),
+         "conv2_w": f(blk.out_layers[3].conv.weight).reshape(32, 27, 32),
+         "conv2_b": f(blk.out_layers[3].conv.bias),
+         "skip_w": f(blk.skip_connection.conv.weight), "skip_b": f(blk.skip_connection.conv.bias)}
+    _, ref = oracle.subdivide_block(orc, x, coords, p, 32, oracle.F32)
+    assert np.allclose(ym.cpu().numpy(), ref, rtol=1e-4, atol=1e-4)

@@ -67,3 +67,48 @@ def test_group_norm_items_matches_torch():
     z = oracle.group_norm_items(np.ones((4, 64), np.float32), np.array([0, 4]), 32, None, b)
     assert np.allclose(z, np.broadcast_to(b, z.shape))
     assert np.array_equal(oracle.batch_offsets(np.array([0, 0, 1, 3, 3])), [0, 2, 3, 3, 5])
+
+
+def test_tap_merge_matrix_reproduces_child_conv(spc, orc):
+    """The merged-tap form of the subdivided child conv (8 parent taps per
+    child class with summed weights) equals the 27-tap conv over the copied
+    rows on the oracle's child table (F64, every batch / boundary case of a
+    random support)."""
+    import importlib
+
+    import oracle
+
+    blocks = importlib.import_module(spc.__name__ + ".blocks")
+    rng = np.random.default_rng(3)
+    coords = oracle_voxels(rng)
+    npar = coords.shape[0]
+    child, par = orc.subdivide(coords)
+    ptab = orc.conv_table_slat(coords).reshape(npar, 27)
+    ctab = orc.conv_table_slat(child).reshape(-1, 27)
+    ci, co = 5, 3
+    w = rng.standard_normal((co, 27, ci))
+    xp = rng.standard_normal((npar, ci))
+    xc = np.vstack([xp[par], np.zeros((1, ci))])           # row nc = missing
+    y27 = np.einsum("oci,noi->nc", w.transpose(1, 0, 2), xc[ctab])
+    m = blocks._tap_merge_matrix().numpy()
+    wm = np.einsum("vo,coi->vci", m, w)                     # [64, co, ci]
+    xq = np.vstack([xp, np.zeros((1, ci))])                 # row npar = missing
+    nc = child.shape[0]
+    c = np.arange(nc)
+    p, d = c // 8, c % 8
+    y8 = np.zeros((nc, co))
+    for t in range(8):
+        j = [(d >> 2) - 1 + (t >> 2), ((d >> 1) & 1) - 1 + ((t >> 1) & 1), (d & 1) - 1 + (t & 1)]
+        o = (j[0] + 1) * 9 + (j[1] + 1) * 3 + (j[2] + 1)
+        q = ptab[p, o]
+        y8 += np.einsum("nci,ni->nc", wm[d * 8 + t], xq[q])
+    assert np.allclose(y8, y27, rtol=1e-12, atol=1e-12)
+
+
+def oracle_voxels(rng):
+    """Two batch items of random voxels in a 6^3 box (boundaries included)."""
+    pts = []
+    for b in range(2):
+        v = np.unique(rng.integers(0, 6, size=(60, 3)), axis=0)
+        pts.append(np.hstack([np.full((v.shape[0], 1), b), v]))
+    return np.ascontiguousarray(np.vstack(pts), dtype=np.int32)
