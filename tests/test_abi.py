@@ -52,3 +52,32 @@ def test_cpu_tensors_are_rejected(spc):
     with pytest.raises(RuntimeError, match="GPU only"):
         spc._native.sparse_conv(x, torch.zeros((32, 27, 32), dtype=torch.bfloat16), None,
                                 torch.zeros(108, dtype=torch.int32), ntaps=27, n_out=4)
+
+
+def test_block_entries_validate_before_device_work(spc):
+    """The block entry points reject bad shapes on the host, with a message,
+    before any device work (no GPU needed)."""
+    nat = spc._native
+    L = nat.lib()
+    fake = 1 << 12  # aligned, never dereferenced: validation fails first
+    assert L.spc_subdivide_tap_classes(None, fake, 1000, 1000, fake, fake) == nat.BAD_SHAPE
+    assert b"multiple of" in L.spc_last_error()
+    assert L.spc_subdivide_tap_classes(None, fake, 1000, 768, fake, fake) == nat.BAD_SHAPE
+    assert L.spc_subdivide_neighbors(None, fake, -1, fake) == nat.BAD_SHAPE
+    assert L.spc_compose_rows(None, fake, 10, fake, -1, fake) == nat.BAD_SHAPE
+    assert L.spc_compose_rows(None, fake + 4, 10, fake, 5, fake) == nat.BAD_ARG  # misaligned idx
+    # weight classes: class_rows must be a positive multiple of 256 covering n_out
+    args = (None, nat.BF16, fake, fake, None, fake, fake, nat.IDX_TOKEN_MAJOR, None, None, 8)
+    assert L.spc_sparse_conv_classes(*args, 1024, 64, 64, 32, 0, 8, None) == nat.BAD_ARG
+    assert L.spc_sparse_conv_classes(*args, 1024, 64, 64, 32, 100, 8, None) == nat.BAD_ARG
+    assert L.spc_sparse_conv_classes(*args, 4096, 64, 64, 32, 256, 8, None) == nat.BAD_ARG
+    assert b"class_rows" in L.spc_last_error()
+    # GroupNorm shapes
+    ws = L.spc_group_norm_workspace_bytes(1, 21766, 32)
+    assert ws >= 32 * 2 * 8 * (21766 // 1024)
+    assert L.spc_group_norm_stats(None, nat.BF16, fake, 1028, 32, fake, 1, 100, 1e-5, fake, fake,
+                                  ws) == nat.BAD_SHAPE
+    assert L.spc_group_norm_stats(None, nat.BF16, fake, 96, 32, fake, 1, 100, 1e-5, fake, fake,
+                                  0) == nat.BAD_ARG  # workspace too small
+    assert L.spc_group_norm_silu(None, nat.BF16, fake, 10, 100, 32, fake, 1, fake, None, None, 1,
+                                 None, 10, fake) == nat.BAD_SHAPE  # c not a multiple of groups
