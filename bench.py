@@ -50,6 +50,8 @@ def parse():
     ap.add_argument("--order", choices=["natural", "mask"], default="natural",
                     help="row processing order of the conv kernel")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--fused-only", action="store_true",
+                    help="configs 6 / 7: time the fused block only (no unfused comparison)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target duration of the all-core CPU baseline sample (5 runs)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -454,11 +456,13 @@ def bench_res_block(spc, nat, wl, orc, coords, c_dev, dev, args, workload):
             return h + xt
 
     ms_f, _ = time_gpu(fused, args.steps, args.warmup)
-    ms_u, _ = time_gpu(unfused, args.steps, args.warmup)
-    diff = float((fused().feats.float() - unfused().feats.float()).abs().max())
+    ms_u = diff = None
+    if not args.fused_only:
+        ms_u, _ = time_gpu(unfused, args.steps, args.warmup)
+        diff = float((fused().feats.float() - unfused().feats.float()).abs().max())
     return {"metric": f"config 6: {workload}", "value": n / (ms_f / 1e3) / 1e6, "unit": "Mvoxel/s",
-            "ms_per_step": ms_f, "unfused_ms": ms_u, "speedup": ms_u / ms_f, "dtype": "bf16",
-            "max_abs_diff_fused_vs_unfused": diff,
+            "ms_per_step": ms_f, "unfused_ms": ms_u, "speedup": ms_u / ms_f if ms_u else None,
+            "dtype": "bf16", "max_abs_diff_fused_vs_unfused": diff,
             "config": {"workload": workload, "n_voxels": n, "channels": 128, "batch": 4}}
 
 
@@ -502,13 +506,15 @@ def bench_subdivide_block(spc, nat, wl, orc, coords, c_dev, dev, args, workload)
             return h + blk.skip_connection(xs)
 
     ms_f, _ = time_gpu(fused, args.steps, args.warmup)
-    ms_u, _ = time_gpu(unfused, args.steps, args.warmup)
     yf = fused()
     nc = yf.feats.shape[0]
-    diff = float((yf.feats.float() - unfused().feats.float()).abs().max())
+    ms_u = diff = None
+    if not args.fused_only:
+        ms_u, _ = time_gpu(unfused, args.steps, args.warmup)
+        diff = float((yf.feats.float() - unfused().feats.float()).abs().max())
     return {"metric": f"config 7: {workload}", "value": nc / (ms_f / 1e3) / 1e6, "unit": "Mvoxel/s",
-            "ms_per_step": ms_f, "unfused_ms": ms_u, "speedup": ms_u / ms_f, "dtype": "bf16",
-            "max_abs_diff_fused_vs_unfused": diff,
+            "ms_per_step": ms_f, "unfused_ms": ms_u, "speedup": ms_u / ms_f if ms_u else None,
+            "dtype": "bf16", "max_abs_diff_fused_vs_unfused": diff,
             "config": {"workload": workload, "n_parents": n, "n_children": nc, "cin": 768,
                        "cout": 192}}
 
