@@ -498,11 +498,15 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
         tile_mask = (uint32_t)misc[1];
         fast = misc[2] != 0;
     } else {
-        const TileLds L{reinterpret_cast<uint32_t*>(Au), sidx, tlw, urow, srow, wsum, misc};
-        tile_setup<NTAPS, NT, PD>(a, r0, L);
-        tile_mask = (uint32_t)misc[0];
-        U = misc[3];
-        fast = misc[4] != 0;
+        if constexpr (kWinWords % NT == 0) {
+            const TileLds L{reinterpret_cast<uint32_t*>(Au), sidx, tlw, urow, srow, wsum, misc};
+            tile_setup<NTAPS, NT, PD>(a, r0, L);
+            tile_mask = (uint32_t)misc[0];
+            U = misc[3];
+            fast = misc[4] != 0;
+        } else {
+            return;  // wave counts that do not divide the setup are launched with a plan only
+        }
     }
     // tile-uniform values: keep them (and the control flow they drive) scalar
     U = __builtin_amdgcn_readfirstlane(U);
@@ -864,10 +868,11 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
                 lds_barrier();  // every wave is done reading the stage
                 {
                     const int64_t koff = (int64_t)kc * KC * ES;
-                    constexpr int UPT = TM * kSegs / NT;
+                    constexpr int UPT = (TM * kSegs + NT - 1) / NT;
 #pragma unroll
                     for (int j = 0; j < UPT; ++j) {
                         const int u = j * NT + tid;
+                        if (TM * kSegs % NT != 0 && u >= TM * kSegs) break;
                         const int32_t src = src_of(o, u >> 2);
                         u32x4 v = zero4;
                         if (src >= 0)
@@ -894,7 +899,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
     // conv outputs go to an F32 LDS tile; groups of TN/4 lanes then take one
     // row each (four channels per lane, four rows in flight per lane group),
     // with group-local shuffles for the mean and the biased variance.
-    if (a.epi_mode == SPC_EPI_NORM_MOD_SILU) {
+    if constexpr (TN <= 128) if (a.epi_mode == SPC_EPI_NORM_MOD_SILU) {
         constexpr int FP = TN + 4;           // f32 row pitch (16-byte multiple)
         static_assert(TM * FP * 4 <= 2 * STAGE * 16, "f32 output tile fits the A stage");
         constexpr int G = TN / 4;            // lanes per row
@@ -1105,6 +1110,16 @@ hipError_t dispatch_tn(hipStream_t s, const ConvArgs& a) {
     if (a.epi_mode == SPC_EPI_NORM_MOD_SILU) {
         if (a.cout > 128) return hipErrorInvalidValue;  // rows wider than one tile
         tn = a.cout;                                    // one tile covers the row
+    }
+    // widths 128 does not divide but 192 does (the mesh decoder's 768 / 4):
+    // one 192-column tile of 4 waves (2 x 2, 128x96 wave tiles, one per
+    // SIMD) instead of three 64-column tiles of 64x32 wave tiles, which read
+    // each A fragment for half the MFMA work and are LDS-bound.  Packed
+    // 16-bit weights, and only once the row tiles alone fill the device.
+    if constexpr (!Q8 && PACKED && sizeof(T) == 2) {
+        if (a.cout % 192 == 0 && a.cout % 128 != 0 && a.epi_mode != SPC_EPI_NORM_MOD_SILU &&
+            tiles_m * (a.cout / 192) >= a.num_cu)
+            return launch_conv<T, Q8, PACKED, NTAPS, 192, 2, 2>(s, a);
     }
     if (tn == 128) {
         if constexpr (Q8) return launch_conv<T, Q8, PACKED, NTAPS, 128, 2, 2>(s, a);

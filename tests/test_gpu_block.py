@@ -332,3 +332,41 @@ def test_subdivide_block_merged_taps_f32(spc, orc, dev):
          "skip_w": f(blk.skip_connection.conv.weight), "skip_b": f(blk.skip_connection.conv.bias)}
     _, ref = oracle.subdivide_block(orc, x, coords, p, 32, oracle.F32)
     assert np.allclose(ym.cpu().numpy(), ref, rtol=1e-4, atol=1e-4)
+
+
+def test_subdivide_block_192_channels(spc, orc, dev):
+    """C_out = 192 over 75k children (the 192-column conv tiles): merged taps
+    against the 27-tap conv1, and the 27-tap block bit-identical to the block
+    over materialised child rows."""
+    import torch
+
+    blocks, nat, sp = spc.blocks, spc._native, spc.sparse
+    coords = spc.workloads.random_voxels(9600, 40, batches=2, seed=95)
+    n = coords.shape[0]
+    assert 8 * n >= 256 * 256
+    _case(f"SparseSubdivideBlock3d bf16 N={n} -> {8 * n} children 64->192")
+    torch.manual_seed(6)
+    blk = blocks.SparseSubdivideBlock3d(64, 40, 192).to(dev)
+    with torch.no_grad():
+        for prm in blk.out_layers[3].parameters():
+            prm.normal_(0, 0.02)
+    blk = blk.to(torch.bfloat16)
+    blk.act_layers[0].float()
+    blk.out_layers[1].float()
+    x = spc.workloads.normal((n, 64), 1.0, seed=96)
+    xt = sp.SparseTensor(_dev_feats(orc, x, "bf16", dev), torch.from_numpy(coords).to(dev))
+    with torch.no_grad():
+        ym = blk(xt)
+        blk.merged_taps = False
+        y27 = blk(xt)
+        cc, par = blk.sub.map(xt)
+        gn0, gn1 = blk.act_layers[0], blk.out_layers[1]
+        h = blk.sub.assemble(xt, cc, nat.group_norm_silu(
+            xt.feats, sp.batch_offsets(xt), 32, gn0.weight, gn0.bias, gn0.eps, rows=par))
+        xs = blk.sub.assemble(xt, cc, nat.gather_rows(xt.feats, par))
+        h = blk.out_layers[0](h)
+        h = h.replace(nat.group_norm_silu(h.feats, sp.batch_offsets(h), 32, gn1.weight, gn1.bias,
+                                          gn1.eps))
+        want = blk.out_layers[3](h) + blk.skip_connection(xs)
+    assert torch.equal(y27.feats, want.feats)
+    assert max_rel(from_dev(ym.feats), from_dev(y27.feats)) <= 1e-2

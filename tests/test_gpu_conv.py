@@ -66,6 +66,38 @@ def test_bf16_channels(spc, orc, dev, cin, cout):
     assert torch.equal(y, yp)
 
 
+@pytest.mark.parametrize("ntaps", [27, 8])
+def test_bf16_cout192_wide_tiles(spc, orc, dev, ntaps):
+    """C_out = 192 with at least 256 row tiles runs the 192-column tile (four
+    waves of 128x96): sampled rows against the oracle, and bit-identical to
+    the unpacked-weight launch, which runs three 64-column tiles."""
+    import torch
+
+    nat = spc._native
+    if ntaps == 27:
+        coords = spc.workloads.random_voxels(90000, 64, batches=2, seed=91)
+        n = coords.shape[0]
+        m = nat.map_build(torch.from_numpy(coords).to(dev))
+        idx, n_out, n_in = m.token_major, n, n
+    else:  # stride-2 2x2x2 onto the coarse rows
+        coords = spc.workloads.random_voxels(400000, 128, batches=1, seed=92)
+        d = nat.downsample_map(torch.from_numpy(coords).to(dev), 1, 128, with_taps=True)
+        idx, n_out, n_in = d.stride2_taps, d.nc, coords.shape[0]
+    assert n_out >= 256 * 256
+    _case(f"bf16 {ntaps}-tap conv N_out={n_out} 64->192 (192-column tiles)")
+    x, w, b = _bf16_inputs(spc, orc, n_in, 64, 192, ntaps=ntaps, seed=93)
+    wd = to_dev_bf16(w, dev)
+    xd, bd = to_dev_bf16(x, dev), to_dev_bf16(b, dev)
+    plan = nat.conv_plan(idx, ntaps=ntaps, n_out=n_out, n_in=n_in)
+    yp = nat.sparse_conv(xd, nat.pack_weights(wd), bd, idx, ntaps=ntaps, n_out=n_out, plan=plan)
+    y = nat.sparse_conv(xd, wd, bd, idx, ntaps=ntaps, n_out=n_out, plan=plan)
+    torch.cuda.synchronize()
+    rows = _sample_rows(n_out, 2000, seed=94)
+    ref = _oracle_bf16(orc, x, w, b, idx.cpu().numpy(), rows, ntaps, n_in)
+    assert max_rel(from_dev(yp)[rows], ref) <= MAXREL
+    assert torch.equal(y, yp)
+
+
 def test_bf16_config2_ellipsoids(spc, orc, dev):
     """4 ellipsoid shells, C=128, bf16, fp32 accumulate."""
     import torch
