@@ -45,7 +45,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5, 6, 7],
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5, 6, 7, 8],
                     help="2 = the headline workload; others print diagnostic lines")
     ap.add_argument("--order", choices=["natural", "mask"], default="natural",
                     help="row processing order of the conv kernel")
@@ -269,6 +269,18 @@ def main():
         workload = ("mesh-decoder upsample block (GroupNorm32, SiLU, subdivide, subm3x3x3 "
                     "768->192, GroupNorm32, SiLU, subm3x3x3, + 1x1x1 skip), bf16, sphere shell "
                     "64^3 -> 128^3")
+    elif cfg == 8:
+        # the first block's output support: every sphere-shell voxel's 8 children
+        par = wl.sphere_shell()
+        kids = np.array([[0, dx, dy, dz] for dx in (0, 1) for dy in (0, 1) for dz in (0, 1)],
+                        np.int32)
+        coords = (par[:, None, :] * np.array([1, 2, 2, 2], np.int32) + kids[None]).reshape(-1, 4)
+        coords = np.ascontiguousarray(coords, dtype=np.int32)
+        cin, cout = 192, 96
+        batch = 1
+        workload = ("mesh-decoder second upsample block (GroupNorm32, SiLU, subdivide, subm3x3x3 "
+                    "192->96, GroupNorm32, SiLU, subm3x3x3, + 1x1x1 skip), bf16, subdivided "
+                    "sphere shell 128^3 -> 256^3")
     else:
         coords = wl.sphere_shell()
         cin = cout = 64
@@ -394,8 +406,9 @@ def main():
                   "pct_peak_subm": 100 * f2 / (ms2 / 1e3) / 1e12 / PEAK_BF16_TFLOPS}
     elif cfg == 6:
         result = bench_res_block(spc, nat, wl, orc, coords, c_dev, dev, args, workload)
-    elif cfg == 7:
-        result = bench_subdivide_block(spc, nat, wl, orc, coords, c_dev, dev, args, workload)
+    elif cfg in (7, 8):
+        result = bench_subdivide_block(spc, nat, wl, orc, coords, c_dev, dev, args, workload,
+                                       cin, cout, res=64 if cfg == 7 else 128)
     else:
         keeps = wl.prune_masks(n)
         lv = []
@@ -466,24 +479,24 @@ def bench_res_block(spc, nat, wl, orc, coords, c_dev, dev, args, workload):
             "config": {"workload": workload, "n_voxels": n, "channels": 128, "batch": 4}}
 
 
-def bench_subdivide_block(spc, nat, wl, orc, coords, c_dev, dev, args, workload):
-    """SparseSubdivideBlock3d forward (768 -> 192, the first mesh-decoder
-    upsample block) on the fused path against the same block with separate
-    GroupNorm, SiLU, gather and residual passes.  Both include the child
-    map build, as the block builds it on every call."""
+def bench_subdivide_block(spc, nat, wl, orc, coords, c_dev, dev, args, workload, cin, cout, res):
+    """SparseSubdivideBlock3d forward (768 -> 192 or 192 -> 96, the mesh
+    decoder's upsample blocks) on the fused path against the same block with
+    separate GroupNorm, SiLU, gather and residual passes.  Both include the
+    child map build, as the block builds it on every call."""
     import torch
 
     sp = spc.sparse
     n = coords.shape[0]
     torch.manual_seed(0)
-    blk = spc.blocks.SparseSubdivideBlock3d(768, 64, 192).to(dev)
+    blk = spc.blocks.SparseSubdivideBlock3d(cin, res, cout).to(dev)
     with torch.no_grad():
         for p in blk.out_layers[3].parameters():
             p.normal_(0, 0.02)
     blk = blk.to(torch.bfloat16)
     blk.act_layers[0].float()
     blk.out_layers[1].float()
-    x, _ = bf16_dev(orc, wl.normal((n, 768), 1.0, seed=701), dev)
+    x, _ = bf16_dev(orc, wl.normal((n, cin), 1.0, seed=701), dev)
     xt = sp.SparseTensor(x, c_dev)
     gn0, gn1 = blk.act_layers[0], blk.out_layers[1]
 
@@ -512,11 +525,12 @@ def bench_subdivide_block(spc, nat, wl, orc, coords, c_dev, dev, args, workload)
     if not args.fused_only:
         ms_u, _ = time_gpu(unfused, args.steps, args.warmup)
         diff = float((yf.feats.float() - unfused().feats.float()).abs().max())
-    return {"metric": f"config 7: {workload}", "value": nc / (ms_f / 1e3) / 1e6, "unit": "Mvoxel/s",
+    return {"metric": f"config {args.config}: {workload}", "value": nc / (ms_f / 1e3) / 1e6,
+            "unit": "Mvoxel/s",
             "ms_per_step": ms_f, "unfused_ms": ms_u, "speedup": ms_u / ms_f if ms_u else None,
             "dtype": "bf16", "max_abs_diff_fused_vs_unfused": diff,
-            "config": {"workload": workload, "n_parents": n, "n_children": nc, "cin": 768,
-                       "cout": 192}}
+            "config": {"workload": workload, "n_parents": n, "n_children": nc, "cin": cin,
+                       "cout": cout}}
 
 
 if __name__ == "__main__":

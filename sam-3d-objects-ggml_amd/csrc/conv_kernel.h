@@ -1120,6 +1120,11 @@ hipError_t dispatch_tn(hipStream_t s, const ConvArgs& a) {
         if (a.cout % 192 == 0 && a.cout % 128 != 0 && a.epi_mode != SPC_EPI_NORM_MOD_SILU &&
             tiles_m * (a.cout / 192) >= a.num_cu)
             return launch_conv<T, Q8, PACKED, NTAPS, 192, 2, 2>(s, a);
+        // 96 (the mesh decoder's 768 / 8): four waves of 64x96 instead of
+        // three 32-column tiles of 32x32 wave tiles
+        if (a.cout % 96 == 0 && a.cout % 64 != 0 && a.epi_mode != SPC_EPI_NORM_MOD_SILU &&
+            tiles_m * (a.cout / 96) >= a.num_cu)
+            return launch_conv<T, Q8, PACKED, NTAPS, 96, 4, 1>(s, a);
     }
     if (tn == 128) {
         if constexpr (Q8) return launch_conv<T, Q8, PACKED, NTAPS, 128, 2, 2>(s, a);

@@ -66,11 +66,12 @@ def test_bf16_channels(spc, orc, dev, cin, cout):
     assert torch.equal(y, yp)
 
 
-@pytest.mark.parametrize("ntaps", [27, 8])
-def test_bf16_cout192_wide_tiles(spc, orc, dev, ntaps):
-    """C_out = 192 with at least 256 row tiles runs the 192-column tile (four
-    waves of 128x96): sampled rows against the oracle, and bit-identical to
-    the unpacked-weight launch, which runs three 64-column tiles."""
+@pytest.mark.parametrize("ntaps,cout", [(27, 192), (8, 192), (27, 96)])
+def test_bf16_wide_tiles(spc, orc, dev, ntaps, cout):
+    """C_out = 192 / 96 with at least 256 row tiles runs the 192-column tile
+    (four waves of 128x96) / the 96-column tile (four waves of 64x96):
+    sampled rows against the oracle, and bit-identical to the unpacked-weight
+    launch, which runs 64- / 32-column tiles."""
     import torch
 
     nat = spc._native
@@ -84,8 +85,8 @@ def test_bf16_cout192_wide_tiles(spc, orc, dev, ntaps):
         d = nat.downsample_map(torch.from_numpy(coords).to(dev), 1, 128, with_taps=True)
         idx, n_out, n_in = d.stride2_taps, d.nc, coords.shape[0]
     assert n_out >= 256 * 256
-    _case(f"bf16 {ntaps}-tap conv N_out={n_out} 64->192 (192-column tiles)")
-    x, w, b = _bf16_inputs(spc, orc, n_in, 64, 192, ntaps=ntaps, seed=93)
+    _case(f"bf16 {ntaps}-tap conv N_out={n_out} 64->{cout} ({cout}-column tiles)")
+    x, w, b = _bf16_inputs(spc, orc, n_in, 64, cout, ntaps=ntaps, seed=93)
     wd = to_dev_bf16(w, dev)
     xd, bd = to_dev_bf16(x, dev), to_dev_bf16(b, dev)
     plan = nat.conv_plan(idx, ntaps=ntaps, n_out=n_out, n_in=n_in)
