@@ -159,6 +159,11 @@ constexpr int kTM = 256;        // output rows per tile
 constexpr int kUMax = 895;      // capacity of the deduplicated source-row stage
 constexpr int kURowCap = (kUMax + 3) / 4 * 4;  // union-row table entries (16-byte multiple)
 constexpr int kWinWords = 1024; // dedupe bitmap: 32768 source rows
+constexpr int kHashBits = 13;    // wider spans: LDS hash of the tile's source rows
+constexpr int kHashSlots = 1 << kHashBits;
+constexpr int kSortCap = 1024;   // distinct rows sorted after hashing (>= kUMax + 1)
+constexpr int kSetupScratchWords =
+    2 * kWinWords > kHashSlots + kSortCap ? 2 * kWinWords : kHashSlots + kSortCap;
 constexpr int kSegs = 4;        // 16-byte segments per staged 64-byte row chunk
 constexpr int kPitch = 5;       // staged row pitch in 16-byte units (64 bytes + 16 of padding)
 // 16-byte units per A stage buffer: whole 64-unit blocks (one LDS-DMA
@@ -195,7 +200,8 @@ struct TileLds {
     int32_t* urow;      // kUMax source rows of the union slots
     int32_t* srow;      // kTM output rows of the tile rows
     int32_t* wsum;      // one per wave
-    int32_t* misc;      // [0] tap mask [1] min source row [2] fail [3] U [4] fast
+    int32_t* misc;      // [0] tap mask [1] min source row [2] wide span [3] U [4] fast
+                        // [5] distinct rows (hash path)
 };
 
 // Tile setup: the tile's NTAPS x 256 neighbour indices are loaded
@@ -293,64 +299,142 @@ __device__ __forceinline__ void tile_setup(const ConvArgs& a, int64_t r0, const 
     }
     if (fail) L.misc[2] = 1;
     lds_barrier();
-    // ranks: thread tid owns words WPT*tid .. WPT*tid + WPT - 1
-    uint32_t wv[WPT];
-    int cnt = 0;
-#pragma unroll
-    for (int w = 0; w < WPT; ++w) {
-        wv[w] = bm[WPT * tid + w];
-        cnt += __popc(wv[w]);
-    }
-    int incl = cnt;
-    for (int off = 1; off < 64; off <<= 1) {
-        const int v = __shfl_up(incl, off);
-        if (lane >= off) incl += v;
-    }
-    if (lane == 63) L.wsum[wave] = incl;
-    lds_barrier();
-    int base = incl - cnt;
-    int U = 0;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-        if (w < wave) base += L.wsum[w];
-        U += L.wsum[w];
-    }
-    const bool fast = !L.misc[2] && U <= kUMax;
-    {
-        int b = base;
-#pragma unroll
-        for (int w = 0; w < WPT; ++w) {
-            wbase[WPT * tid + w] = b;
-            if (fast) {
-                uint32_t m = wv[w];
-                while (m) {
-                    const int bit = __ffs(m) - 1;
-                    m &= m - 1;
-                    L.urow[b++] = lo + (WPT * tid + w) * 32 + bit;
-                }
-            } else {
-                b += __popc(wv[w]);
-            }
-        }
-    }
-    lds_barrier();
-    if (fast) {
+    int U;
+    bool fast;
+    if (L.misc[2]) {
+        // ---- the sources span more than the window (large tensors whose
+        // neighbour slabs lie far apart in row order): insert them into an
+        // LDS hash table (linear probing; more slots than entries, so every
+        // probe ends), collect the distinct rows, sort them (bitonic), and
+        // rank every entry by binary search -- the same ascending union as
+        // the bitmap gives.
+        static_assert(kHashSlots > NQ && kSortCap > kUMax && (kSortCap & (kSortCap - 1)) == 0,
+                      "hash geometry");
+        int32_t* ht = reinterpret_cast<int32_t*>(L.scratch);
+        int32_t* ul = ht + kHashSlots;
+        for (int i = tid; i < kHashSlots; i += NT) ht[i] = -1;
+        if (tid == 0) L.misc[5] = 0;
+        lds_barrier();
 #pragma unroll
         for (int k = 0; k < EPT; ++k) {
-            const int e = tid + k * NT;
-            if (e < NQ) {
-                const int r = e / NTAPS;
-                const int o = e - r * NTAPS;
-                int32_t out = U;  // the zero row
-                if (ent[k] >= 0) {
-                    const int32_t off = ent[k] - lo;
-                    const int wi = off >> 5;
-                    out = wbase[wi] + __popc(bm[wi] & ((1u << (off & 31)) - 1u));
+            const int32_t key = ent[k];
+            if (key >= 0) {
+                uint32_t h = ((uint32_t)key * 2654435761u) >> (32 - kHashBits);
+                for (;;) {
+                    const int32_t prev = atomicCAS(&ht[h], -1, key);
+                    if (prev == -1) {
+                        const int i = atomicAdd(&L.misc[5], 1);
+                        if (i < kSortCap) ul[i] = key;
+                        break;
+                    }
+                    if (prev == key) break;
+                    h = (h + 1) & (kHashSlots - 1);
                 }
-                L.sidx[o * TM + r] = (uint16_t)slot_key(out);
             }
         }
-        for (int r = tid; r < TM; r += NT) L.sidx[NTAPS * TM + r] = (uint16_t)slot_key(U);
+        lds_barrier();
+        U = L.misc[5];
+        fast = U <= kUMax;
+        if (fast) {
+            for (int i = U + tid; i < kSortCap; i += NT) ul[i] = INT_MAX;
+            lds_barrier();
+            for (int kk = 2; kk <= kSortCap; kk <<= 1) {
+                for (int j = kk >> 1; j > 0; j >>= 1) {
+                    for (int i = tid; i < kSortCap; i += NT) {
+                        const int ixj = i ^ j;
+                        if (ixj > i) {
+                            const int32_t va = ul[i], vb = ul[ixj];
+                            if ((va > vb) == ((i & kk) == 0)) {
+                                ul[i] = vb;
+                                ul[ixj] = va;
+                            }
+                        }
+                    }
+                    lds_barrier();
+                }
+            }
+            for (int i = tid; i < U; i += NT) L.urow[i] = ul[i];
+#pragma unroll
+            for (int k = 0; k < EPT; ++k) {
+                const int e = tid + k * NT;
+                if (e < NQ) {
+                    const int r = e / NTAPS;
+                    const int o = e - r * NTAPS;
+                    int32_t out = U;  // the zero row
+                    if (ent[k] >= 0) {
+                        int a0 = 0, a1 = U;  // first position holding >= the key
+                        while (a0 < a1) {
+                            const int mid = (a0 + a1) >> 1;
+                            if (ul[mid] < ent[k]) a0 = mid + 1;
+                            else a1 = mid;
+                        }
+                        out = a0;
+                    }
+                    L.sidx[o * TM + r] = (uint16_t)slot_key(out);
+                }
+            }
+            for (int r = tid; r < TM; r += NT) L.sidx[NTAPS * TM + r] = (uint16_t)slot_key(U);
+        }
+    } else {
+        // ranks: thread tid owns words WPT*tid .. WPT*tid + WPT - 1
+        uint32_t wv[WPT];
+        int cnt = 0;
+#pragma unroll
+        for (int w = 0; w < WPT; ++w) {
+            wv[w] = bm[WPT * tid + w];
+            cnt += __popc(wv[w]);
+        }
+        int incl = cnt;
+        for (int off = 1; off < 64; off <<= 1) {
+            const int v = __shfl_up(incl, off);
+            if (lane >= off) incl += v;
+        }
+        if (lane == 63) L.wsum[wave] = incl;
+        lds_barrier();
+        int base = incl - cnt;
+        U = 0;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            if (w < wave) base += L.wsum[w];
+            U += L.wsum[w];
+        }
+        fast = U <= kUMax;
+        {
+            int b = base;
+#pragma unroll
+            for (int w = 0; w < WPT; ++w) {
+                wbase[WPT * tid + w] = b;
+                if (fast) {
+                    uint32_t m = wv[w];
+                    while (m) {
+                        const int bit = __ffs(m) - 1;
+                        m &= m - 1;
+                        L.urow[b++] = lo + (WPT * tid + w) * 32 + bit;
+                    }
+                } else {
+                    b += __popc(wv[w]);
+                }
+            }
+        }
+        lds_barrier();
+        if (fast) {
+#pragma unroll
+            for (int k = 0; k < EPT; ++k) {
+                const int e = tid + k * NT;
+                if (e < NQ) {
+                    const int r = e / NTAPS;
+                    const int o = e - r * NTAPS;
+                    int32_t out = U;  // the zero row
+                    if (ent[k] >= 0) {
+                        const int32_t off = ent[k] - lo;
+                        const int wi = off >> 5;
+                        out = wbase[wi] + __popc(bm[wi] & ((1u << (off & 31)) - 1u));
+                    }
+                    L.sidx[o * TM + r] = (uint16_t)slot_key(out);
+                }
+            }
+            for (int r = tid; r < TM; r += NT) L.sidx[NTAPS * TM + r] = (uint16_t)slot_key(U);
+        }
     }
     if (tid == 0) {
         // the active taps in ascending order, four per word; padding 0xff
@@ -377,7 +461,7 @@ __device__ __forceinline__ void tile_setup(const ConvArgs& a, int64_t r0, const 
 // every conv over the same index table skips it.
 template <int NTAPS>
 __global__ __launch_bounds__(512) void conv_plan_kernel(ConvArgs a, char* plan) {
-    __shared__ uint32_t scratch[2 * kWinWords];
+    __shared__ uint32_t scratch[kSetupScratchWords];
     __shared__ __attribute__((aligned(16))) uint16_t sidx[(NTAPS + 1) * kTM];
     __shared__ __attribute__((aligned(16))) uint32_t tlw[kTapWords];
     __shared__ __attribute__((aligned(16))) int32_t urow[kURowCap];
@@ -420,7 +504,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
     static_assert(FM >= 1 && FN >= 1, "wave geometry");
     static_assert(!Q8 || ES == 2, "Q8_0 weights feed 16-bit MFMA operands");
     static_assert(NTAPS <= 32, "tap mask is 32-bit");
-    static_assert(2 * kWinWords * 4 <= STAGE * 16, "bitmap aliases the A stage");
+    static_assert(kSetupScratchWords * 4 <= 2 * STAGE * 16, "setup scratch aliases the A stage");
     static_assert(PD == 4, "the step groups pack four taps per word");
 
     __shared__ u32x4 Au[2 * STAGE];    // two A buffers: (U + 1) rows x 64 bytes each

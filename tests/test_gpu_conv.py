@@ -255,6 +255,44 @@ def test_empty_and_missing(spc, orc, dev):
     assert torch.equal(y, bb.unsqueeze(0).expand(n, 32))
 
 
+def _two_slabs():
+    """x in {0, 1}, y in [0, 2048), z in [0, 16): a tile's x + 1 neighbours
+    lie 32768 rows away, beyond the setup's bitmap window."""
+    g = np.stack(np.meshgrid([0], [0, 1], np.arange(2048), np.arange(16), indexing="ij"), -1)
+    return np.ascontiguousarray(g.reshape(-1, 4), dtype=np.int32)
+
+
+def test_wide_span_tiles_stay_on_the_fast_path(spc, orc, dev):
+    """Tiles whose source rows span more than the 32768-row bitmap window are
+    deduplicated by the hash path: every tile keeps the staged fast path
+    (plan header), results match the oracle, and the plan and the in-kernel
+    setup agree bit-exactly."""
+    import torch
+
+    nat = spc._native
+    coords = _two_slabs()
+    n = coords.shape[0]
+    _case(f"wide-span tiles N={n} bf16 32->32")
+    m = nat.map_build(torch.from_numpy(coords).to(dev))
+    plan = nat.conv_plan(m.token_major, ntaps=27, n_out=n)
+    tiles = (n + 255) // 256
+    hdr = plan.view(torch.int32).cpu().numpy().reshape(tiles, -1)
+    assert (hdr[:, 2] == 1).all() and (hdr[:, 0] <= 895).all()
+    tm = m.token_major.cpu().numpy().reshape(n, 27)
+    span = np.where(tm < n, tm, -1).max(1).max() - np.where(tm < n, tm, n).min(1).min()
+    assert span > 32768
+    x, w, b = _bf16_inputs(spc, orc, n, 32, 32, seed=97)
+    args = (to_dev_bf16(x, dev), nat.pack_weights(to_dev_bf16(w, dev)), to_dev_bf16(b, dev),
+            m.token_major)
+    y = nat.sparse_conv(*args, ntaps=27, n_out=n, plan=plan)
+    y0 = nat.sparse_conv(*args, ntaps=27, n_out=n)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y0)
+    rows = _sample_rows(n, 2000, seed=98)
+    ref = _oracle_bf16(orc, x, w, b, m.token_major.cpu().numpy(), rows, 27, n)
+    assert max_rel(from_dev(y)[rows], ref) <= MAXREL
+
+
 @pytest.mark.parametrize("case", ["bf16_natural", "bf16_mask_order", "f32", "q8_0", "stride2",
                                   "dense1", "fallback_unsorted"])
 def test_plan_matches_in_kernel_setup(spc, orc, dev, case):
