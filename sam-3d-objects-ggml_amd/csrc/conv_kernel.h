@@ -159,11 +159,12 @@ constexpr int kTM = 256;        // output rows per tile
 constexpr int kUMax = 895;      // capacity of the deduplicated source-row stage
 constexpr int kURowCap = (kUMax + 3) / 4 * 4;  // union-row table entries (16-byte multiple)
 constexpr int kWinWords = 1024; // dedupe bitmap: 32768 source rows
-constexpr int kHashBits = 13;    // wider spans: LDS hash of the tile's source rows
-constexpr int kHashSlots = 1 << kHashBits;
-constexpr int kSortCap = 1024;   // distinct rows sorted after hashing (>= kUMax + 1)
-constexpr int kSetupScratchWords =
-    2 * kWinWords > kHashSlots + kSortCap ? 2 * kWinWords : kHashSlots + kSortCap;
+constexpr int kHashBits = 12;    // wider spans: LDS hash of the tile's source rows
+constexpr int kHashSlots = 1 << kHashBits;  // 64-bit slots: row | rank << 32
+constexpr int kSortCap = 1024;   // distinct rows collected after hashing (> kUMax)
+constexpr int kSetupScratchWords = 2 * kWinWords > 2 * kHashSlots + 2 * kSortCap
+                                       ? 2 * kWinWords
+                                       : 2 * kHashSlots + 2 * kSortCap;
 constexpr int kSegs = 4;        // 16-byte segments per staged 64-byte row chunk
 constexpr int kPitch = 5;       // staged row pitch in 16-byte units (64 bytes + 16 of padding)
 // 16-byte units per A stage buffer: whole 64-unit blocks (one LDS-DMA
@@ -304,30 +305,39 @@ __device__ __forceinline__ void tile_setup(const ConvArgs& a, int64_t r0, const 
     if (L.misc[2]) {
         // ---- the sources span more than the window (large tensors whose
         // neighbour slabs lie far apart in row order): insert them into an
-        // LDS hash table (linear probing; more slots than entries, so every
-        // probe ends), collect the distinct rows, sort them (bitonic), and
-        // rank every entry by binary search -- the same ascending union as
-        // the bitmap gives.
-        static_assert(kHashSlots > NQ && kSortCap > kUMax && (kSortCap & (kSortCap - 1)) == 0,
-                      "hash geometry");
-        int32_t* ht = reinterpret_cast<int32_t*>(L.scratch);
-        int32_t* ul = ht + kHashSlots;
-        for (int i = tid; i < kHashSlots; i += NT) ht[i] = -1;
+        // LDS hash table (64-bit slots, linear probing), collect the distinct
+        // rows, place each at its rank among them (a count of smaller rows,
+        // read by all lanes at once) and store the rank in its slot; every
+        // entry then finds its rank in its slot -- the same ascending union
+        // as the bitmap gives.  Inserting stops once kSortCap distinct rows
+        // are in (the tile is then not staged), so at most kSortCap + NT
+        // slots are ever taken and every probe ends at an empty slot.
+        static_assert(kHashSlots > kSortCap + 1024 && kSortCap > kUMax, "hash geometry");
+        unsigned long long* ht = reinterpret_cast<unsigned long long*>(L.scratch);
+        int32_t* ul = reinterpret_cast<int32_t*>(ht + kHashSlots);  // distinct rows
+        int32_t* us = ul + kSortCap;                                 // their slots
+        constexpr unsigned long long kEmpty = ~0ull;
+        for (int i = tid; i < kHashSlots; i += NT) ht[i] = kEmpty;
         if (tid == 0) L.misc[5] = 0;
         lds_barrier();
+        volatile int32_t* ndist = &L.misc[5];
+        auto hash = [](int32_t key) { return ((uint32_t)key * 2654435761u) >> (32 - kHashBits); };
 #pragma unroll
         for (int k = 0; k < EPT; ++k) {
             const int32_t key = ent[k];
             if (key >= 0) {
-                uint32_t h = ((uint32_t)key * 2654435761u) >> (32 - kHashBits);
-                for (;;) {
-                    const int32_t prev = atomicCAS(&ht[h], -1, key);
-                    if (prev == -1) {
+                uint32_t h = hash(key);
+                for (int probe = 0; probe < kHashSlots && *ndist < kSortCap; ++probe) {
+                    const unsigned long long prev = atomicCAS(&ht[h], kEmpty, (unsigned long long)(uint32_t)key);
+                    if (prev == kEmpty) {
                         const int i = atomicAdd(&L.misc[5], 1);
-                        if (i < kSortCap) ul[i] = key;
+                        if (i < kSortCap) {
+                            ul[i] = key;
+                            us[i] = (int32_t)h;
+                        }
                         break;
                     }
-                    if (prev == key) break;
+                    if ((uint32_t)prev == (uint32_t)key) break;
                     h = (h + 1) & (kHashSlots - 1);
                 }
             }
@@ -336,24 +346,14 @@ __device__ __forceinline__ void tile_setup(const ConvArgs& a, int64_t r0, const 
         U = L.misc[5];
         fast = U <= kUMax;
         if (fast) {
-            for (int i = U + tid; i < kSortCap; i += NT) ul[i] = INT_MAX;
-            lds_barrier();
-            for (int kk = 2; kk <= kSortCap; kk <<= 1) {
-                for (int j = kk >> 1; j > 0; j >>= 1) {
-                    for (int i = tid; i < kSortCap; i += NT) {
-                        const int ixj = i ^ j;
-                        if (ixj > i) {
-                            const int32_t va = ul[i], vb = ul[ixj];
-                            if ((va > vb) == ((i & kk) == 0)) {
-                                ul[i] = vb;
-                                ul[ixj] = va;
-                            }
-                        }
-                    }
-                    lds_barrier();
-                }
+            for (int i = tid; i < U; i += NT) {
+                const int32_t key = ul[i];
+                int rank = 0;
+                for (int j = 0; j < U; ++j) rank += ul[j] < key ? 1 : 0;
+                L.urow[rank] = key;  // distinct keys: the ranks are a permutation of [0, U)
+                ht[us[i]] = ((unsigned long long)rank << 32) | (uint32_t)key;
             }
-            for (int i = tid; i < U; i += NT) L.urow[i] = ul[i];
+            lds_barrier();
 #pragma unroll
             for (int k = 0; k < EPT; ++k) {
                 const int e = tid + k * NT;
@@ -362,13 +362,14 @@ __device__ __forceinline__ void tile_setup(const ConvArgs& a, int64_t r0, const 
                     const int o = e - r * NTAPS;
                     int32_t out = U;  // the zero row
                     if (ent[k] >= 0) {
-                        int a0 = 0, a1 = U;  // first position holding >= the key
-                        while (a0 < a1) {
-                            const int mid = (a0 + a1) >> 1;
-                            if (ul[mid] < ent[k]) a0 = mid + 1;
-                            else a1 = mid;
+                        // present: no insert stopped early when U <= kUMax
+                        uint32_t h = hash(ent[k]);
+                        unsigned long long v = ht[h];
+                        for (int probe = 1; probe < kHashSlots && (uint32_t)v != (uint32_t)ent[k]; ++probe) {
+                            h = (h + 1) & (kHashSlots - 1);
+                            v = ht[h];
                         }
-                        out = a0;
+                        out = (uint32_t)v == (uint32_t)ent[k] ? (int32_t)(v >> 32) : U;
                     }
                     L.sidx[o * TM + r] = (uint16_t)slot_key(out);
                 }
@@ -461,7 +462,7 @@ __device__ __forceinline__ void tile_setup(const ConvArgs& a, int64_t r0, const 
 // every conv over the same index table skips it.
 template <int NTAPS>
 __global__ __launch_bounds__(512) void conv_plan_kernel(ConvArgs a, char* plan) {
-    __shared__ uint32_t scratch[kSetupScratchWords];
+    __shared__ __attribute__((aligned(16))) uint32_t scratch[kSetupScratchWords];
     __shared__ __attribute__((aligned(16))) uint16_t sidx[(NTAPS + 1) * kTM];
     __shared__ __attribute__((aligned(16))) uint32_t tlw[kTapWords];
     __shared__ __attribute__((aligned(16))) int32_t urow[kURowCap];
