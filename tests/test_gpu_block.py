@@ -128,8 +128,9 @@ def _block_params(blk):
     return out
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
 @pytest.mark.parametrize("cin,cout", [(128, 128), (64, 128), (128, 256)])
-def test_res_block(spc, orc, dev, cin, cout):
+def test_res_block(spc, orc, dev, cin, cout, dt):
     """SparseResBlock3d on the fused kernels (the 256-channel block runs the
     unfused norm path) against the oracle's block with the reference's
     rounding points."""
@@ -137,9 +138,10 @@ def test_res_block(spc, orc, dev, cin, cout):
     import torch
 
     blocks = spc.blocks
+    td, code = {"bf16": (torch.bfloat16, oracle.BF16), "f16": (torch.float16, oracle.F16)}[dt]
     coords = spc.workloads.random_voxels(4000, 22, batches=2, seed=61 + cout)
     n = coords.shape[0]
-    _case(f"SparseResBlock3d bf16 N={n} {cin}->{cout}")
+    _case(f"SparseResBlock3d {dt} N={n} {cin}->{cout}")
     torch.manual_seed(cin + cout)
     blk = blocks.SparseResBlock3d(cin, 96, cout).to(dev)
     with torch.no_grad():
@@ -147,20 +149,20 @@ def test_res_block(spc, orc, dev, cin, cout):
             p.normal_(0, 0.02)
         blk.norm1.weight.normal_(1, 0.1)
         blk.norm1.bias.normal_(0, 0.1)
-    blk = blk.to(torch.bfloat16)
+    blk = blk.to(td)
     # keep LayerNorm affine parameters f32 like LayerNorm32 (computed in F32)
     blk.norm1.float()
     x = spc.workloads.normal((n, cin), 1.0, seed=62)
-    xt = spc.sparse.SparseTensor(_dev_feats(orc, x, "bf16", dev), torch.from_numpy(coords).to(dev))
-    emb = torch.randn(2, 96, device=dev).bfloat16()
+    xt = spc.sparse.SparseTensor(_dev_feats(orc, x, dt, dev), torch.from_numpy(coords).to(dev))
+    emb = torch.randn(2, 96, device=dev).to(td)
     with torch.no_grad():
         y = blk(xt, emb)
         emb_out = blk.emb_layers(emb).float().cpu().numpy()
     scale, shift = emb_out[:, :cout], emb_out[:, cout:]
-    xr = oracle.round_to(orc, x, oracle.BF16)
+    xr = oracle.round_to(orc, x, code)
     p = _block_params(blk)
     ref = oracle.res_block(orc, xr, orc.conv_table_slat(coords), p, scale, shift,
-                           coords[:, 0].astype(np.int64), oracle.BF16)
+                           coords[:, 0].astype(np.int64), code)
     got = from_dev(y.feats)
     assert got.shape == ref.shape
     assert max_rel(got, ref) <= MAXREL
@@ -235,17 +237,19 @@ def test_conv_residual_rows_epilogue(spc, orc, dev):
     assert torch.equal(yf, y + add)
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
 @pytest.mark.parametrize("cin,cout", [(64, 32), (32, 32)])
-def test_subdivide_block(spc, orc, dev, cin, cout):
+def test_subdivide_block(spc, orc, dev, cin, cout, dt):
     """SparseSubdivideBlock3d (GroupNorm/SiLU/gather pass, conv, GroupNorm/
     SiLU, conv with the residual epilogue) against the oracle's block."""
     import oracle
     import torch
 
     blocks = spc.blocks
+    td, code = {"bf16": (torch.bfloat16, oracle.BF16), "f16": (torch.float16, oracle.F16)}[dt]
     coords = spc.workloads.random_voxels(1500, 16, batches=2, seed=71 + cin)
     n = coords.shape[0]
-    _case(f"SparseSubdivideBlock3d bf16 N={n} {cin}->{cout}")
+    _case(f"SparseSubdivideBlock3d {dt} N={n} {cin}->{cout}")
     torch.manual_seed(cin)
     blk = blocks.SparseSubdivideBlock3d(cin, 16, cout).to(dev)
     with torch.no_grad():
@@ -254,11 +258,11 @@ def test_subdivide_block(spc, orc, dev, cin, cout):
         for gn in (blk.act_layers[0], blk.out_layers[1]):
             gn.weight.normal_(1, 0.1)
             gn.bias.normal_(0, 0.1)
-    blk = blk.to(torch.bfloat16)
+    blk = blk.to(td)
     blk.act_layers[0].float()
     blk.out_layers[1].float()
     x = spc.workloads.normal((n, cin), 1.0, seed=72)
-    xt = spc.sparse.SparseTensor(_dev_feats(orc, x, "bf16", dev), torch.from_numpy(coords).to(dev))
+    xt = spc.sparse.SparseTensor(_dev_feats(orc, x, dt, dev), torch.from_numpy(coords).to(dev))
     with torch.no_grad():
         y = blk(xt)
     f = lambda t: t.detach().float().cpu().numpy()  # noqa: E731
@@ -271,8 +275,7 @@ def test_subdivide_block(spc, orc, dev, cin, cout):
     if cin != cout:
         p["skip_w"] = f(blk.skip_connection.conv.weight)
         p["skip_b"] = f(blk.skip_connection.conv.bias)
-    child, ref = oracle.subdivide_block(orc, oracle.round_to(orc, x, oracle.BF16), coords, p, 32,
-                                        oracle.BF16)
+    child, ref = oracle.subdivide_block(orc, oracle.round_to(orc, x, code), coords, p, 32, code)
     assert np.array_equal(y.coords.cpu().numpy(), child)
     assert max_rel(from_dev(y.feats), ref) <= MAXREL
     # merged taps: the same block with the 27-tap conv1 agrees to the
