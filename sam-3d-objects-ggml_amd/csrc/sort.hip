@@ -97,7 +97,8 @@ __global__ __launch_bounds__(kRsThreads) void rs_downsweep(
         for (int j = 0; j < kRsBinsPerThread; ++j) {
             const int32_t* c = offsets + (int64_t)(kRsBinsPerThread * tid + j) * nblocks;
             int32_t t = 0, bsum = 0;
-            for (int b = 0; b < nblocks; ++b) {
+#pragma unroll 8
+            for (int b = 0; b < nblocks; ++b) {  // eight loads in flight
                 const int32_t v = c[b];
                 t += v;
                 if (b < (int)blockIdx.x) bsum += v;
