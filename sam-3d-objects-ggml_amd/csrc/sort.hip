@@ -8,7 +8,8 @@
 // std::stable_sort orders it.
 //
 // Per pass (9-bit digit, 512 bins; 27-bit masks take 3 passes):
-//   upsweep   : per-tile digit histogram (tile = 256 threads x 8 keys)
+//   upsweep   : per-tile digit histogram (tile = 256 threads x 1-8 keys:
+//               small sorts take fewer keys per thread, up to 64 tiles)
 //   offsets   : up to 128 tiles, every downsweep block derives its own
 //               offsets from the digit-major [512 x tiles] counts; beyond
 //               that one workgroup scans them first
@@ -27,13 +28,13 @@ namespace {
 thread_local char g_last_error[512] = "";
 
 constexpr int kRsThreads = 256;
-constexpr int kRsItems = 8;
-constexpr int kRsTile = kRsThreads * kRsItems;
+constexpr int kRsItems = 8;                 // keys per thread of large sorts
 constexpr int kRsBits = 9;                 // digit bits: 27-bit masks sort in 3 passes
 constexpr int kRsBins = 1 << kRsBits;
 constexpr int kRsWaves = kRsThreads / 64;
 constexpr int kRsBinsPerThread = kRsBins / kRsThreads;
 constexpr int kRsFusedBlocks = 128;        // up to here each downsweep block scans the counts
+constexpr int kRsSpreadBlocks = 64;        // small sorts: fewer keys per thread up to this many tiles
 
 // Inclusive prefix sum across the 64 lanes of a wave.
 __device__ inline int32_t wave_incl_scan(int32_t v, int lane) {
@@ -46,7 +47,8 @@ __device__ inline int32_t wave_incl_scan(int32_t v, int lane) {
 }
 
 // Per-tile digit histogram, digit-major: counts[d * nblocks + block].
-template <typename K>
+// A tile is kRsThreads x ITEMS keys.
+template <typename K, int ITEMS>
 __global__ __launch_bounds__(kRsThreads) void rs_upsweep(const K* __restrict__ keys, int64_t n,
                                                          int shift, int32_t* __restrict__ counts,
                                                          int nblocks) {
@@ -54,9 +56,9 @@ __global__ __launch_bounds__(kRsThreads) void rs_upsweep(const K* __restrict__ k
 #pragma unroll
     for (int j = 0; j < kRsBinsPerThread; ++j) hist[j * kRsThreads + threadIdx.x] = 0;
     __syncthreads();
-    const int64_t base = (int64_t)blockIdx.x * kRsTile;
+    const int64_t base = (int64_t)blockIdx.x * (kRsThreads * ITEMS);
 #pragma unroll
-    for (int r = 0; r < kRsItems; ++r) {
+    for (int r = 0; r < ITEMS; ++r) {
         const int64_t i = base + r * kRsThreads + threadIdx.x;
         if (i < n) {
             const uint32_t d = (uint32_t)(keys[i] >> shift) & (kRsBins - 1);
@@ -78,7 +80,7 @@ __global__ __launch_bounds__(kRsThreads) void rs_upsweep(const K* __restrict__ k
 // blocks).  Within the tile every key is ranked among equal digits by
 // 64-lane ballots (peer mask -> popcount of lower lanes), wave counts
 // combined in LDS, rounds in input order.
-template <typename K, bool FUSED>
+template <typename K, bool FUSED, int ITEMS>
 __global__ __launch_bounds__(kRsThreads) void rs_downsweep(
     const K* __restrict__ keys_in, const int32_t* __restrict__ vals_in, K* __restrict__ keys_out,
     int32_t* __restrict__ vals_out, int64_t n, int shift, const int32_t* __restrict__ offsets,
@@ -126,9 +128,9 @@ __global__ __launch_bounds__(kRsThreads) void rs_downsweep(
             run[d] = offsets[(int64_t)d * nblocks + blockIdx.x];
         }
     }
-    const int64_t base = (int64_t)blockIdx.x * kRsTile;
+    const int64_t base = (int64_t)blockIdx.x * (kRsThreads * ITEMS);
     const unsigned long long lower = (1ull << lane) - 1ull;
-    for (int r = 0; r < kRsItems; ++r) {
+    for (int r = 0; r < ITEMS; ++r) {
 #pragma unroll
         for (int w = 0; w < kRsWaves; ++w)
 #pragma unroll
@@ -283,11 +285,18 @@ __global__ void iota_kernel(int32_t* p, int64_t n) {
 
 inline unsigned grid_for(int64_t n, int threads) { return (unsigned)((n + threads - 1) / threads); }
 
-template <typename K>
-hipError_t radix_sort(hipStream_t s, const K* keys_in, const int32_t* vals_in, K* keys_out,
-                      int32_t* vals_out, int64_t n, int end_bit, void* ws, size_t ws_bytes) {
-    if (n <= 0) return hipSuccess;
-    const int nblocks = (int)ceil_div(n, kRsTile);
+// Keys per thread: the fewest that keep at most kRsSpreadBlocks tiles (small
+// sorts spread over more compute units); large sorts take kRsItems.
+inline int rs_items(int64_t n) {
+    for (int it = 1; it < kRsItems; it *= 2)
+        if (ceil_div(n, (int64_t)kRsThreads * it) <= kRsSpreadBlocks) return it;
+    return kRsItems;
+}
+
+template <typename K, int ITEMS>
+hipError_t radix_sort_items(hipStream_t s, const K* keys_in, const int32_t* vals_in, K* keys_out,
+                            int32_t* vals_out, int64_t n, int end_bit, void* ws, size_t ws_bytes) {
+    const int nblocks = (int)ceil_div(n, (int64_t)kRsThreads * ITEMS);
     Carver c(ws, ws_bytes);
     int32_t* counts = c.take<int32_t>((size_t)kRsBins * nblocks);
     K* tk[2] = {c.take<K>(n), c.take<K>(n)};
@@ -303,19 +312,31 @@ hipError_t radix_sort(hipStream_t s, const K* keys_in, const int32_t* vals_in, K
         K* kout = last ? keys_out : tk[p & 1];
         int32_t* vout = last ? vals_out : tv[p & 1];
         const int shift = p * kRsBits;
-        rs_upsweep<K><<<nblocks, kRsThreads, 0, s>>>(kin, n, shift, counts, nblocks);
+        rs_upsweep<K, ITEMS><<<nblocks, kRsThreads, 0, s>>>(kin, n, shift, counts, nblocks);
         if (fused) {
-            rs_downsweep<K, true><<<nblocks, kRsThreads, 0, s>>>(kin, vin, kout, vout, n, shift,
-                                                                 counts, nblocks);
+            rs_downsweep<K, true, ITEMS><<<nblocks, kRsThreads, 0, s>>>(kin, vin, kout, vout, n,
+                                                                        shift, counts, nblocks);
         } else {
             scan_one_block<<<1, 1024, 0, s>>>(counts, counts, nullptr, (int64_t)kRsBins * nblocks);
-            rs_downsweep<K, false><<<nblocks, kRsThreads, 0, s>>>(kin, vin, kout, vout, n, shift,
-                                                                  counts, nblocks);
+            rs_downsweep<K, false, ITEMS><<<nblocks, kRsThreads, 0, s>>>(kin, vin, kout, vout, n,
+                                                                         shift, counts, nblocks);
         }
         kin = kout;
         vin = vout;
     }
     return hipGetLastError();
+}
+
+template <typename K>
+hipError_t radix_sort(hipStream_t s, const K* keys_in, const int32_t* vals_in, K* keys_out,
+                      int32_t* vals_out, int64_t n, int end_bit, void* ws, size_t ws_bytes) {
+    if (n <= 0) return hipSuccess;
+    switch (rs_items(n)) {
+        case 1: return radix_sort_items<K, 1>(s, keys_in, vals_in, keys_out, vals_out, n, end_bit, ws, ws_bytes);
+        case 2: return radix_sort_items<K, 2>(s, keys_in, vals_in, keys_out, vals_out, n, end_bit, ws, ws_bytes);
+        case 4: return radix_sort_items<K, 4>(s, keys_in, vals_in, keys_out, vals_out, n, end_bit, ws, ws_bytes);
+        default: return radix_sort_items<K, kRsItems>(s, keys_in, vals_in, keys_out, vals_out, n, end_bit, ws, ws_bytes);
+    }
 }
 
 }  // namespace
@@ -351,7 +372,8 @@ hipError_t iota_i32(hipStream_t s, int32_t* p, int64_t n) {
 }
 
 size_t radix_sort_ws_bytes(int64_t n, int key_bytes) {
-    const int64_t nblocks = ceil_div(n > 0 ? n : 1, kRsTile);
+    const int64_t m = n > 0 ? n : 1;
+    const int64_t nblocks = ceil_div(m, (int64_t)kRsThreads * rs_items(m));
     Sizer z;
     z.take<int32_t>((size_t)kRsBins * nblocks);
     for (int i = 0; i < 2; ++i) z.take<char>((size_t)n * key_bytes);
