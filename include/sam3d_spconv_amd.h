@@ -256,9 +256,11 @@ int spc_conv_pack_weights(spc_stream_t stream, int w_dtype, int w_layout, const 
  * input [tokens, channels], weight [output_channels, 27, channels], bias
  * [output_channels], output [tokens, output_channels]; indices offset-major
  * [27, tokens] (-1 = missing), mask / mask_argsort the sorted masks and
- * permutation of spc_map_build.  Accumulates in F32 (the reference kernel
- * accumulates in f16).  Returns nothing, like the reference; failures are
- * reported through spc_last_error(). */
+ * permutation of spc_map_build, accepted and not needed: rows run in
+ * natural order, which keeps each tile's gathered rows spatially coherent
+ * (the output is the same in any order).  Accumulates in F32 (the
+ * reference kernel accumulates in f16).  Returns nothing, like the
+ * reference; failures are reported through spc_last_error(). */
 void sam3d_spconv_f16_forward(spc_stream_t stream, const void* input, const void* weight,
                               const void* bias, void* output, const int32_t* indices,
                               const uint32_t* mask, const int32_t* mask_argsort, int64_t tokens,

@@ -473,9 +473,13 @@ void sam3d_spconv_f16_forward(spc_stream_t stream, const void* input, const void
                               const void* bias, void* output, const int32_t* indices,
                               const uint32_t* mask, const int32_t* mask_argsort, int64_t tokens,
                               int64_t channels, int64_t output_channels) {
-    (void)mask;  // each tile's tap set is formed from the indices themselves
+    // each tile's tap set is formed from the indices themselves, and rows run
+    // in natural order (spatially coherent tiles share their gathered rows);
+    // every output row is computed the same way in any order
+    (void)mask;
+    (void)mask_argsort;
     spc_sparse_conv(stream, SPC_F16, input, SPC_F16, SPC_W_KRSC, weight, nullptr, bias, output,
-                    indices, SPC_IDX_OFFSET_MAJOR, mask_argsort, 27, tokens, tokens, channels,
+                    indices, SPC_IDX_OFFSET_MAJOR, nullptr, 27, tokens, tokens, channels,
                     output_channels);
 }
 
