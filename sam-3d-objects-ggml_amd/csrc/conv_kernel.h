@@ -346,10 +346,20 @@ __device__ __forceinline__ void tile_setup(const ConvArgs& a, int64_t r0, const 
         U = L.misc[5];
         fast = U <= kUMax;
         if (fast) {
+            // pad to a multiple of four with keys above every row, then
+            // count in 16-byte broadcast reads
+            if (tid < 4 && U + tid < kSortCap) ul[U + tid] = INT_MAX;
+            lds_barrier();
+            const int u4 = (U + 3) / 4;
+            const int4* ul4 = reinterpret_cast<const int4*>(ul);
             for (int i = tid; i < U; i += NT) {
                 const int32_t key = ul[i];
                 int rank = 0;
-                for (int j = 0; j < U; ++j) rank += ul[j] < key ? 1 : 0;
+#pragma unroll 4
+                for (int j = 0; j < u4; ++j) {
+                    const int4 v = ul4[j];
+                    rank += (v.x < key) + (v.y < key) + (v.z < key) + (v.w < key);
+                }
                 L.urow[rank] = key;  // distinct keys: the ranks are a permutation of [0, U)
                 ht[us[i]] = ((unsigned long long)rank << 32) | (uint32_t)key;
             }
