@@ -309,11 +309,17 @@ __global__ __launch_bounds__(64) void gn_finalize_kernel(const double* __restric
     }
 }
 
-// y[i] = dt(silu(dt((x[src] - mean) * rstd * gamma + beta))), src = rows[i]
-// (or i); the batch item of src by a binary search over the row offsets.
-// Each lane handles a run of 4 * NV channels (16 bytes for 2-byte types
-// with NV = 2).
-template <int DT, int NV>
+// y[i] = dt(silu(dt(x[src] * a + b))) with the per-channel coefficients
+// a = rstd * gamma, b = beta - a * mean of src's batch item (the fused form
+// torch's group_norm evaluates), src = rows[i] (or i); the batch item of src
+// by a binary search over the row offsets.  Each lane handles a run of
+// 4 * NV channels (16 bytes for 2-byte types with NV = 2).  With TAB the
+// block first tabulates a and b for every (item, channel) in LDS
+// (n_batch * c <= kGnCoefMax), so a run reads them as two 16-byte words per
+// four channels.
+constexpr int kGnCoefMax = 4096;
+
+template <int DT, int NV, bool TAB>
 __global__ __launch_bounds__(256) void gn_apply_kernel(const void* __restrict__ x, int64_t n_src, int c,
                                                        int groups, const int64_t* __restrict__ off,
                                                        int n_batch, const float* __restrict__ stats,
@@ -323,8 +329,20 @@ __global__ __launch_bounds__(256) void gn_apply_kernel(const void* __restrict__ 
                                                        int64_t n_out, void* __restrict__ y) {
     using E = Elem<DT>;
     constexpr int W = 4 * NV;
+    __shared__ __attribute__((aligned(16))) float2 coef[TAB ? kGnCoefMax : 1];
     const int nrun = c / W;
     const int cpg = c / groups;
+    auto coef_of = [&](int b, int ch) __attribute__((always_inline)) {
+        const int g = ch / cpg;
+        const float mean = stats[2 * ((int64_t)b * groups + g)];
+        const float rstd = stats[2 * ((int64_t)b * groups + g) + 1];
+        const float av = rstd * (gamma ? gamma[ch] : 1.0f);
+        return float2{av, (beta ? beta[ch] : 0.0f) - av * mean};
+    };
+    if constexpr (TAB) {
+        for (int k = threadIdx.x; k < n_batch * c; k += blockDim.x) coef[k] = coef_of(k / c, k % c);
+        __syncthreads();
+    }
     const int64_t total = n_out * nrun;
     for (int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; id < total;
          id += (int64_t)gridDim.x * blockDim.x) {
@@ -344,25 +362,14 @@ __global__ __launch_bounds__(256) void gn_apply_kernel(const void* __restrict__ 
             float t[W];
 #pragma unroll
             for (int h = 0; h < NV; ++h) E::ld4(x, src * c + c0 + 4 * h, t + 4 * h);
-            const float* st = stats + 2 * (int64_t)lo * groups;
-            int g = c0 / cpg, rem = c0 - g * cpg;
 #pragma unroll
-            for (int h = 0; h < NV; ++h) {
-                const floatx4 g4 = gamma ? *reinterpret_cast<const floatx4*>(gamma + c0 + 4 * h)
-                                         : floatx4{1.f, 1.f, 1.f, 1.f};
-                const floatx4 b4 = beta ? *reinterpret_cast<const floatx4*>(beta + c0 + 4 * h)
-                                        : floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float mean = st[2 * g], rstd = st[2 * g + 1];
-                    float u = (t[4 * h + e] - mean) * rstd * g4[e] + b4[e];
-                    u = E::round(u);  // GroupNorm32 casts back to the feature dtype
-                    o[4 * h + e] = silu ? silu_f32(u) : u;
-                    if (++rem == cpg) {
-                        rem = 0;
-                        ++g;
-                    }
-                }
+            for (int e = 0; e < W; ++e) {
+                float2 ab;
+                if constexpr (TAB) ab = coef[lo * c + c0 + e];
+                else ab = coef_of(lo, c0 + e);
+                float u = t[e] * ab.x + ab.y;
+                u = E::round(u);  // GroupNorm32 casts back to the feature dtype
+                o[e] = silu ? silu_f32(u) : u;
             }
         }
 #pragma unroll
@@ -387,14 +394,18 @@ hipError_t launch_gn_apply(hipStream_t s, const void* x, int64_t n_src, int c, i
                            const int64_t* off, int n_batch, const float* stats, const float* gamma,
                            const float* beta, int silu, const int32_t* rows, int64_t n_out, void* y) {
     const bool wide = DT != SPC_F32 && c % 8 == 0;
+    const bool tab = (int64_t)n_batch * c <= kGnCoefMax;
     const int64_t total = n_out * (c / (wide ? 8 : 4));
-    const unsigned grid = (unsigned)std::min<int64_t>(ceil_div(total, 256), 65536);
-    if (wide)
-        gn_apply_kernel<DT, 2><<<grid, 256, 0, s>>>(x, n_src, c, groups, off, n_batch, stats, gamma,
-                                                    beta, silu, rows, n_out, y);
-    else
-        gn_apply_kernel<DT, 1><<<grid, 256, 0, s>>>(x, n_src, c, groups, off, n_batch, stats, gamma,
-                                                    beta, silu, rows, n_out, y);
+    // tabulating blocks take more rows each, so the table is built fewer times
+    const unsigned grid = (unsigned)std::min<int64_t>(ceil_div(total, 256), tab ? 4096 : 65536);
+#define SPC_GN_APPLY(NV, TAB)                                                                  \
+    gn_apply_kernel<DT, NV, TAB><<<grid, 256, 0, s>>>(x, n_src, c, groups, off, n_batch, stats, \
+                                                      gamma, beta, silu, rows, n_out, y)
+    if (wide && tab) SPC_GN_APPLY(2, true);
+    else if (wide) SPC_GN_APPLY(2, false);
+    else if (tab) SPC_GN_APPLY(1, true);
+    else SPC_GN_APPLY(1, false);
+#undef SPC_GN_APPLY
     return hipGetLastError();
 }
 
