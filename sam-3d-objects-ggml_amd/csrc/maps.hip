@@ -343,27 +343,38 @@ __global__ void compose_rows_kernel(const int32_t* __restrict__ idx, int64_t n,
 // delta(o) is child e of parent p + j, per axis s = d + delta, j = floor(s/2),
 // e = s - 2j.  Non-owning (duplicate) parents give children with no
 // neighbours, as the hash table's first-row rule gives for their copies.
+// A block takes kSnParents parents: their table rows are read once into LDS
+// (coalesced), then the block's 8 * 27 entries per parent are written in
+// order (coalesced).  The host bounds 8 * np * 27 by INT32_MAX.
+constexpr int kSnParents = 32;
+
 __global__ __launch_bounds__(256) void subdivide_neighbors_kernel(const int32_t* __restrict__ ptm,
                                                                   int64_t np,
                                                                   int32_t* __restrict__ ctm) {
-    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int64_t nc = 8 * np;
-    if (e >= nc * 27) return;
-    const int64_t c = e / 27;
-    const int o = (int)(e - c * 27);
-    const int64_t p = c >> 3;
-    const int d = (int)(c & 7);
-    const int32_t* pr = ptm + p * 27;
-    int32_t out = (int32_t)nc;
-    if (pr[13] == (int32_t)p) {
-        const int sx = (d >> 2) + o / 9 - 1, sy = ((d >> 1) & 1) + (o / 3) % 3 - 1,
-                  sz = (d & 1) + o % 3 - 1;
-        const int jx = sx >> 1, jy = sy >> 1, jz = sz >> 1;  // floor division (arithmetic shift)
-        const int q = pr[(jx + 1) * 9 + (jy + 1) * 3 + (jz + 1)];
-        if (q >= 0 && q < np)
-            out = q * 8 + (sx - 2 * jx) * 4 + (sy - 2 * jy) * 2 + (sz - 2 * jz);
+    __shared__ int32_t pt[kSnParents * 27];
+    const uint32_t p0 = blockIdx.x * kSnParents;
+    const uint32_t npb = min((uint32_t)kSnParents, (uint32_t)np - p0);
+    for (uint32_t k = threadIdx.x; k < npb * 27u; k += blockDim.x) pt[k] = ptm[(size_t)p0 * 27 + k];
+    __syncthreads();
+    const uint32_t nc = 8u * (uint32_t)np;
+    const uint32_t base = p0 * 8u * 27u;
+    for (uint32_t k = threadIdx.x; k < npb * 8u * 27u; k += blockDim.x) {
+        const uint32_t cl = k / 27u;         // child within the block
+        const int o = (int)(k - cl * 27u);
+        const uint32_t pl = cl >> 3;         // parent within the block
+        const int d = (int)(cl & 7u);
+        const int32_t* pr = pt + pl * 27u;
+        int32_t out = (int32_t)nc;
+        if (pr[13] == (int32_t)(p0 + pl)) {
+            const int sx = (d >> 2) + o / 9 - 1, sy = ((d >> 1) & 1) + (o / 3) % 3 - 1,
+                      sz = (d & 1) + o % 3 - 1;
+            const int jx = sx >> 1, jy = sy >> 1, jz = sz >> 1;  // floor division (arithmetic shift)
+            const int q = pr[(jx + 1) * 9 + (jy + 1) * 3 + (jz + 1)];
+            if (q >= 0 && q < np)
+                out = q * 8 + (sx - 2 * jx) * 4 + (sy - 2 * jy) * 2 + (sz - 2 * jz);
+        }
+        ctm[base + k] = out;
     }
-    ctm[e] = out;
 }
 
 // Merged-tap tables of the 3x3x3 conv over a fully subdivided tensor, read
@@ -633,7 +644,7 @@ int spc_subdivide_neighbors(spc_stream_t stream, const int32_t* parent_token_maj
         set_last_error("spc_subdivide_neighbors: null table");
         return SPC_BAD_ARG;
     }
-    subdivide_neighbors_kernel<<<grid_for(n_parent * 8 * 27, 256), 256, 0, s>>>(
+    subdivide_neighbors_kernel<<<(unsigned)ceil_div(n_parent, (int64_t)kSnParents), 256, 0, s>>>(
         parent_token_major, n_parent, child_token_major);
     SPC_HIP(hipGetLastError());
     return SPC_OK;

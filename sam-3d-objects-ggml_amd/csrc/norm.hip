@@ -344,9 +344,10 @@ __global__ __launch_bounds__(256) void gn_apply_kernel(const void* __restrict__ 
         __syncthreads();
     }
     const int64_t total = n_out * nrun;
+    const bool small = total < ((int64_t)1 << 32);  // 32-bit row / run split
     for (int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; id < total;
          id += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t i = id / nrun;
+        const int64_t i = small ? (int64_t)((uint32_t)id / (uint32_t)nrun) : id / nrun;
         const int c0 = W * (int)(id - i * nrun);
         const int64_t src = rows ? rows[i] : i;
         float o[W];
