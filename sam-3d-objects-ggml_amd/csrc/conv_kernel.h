@@ -159,7 +159,7 @@ constexpr int kTM = 256;        // output rows per tile
 constexpr int kUMax = 895;      // capacity of the deduplicated source-row stage
 constexpr int kURowCap = (kUMax + 3) / 4 * 4;  // union-row table entries (16-byte multiple)
 constexpr int kWinWords = 1024; // dedupe bitmap: 32768 source rows
-constexpr int kHashBits = 12;    // wider spans: LDS hash of the tile's source rows
+constexpr int kHashBits = 11;    // wider spans: LDS hash of the tile's source rows
 constexpr int kHashSlots = 1 << kHashBits;  // 64-bit slots: row | rank << 32
 constexpr int kSortCap = 1024;   // distinct rows collected after hashing (> kUMax)
 constexpr int kSetupScratchWords = 2 * kWinWords > 2 * kHashSlots + 2 * kSortCap
@@ -312,7 +312,7 @@ __device__ __forceinline__ void tile_setup(const ConvArgs& a, int64_t r0, const 
         // as the bitmap gives.  Inserting stops once kSortCap distinct rows
         // are in (the tile is then not staged), so at most kSortCap + NT
         // slots are ever taken and every probe ends at an empty slot.
-        static_assert(kHashSlots > kSortCap + 1024 && kSortCap > kUMax, "hash geometry");
+        static_assert(kHashSlots > kSortCap + NT && kSortCap > kUMax, "hash geometry");
         unsigned long long* ht = reinterpret_cast<unsigned long long*>(L.scratch);
         int32_t* ul = reinterpret_cast<int32_t*>(ht + kHashSlots);  // distinct rows
         int32_t* us = ul + kSortCap;                                 // their slots
