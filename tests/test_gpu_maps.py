@@ -150,3 +150,36 @@ def test_subdivide_neighbors_matches_child_map(spc, orc, dev, name):
     assert torch.equal(got, want)
     ref = orc.conv_table_slat(child.cpu().numpy())
     assert np.array_equal(got.cpu().numpy().reshape(-1), ref.reshape(-1))
+
+
+def test_large_subdivided_shell_maps(spc, dev):
+    """The 256^3 level of the mesh decoder (sphere shell subdivided twice,
+    1.39M voxels): the hash-built table satisfies the closed-form invariants
+    (centre tap = self, symmetry nbr(i, o) = j <=> nbr(j, 26 - o) = i, masks =
+    valid taps, argsort stable by mask) and equals the table derived from the
+    128^3 parents' table."""
+    import torch
+
+    nat = spc._native
+    kids = np.array([[0, dx, dy, dz] for dx in (0, 1) for dy in (0, 1) for dz in (0, 1)], np.int32)
+    up = lambda c: (c[:, None, :] * np.array([1, 2, 2, 2], np.int32) + kids[None]).reshape(-1, 4)  # noqa: E731
+    par = np.ascontiguousarray(up(spc.workloads.sphere_shell()), dtype=np.int32)
+    child = np.ascontiguousarray(up(par), dtype=np.int32)
+    n, npar = child.shape[0], par.shape[0]
+    _case(f"large maps: {npar} parents at 128^3 -> {n} children at 256^3")
+    m = nat.map_build(torch.from_numpy(child).to(dev))
+    pm = nat.map_build(torch.from_numpy(par).to(dev), outputs="token")
+    derived = nat.subdivide_neighbors(pm.token_major, npar).token_major
+    assert torch.equal(derived, m.token_major)
+    tm = m.token_major.cpu().numpy().reshape(n, 27)
+    assert np.array_equal(tm[:, 13], np.arange(n))
+    i, o = np.nonzero(tm < n)
+    j = tm[i, o]
+    assert np.array_equal(tm[j, 26 - o], i)
+    om = m.offset_major.cpu().numpy().reshape(27, n)
+    assert np.array_equal(np.where(tm < n, tm, -1).T, om)
+    mask = ((tm < n) << np.arange(27)).sum(1)
+    assert np.array_equal(m.mask_natural.cpu().numpy(), mask)
+    ar = m.argsort.cpu().numpy()
+    assert np.array_equal(ar, np.argsort(mask, kind="stable"))
+    assert np.array_equal(m.mask_sorted.cpu().numpy(), mask[ar])
