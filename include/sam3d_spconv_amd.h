@@ -329,11 +329,12 @@ int spc_layernorm_silu(spc_stream_t stream, int dtype, const void* x, int64_t n,
  *   spc_group_norm_stats: stats (device f32 [n_batch, groups, 2]) =
  *     (mean, 1 / sqrt(var + eps)); F64 partial sums in a fixed order
  *     (deterministic), workspace of spc_group_norm_workspace_bytes.
- *   spc_group_norm_silu: y[i] = dt(silu(dt((x[r] - mean) * rstd * gamma +
- *     beta))) with r = rows[i] (rows NULL: r = i) -- the norm, SiLU and
- *     SparseSubdivide's parent gather of SparseSubdivideBlock3d's act_layers
- *     (decoder_mesh.py:69-73) in one pass; silu 0 skips the activation;
- *     gamma / beta f32 [c] or NULL.
+ *   spc_group_norm_silu: y[i] = dt(silu(dt(x[r] * a + b))) with the
+ *     per-channel a = rstd * gamma, b = beta - a * mean of r's item (the
+ *     fused form torch's group_norm evaluates) and r = rows[i] (rows NULL:
+ *     r = i) -- the norm, SiLU and SparseSubdivide's parent gather of
+ *     SparseSubdivideBlock3d's act_layers (decoder_mesh.py:69-73) in one
+ *     pass; silu 0 skips the activation; gamma / beta f32 [c] or NULL.
  * c <= 1024, a multiple of 4 and of groups. */
 size_t spc_group_norm_workspace_bytes(int64_t n_batch, int64_t max_rows, int64_t groups);
 int spc_group_norm_stats(spc_stream_t stream, int dtype, const void* x, int64_t c, int64_t groups,
