@@ -96,6 +96,19 @@ int spc_map_build(spc_stream_t stream, const int32_t* coords, int64_t n, int32_t
                   int32_t* mask_sorted, int32_t* argsort, int32_t* mask_natural,
                   void* workspace, size_t workspace_bytes);
 
+/* spc_map_build over a dense grid [n_batch][R][R][R] of row ids (R =
+ * resolution) instead of the hash table, for callers that bound the
+ * coordinates: 0 <= b < n_batch and 0 <= x, y, z < R (others are BAD_COORD).
+ * Same outputs, flags and duplicate rule (the first row owns a cell); each
+ * lookup is one load.  The workspace holds the grid (4 bytes a cell, at
+ * most 2^32 cells).  No reference counterpart (the reference's tables come
+ * from a std::map). */
+size_t spc_map_dense_workspace_bytes(int64_t n, int64_t n_batch, int32_t resolution);
+int spc_map_build_dense(spc_stream_t stream, const int32_t* coords, int64_t n, int64_t n_batch,
+                        int32_t resolution, uint32_t flags, int32_t* token_major,
+                        int32_t* offset_major, int32_t* mask_sorted, int32_t* argsort,
+                        int32_t* mask_natural, void* workspace, size_t workspace_bytes);
+
 /* Reads (and clears) the device status word of a map / downsample /
  * subdivide workspace.  Synchronises `stream`. */
 int spc_read_status(spc_stream_t stream, void* workspace);

@@ -64,6 +64,9 @@ def lib() -> ctypes.CDLL:
     L.spc_downsample_map.argtypes = [_P, _P, _I64, _I64, _I32, _P, _P, _P, _P, _P, _P, _P, _SZ]
     L.spc_stride2_inverse_taps.argtypes = [_P, _P, _P, _I64, _I64, _P]
     L.spc_compose_rows.argtypes = [_P, _P, _I64, _P, _I64, _P]
+    L.spc_map_dense_workspace_bytes.restype = _SZ
+    L.spc_map_dense_workspace_bytes.argtypes = [_I64, _I64, _I32]
+    L.spc_map_build_dense.argtypes = [_P, _P, _I64, _I64, _I32, _U32, _P, _P, _P, _P, _P, _P, _SZ]
     L.spc_subdivide_neighbors.argtypes = [_P, _P, _I64, _P]
     L.spc_subdivide_tap_classes.argtypes = [_P, _P, _I64, _I64, _P, _P]
     L.spc_sparse_conv_classes.argtypes = [_P, _INT, _P, _P, _P, _P, _P, _INT, _P, _P, _I64, _I64,
@@ -174,11 +177,18 @@ class SubmMap:
         return self._plan
 
 
+# dense-grid map builds up to this many cells (4 bytes each)
+DENSE_MAX_CELLS = 1 << 26
+
+
 def map_build(coords: torch.Tensor, *, mesh_resolution: int | None = None,
-              outputs: str = "all", sync: bool = True, workspace: torch.Tensor | None = None):
+              outputs: str = "all", sync: bool = True, workspace: torch.Tensor | None = None,
+              dense: tuple | None = None):
     """spc_map_build on int32 [N,4] device coords.  mesh_resolution selects the
     build_mesh_conv_table semantics (range + uniqueness checks).  outputs
-    "token" builds the token-major table only (no mask sort)."""
+    "token" builds the token-major table only (no mask sort).  dense =
+    (n_batch, resolution) bounds the coordinates (b < n_batch, x, y, z <
+    resolution) and builds over a dense grid (spc_map_build_dense)."""
     _need_gpu(coords)
     coords = coords.contiguous()
     if coords.dtype != torch.int32 or coords.dim() != 2 or coords.shape[1] != 4:
@@ -186,7 +196,14 @@ def map_build(coords: torch.Tensor, *, mesh_resolution: int | None = None,
     n = coords.shape[0]
     dev = coords.device
     L = lib()
-    ws = workspace if workspace is not None else _workspace(L.spc_map_workspace_bytes(n), dev)
+    if dense is not None:
+        nb, res = int(dense[0]), int(dense[1])
+        if mesh_resolution is not None and mesh_resolution != res:
+            raise ValueError("dense resolution must equal mesh_resolution")
+        wsb = L.spc_map_dense_workspace_bytes(n, nb, res)
+    else:
+        wsb = L.spc_map_workspace_bytes(n)
+    ws = workspace if workspace is not None else _workspace(wsb, dev)
     e = lambda k: torch.empty(k, dtype=torch.int32, device=dev)  # noqa: E731
     tm = e(27 * n)
     full = outputs == "all"
@@ -194,6 +211,11 @@ def map_build(coords: torch.Tensor, *, mesh_resolution: int | None = None,
     # the mask sort runs only when its outputs are asked for
     ms, ar, mn = (e(n), e(n), e(n)) if full else (None, None, None)
     flags = (MAP_MESH if mesh_resolution is not None else 0) | (MAP_SYNC if sync else 0)
+    if dense is not None:
+        st = L.spc_map_build_dense(_stream(dev), _ptr(coords), n, nb, res, flags, _ptr(tm),
+                                   _ptr(om), _ptr(ms), _ptr(ar), _ptr(mn), _ptr(ws), ws.numel())
+        _check("spc_map_build_dense", st)
+        return SubmMap(n, tm, om, ms, ar, mn)
     st = L.spc_map_build(_stream(dev), _ptr(coords), n, int(mesh_resolution or 0), flags,
                          _ptr(tm), _ptr(om), _ptr(ms), _ptr(ar), _ptr(mn), _ptr(ws), ws.numel())
     _check("spc_map_build", st)

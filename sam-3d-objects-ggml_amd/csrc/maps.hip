@@ -66,6 +66,28 @@ __global__ __launch_bounds__(256) void hash_insert_kernel(const int4* __restrict
     atomicOr(status, kErrOom);
 }
 
+// Dense grid: every cell INT_MAX, then each row takes its cell by atomicMin
+// (the first row of a duplicated coordinate owns it, like the hash table).
+__global__ void dense_init_kernel(int32_t* __restrict__ grid, int64_t cells4, int32_t* status) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < cells4) reinterpret_cast<int4*>(grid)[i] = int4{INT_MAX, INT_MAX, INT_MAX, INT_MAX};
+    if (i == 0) *status = 0;
+}
+
+__global__ __launch_bounds__(256) void dense_insert_kernel(const int4* __restrict__ coords,
+                                                           int64_t n, int32_t n_batch, int32_t res,
+                                                           int32_t* grid, int32_t* status) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int4 c = coords[i];
+    if (c.x < 0 || c.x >= n_batch || c.y < 0 || c.y >= res || c.z < 0 || c.z >= res || c.w < 0 ||
+        c.w >= res) {
+        atomicOr(status, kErrBadCoord);
+        return;
+    }
+    atomicMin(&grid[(((int64_t)c.x * res + c.y) * res + c.z) * res + c.w], (int32_t)i);
+}
+
 __device__ inline int32_t hash_find(const unsigned long long* __restrict__ hkeys,
                                     const int32_t* __restrict__ hvals, uint32_t cap_mask,
                                     unsigned long long key) {
@@ -81,12 +103,37 @@ __device__ inline int32_t hash_find(const unsigned long long* __restrict__ hkeys
 
 constexpr int kNbrTokens = 64;
 
+// Row lookups of the 27-offset query: the hash table, or a dense grid
+// [n_batch][R][R][R] of row ids when the caller bounds the coordinates.
+struct HashLookup {
+    const unsigned long long* hkeys;
+    const int32_t* hvals;
+    uint32_t cap_mask;
+    __device__ int32_t operator()(int b, int x, int y, int z) const {
+        if (b < 0 || b >= kBatchLimit || x < 0 || x >= kCoordLimit || y < 0 || y >= kCoordLimit ||
+            z < 0 || z >= kCoordLimit)
+            return -1;
+        return hash_find(hkeys, hvals, cap_mask, pack_key(b, x, y, z));
+    }
+};
+
+struct DenseLookup {
+    const int32_t* grid;
+    int32_t n_batch;
+    int32_t res;
+    __device__ int32_t operator()(int b, int x, int y, int z) const {
+        if (b < 0 || b >= n_batch || x < 0 || x >= res || y < 0 || y >= res || z < 0 || z >= res)
+            return -1;
+        const int32_t v = grid[(((int64_t)b * res + x) * res + y) * res + z];
+        return v == INT_MAX ? -1 : v;
+    }
+};
+
 // MESH: duplicates are an error (build_mesh_conv_table); otherwise the
 // SlatTables rule applies (only the owning row gets its neighbours).
-template <bool MESH>
+template <bool MESH, typename Lookup>
 __global__ __launch_bounds__(256) void neighbor_kernel(
-    const int4* __restrict__ coords, int64_t n, const unsigned long long* __restrict__ hkeys,
-    const int32_t* __restrict__ hvals, uint32_t cap_mask, int32_t* __restrict__ token_major,
+    const int4* __restrict__ coords, int64_t n, Lookup find, int32_t* __restrict__ token_major,
     int32_t* __restrict__ offset_major, int32_t* __restrict__ mask_nat, int32_t* status) {
     __shared__ int32_t nb[27][kNbrTokens + 1];
     __shared__ int32_t owner[kNbrTokens];
@@ -99,12 +146,7 @@ __global__ __launch_bounds__(256) void neighbor_kernel(
         int32_t res = -1;
         if (t < n) {
             const int4 c = coords[t];
-            const int32_t x = c.y + (o / 9 - 1);
-            const int32_t y = c.z + ((o / 3) % 3 - 1);
-            const int32_t z = c.w + (o % 3 - 1);
-            if (c.x >= 0 && c.x < kBatchLimit && x >= 0 && x < kCoordLimit && y >= 0 &&
-                y < kCoordLimit && z >= 0 && z < kCoordLimit)
-                res = hash_find(hkeys, hvals, cap_mask, pack_key(c.x, x, y, z));
+            res = find(c.x, c.y + (o / 9 - 1), c.z + ((o / 3) % 3 - 1), c.w + (o % 3 - 1));
         }
         nb[o][tl] = res;
     }
@@ -193,6 +235,46 @@ void carve_map_ws(C& c, int64_t n, MapWs* w) {
     const size_t sb = radix_sort_ws_bytes(n, 4);
     auto* sw = c.template take<char>(sb);
     if (w) *w = MapWs{st, hk, hv, mn, ms, ar, sw, sb};
+}
+
+// dense grid workspace: status, grid [n_batch * R^3] (a multiple of 4 cells),
+// then the same mask / sort buffers
+template <typename C>
+void carve_dense_ws(C& c, int64_t n, int64_t cells, MapWs* w, int32_t** grid) {
+    auto* st = c.template take<int32_t>(kStatusBytes / 4);
+    auto* g = c.template take<int32_t>((size_t)((cells + 3) / 4 * 4));
+    auto* mn = c.template take<int32_t>(n);
+    auto* ms = c.template take<uint32_t>(n);
+    auto* ar = c.template take<int32_t>(n);
+    const size_t sb = radix_sort_ws_bytes(n, 4);
+    auto* sw = c.template take<char>(sb);
+    if (w) *w = MapWs{st, nullptr, nullptr, mn, ms, ar, sw, sb};
+    if (grid) *grid = g;
+}
+
+// the 27-offset query, the masks' stable sort and the optional status read
+// shared by the hash and the dense builds
+template <typename Lookup>
+int finish_map(hipStream_t s, const int4* c4, int64_t n, bool mesh, Lookup find, uint32_t flags,
+               int32_t* token_major, int32_t* offset_major, int32_t* mask_sorted, int32_t* argsort,
+               int32_t* mask_natural, const MapWs& w) {
+    int32_t* mnat = mask_natural ? mask_natural : w.mask_nat;
+    const unsigned nb = (unsigned)((n + kNbrTokens - 1) / kNbrTokens);
+    if (mesh)
+        neighbor_kernel<true, Lookup><<<nb, 256, 0, s>>>(c4, n, find, token_major, offset_major,
+                                                         mnat, w.status);
+    else
+        neighbor_kernel<false, Lookup><<<nb, 256, 0, s>>>(c4, n, find, token_major, offset_major,
+                                                          mnat, w.status);
+    SPC_HIP(hipGetLastError());
+    if (mask_sorted || argsort) {
+        uint32_t* ms = mask_sorted ? reinterpret_cast<uint32_t*>(mask_sorted) : w.mask_sorted;
+        int32_t* ar = argsort ? argsort : w.argsort;
+        SPC_HIP(radix_sort_u32(s, reinterpret_cast<const uint32_t*>(mnat), nullptr, ms, ar, n, 27,
+                               w.sort_ws, w.sort_bytes));
+    }
+    if (flags & SPC_MAP_SYNC) return read_status_word(s, w.status);
+    return SPC_OK;
 }
 
 // ---- downsample ---------------------------------------------------------
@@ -455,26 +537,56 @@ int spc_map_build(spc_stream_t stream, const int32_t* coords, int64_t n, int32_t
     const int64_t cap = hash_capacity(n);
     const uint32_t cap_mask = (uint32_t)(cap - 1);
     const int4* c4 = reinterpret_cast<const int4*>(coords);
-    int32_t* mnat = mask_natural ? mask_natural : w.mask_nat;
     map_init_kernel<<<grid_for(cap, 256), 256, 0, s>>>(w.hkeys, w.hvals, cap, w.status);
     hash_insert_kernel<<<grid_for(n, 256), 256, 0, s>>>(c4, n, mesh ? resolution : kCoordLimit,
                                                         w.hkeys, w.hvals, cap_mask, w.status);
-    const unsigned nb = grid_for(n, kNbrTokens);
-    if (mesh)
-        neighbor_kernel<true><<<nb, 256, 0, s>>>(c4, n, w.hkeys, w.hvals, cap_mask, token_major,
-                                                 offset_major, mnat, w.status);
-    else
-        neighbor_kernel<false><<<nb, 256, 0, s>>>(c4, n, w.hkeys, w.hvals, cap_mask, token_major,
-                                                  offset_major, mnat, w.status);
-    SPC_HIP(hipGetLastError());
-    if (mask_sorted || argsort) {
-        uint32_t* ms = mask_sorted ? reinterpret_cast<uint32_t*>(mask_sorted) : w.mask_sorted;
-        int32_t* ar = argsort ? argsort : w.argsort;
-        SPC_HIP(radix_sort_u32(s, reinterpret_cast<const uint32_t*>(mnat), nullptr, ms, ar, n, 27,
-                               w.sort_ws, w.sort_bytes));
+    return finish_map(s, c4, n, mesh, HashLookup{w.hkeys, w.hvals, cap_mask}, flags, token_major,
+                      offset_major, mask_sorted, argsort, mask_natural, w);
+}
+
+size_t spc_map_dense_workspace_bytes(int64_t n, int64_t n_batch, int32_t resolution) {
+    if (n_batch <= 0 || resolution <= 0) return 0;
+    const int64_t r = resolution;
+    Sizer z;
+    carve_dense_ws(z, n > 0 ? n : 1, n_batch * r * r * r, nullptr, nullptr);
+    return z.used + 256;
+}
+
+int spc_map_build_dense(spc_stream_t stream, const int32_t* coords, int64_t n, int64_t n_batch,
+                        int32_t resolution, uint32_t flags, int32_t* token_major,
+                        int32_t* offset_major, int32_t* mask_sorted, int32_t* argsort,
+                        int32_t* mask_natural, void* workspace, size_t workspace_bytes) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (n <= 0 || n > INT32_MAX / 27 || n_batch <= 0 || n_batch > kBatchLimit || resolution <= 0 ||
+        resolution > kCoordLimit || n_batch * (int64_t)resolution * resolution * resolution >
+                                        ((int64_t)1 << 32)) {
+        set_last_error("spc_map_build_dense: n = %lld, n_batch = %lld, resolution = %d out of range "
+                       "(at most 2^32 cells)", (long long)n, (long long)n_batch, resolution);
+        return SPC_BAD_SHAPE;
     }
-    if (flags & SPC_MAP_SYNC) return read_status_word(s, w.status);
-    return SPC_OK;
+    if (!coords || !workspace || !aligned16(coords)) {
+        set_last_error("spc_map_build_dense: null or misaligned coords / workspace");
+        return SPC_BAD_ARG;
+    }
+    const int64_t r = resolution;
+    const int64_t cells = n_batch * r * r * r;
+    Carver c(workspace, workspace_bytes);
+    MapWs w;
+    int32_t* grid = nullptr;
+    carve_dense_ws(c, n, cells, &w, &grid);
+    if (!c.ok) {
+        set_last_error("spc_map_build_dense: workspace of %zu bytes < %zu", workspace_bytes,
+                       spc_map_dense_workspace_bytes(n, n_batch, resolution));
+        return SPC_OOM;
+    }
+    const int4* c4 = reinterpret_cast<const int4*>(coords);
+    const int64_t cells4 = (cells + 3) / 4;
+    dense_init_kernel<<<grid_for(cells4, 256), 256, 0, s>>>(grid, cells4, w.status);
+    dense_insert_kernel<<<grid_for(n, 256), 256, 0, s>>>(c4, n, (int32_t)n_batch, resolution, grid,
+                                                         w.status);
+    return finish_map(s, c4, n, (flags & SPC_MAP_MESH) != 0,
+                      DenseLookup{grid, (int32_t)n_batch, resolution}, flags, token_major,
+                      offset_major, mask_sorted, argsort, mask_natural, w);
 }
 
 int spc_read_status(spc_stream_t stream, void* workspace) {

@@ -380,7 +380,18 @@ def sparse_unbind(input: SparseTensor, dim: int) -> List[SparseTensor]:
 # maps (cached on the coordinates)
 # ---------------------------------------------------------------------------
 def _subm_map(x: SparseTensor) -> nat.SubmMap:
-    return x.data.cached("subm3", lambda c: nat.map_build(c.contiguous(), outputs="token"))
+    """The submanifold table of x's coordinates, cached on them: over a dense
+    grid when the batch count and spatial shape bound it within
+    nat.DENSE_MAX_CELLS cells, else over the hash table."""
+    def build(c):
+        nb, shape = x.data.batch_size, x.data.spatial_shape
+        if nb and shape and min(shape) > 0:
+            res = max(int(v) for v in shape)
+            if nb * res ** 3 <= nat.DENSE_MAX_CELLS:
+                return nat.map_build(c.contiguous(), outputs="token", dense=(nb, res))
+        return nat.map_build(c.contiguous(), outputs="token")
+
+    return x.data.cached("subm3", build)
 
 
 def _resolution(x: SparseTensor) -> int:

@@ -24,17 +24,21 @@ def _coord_sets(spc):
     }
 
 
+@pytest.mark.parametrize("dense", [False, True])
 @pytest.mark.parametrize("name", ["sphere64", "ellipsoids4", "random_dups_unsorted", "single",
                                   "ragged_193"])
-def test_map_build_matches_oracle(spc, orc, dev, name):
+def test_map_build_matches_oracle(spc, orc, dev, name, dense):
+    """Hash-table and dense-grid builds, bit-exact with the oracle (the
+    compiled reference's SlatTables)."""
     import torch
 
     coords = _coord_sets(spc)[name]
-    _case(f"map_build {name} N={coords.shape[0]}")
+    _case(f"map_build {name} N={coords.shape[0]} dense={dense}")
     n = coords.shape[0]
     tm_ref = orc.conv_table_slat(coords)
     om_ref, ms_ref, ar_ref = orc.spconv_tables(tm_ref, n)
-    m = spc._native.map_build(torch.from_numpy(coords).to(dev))
+    ext = (int(coords[:, 0].max()) + 1, int(coords[:, 1:].max()) + 1) if dense else None
+    m = spc._native.map_build(torch.from_numpy(coords).to(dev), dense=ext)
     assert np.array_equal(m.token_major.cpu().numpy(), tm_ref)
     assert np.array_equal(m.offset_major.cpu().numpy(), om_ref)
     assert np.array_equal(m.mask_sorted.cpu().numpy(), ms_ref)
@@ -74,6 +78,16 @@ def test_map_mesh_errors(spc, dev):
     with pytest.raises(nat.SparseConvError) as e:
         nat.map_build(torch.from_numpy(neg).to(dev))
     assert e.value.status == nat.BAD_COORD
+    # the dense grid: mesh duplicates, coordinates or batches beyond the bound
+    with pytest.raises(nat.SparseConvError) as e:
+        nat.map_build(torch.from_numpy(dup).to(dev), mesh_resolution=8, dense=(1, 8))
+    assert e.value.status == nat.DUP_COORD
+    m = nat.map_build(torch.from_numpy(ok).to(dev), mesh_resolution=8, dense=(1, 8))
+    assert m.token_major.cpu().numpy().reshape(2, 27)[0, 14] == 1
+    for bad, ext in ((oor, (1, 8)), (neg, (1, 8)), (np.array([[1, 1, 2, 3]], np.int32), (1, 8))):
+        with pytest.raises(nat.SparseConvError) as e:
+            nat.map_build(torch.from_numpy(bad).to(dev), dense=ext)
+        assert e.value.status == nat.BAD_COORD
 
 
 def test_mesh_levels_match_oracle(spc, orc, dev):
@@ -168,6 +182,8 @@ def test_large_subdivided_shell_maps(spc, dev):
     n, npar = child.shape[0], par.shape[0]
     _case(f"large maps: {npar} parents at 128^3 -> {n} children at 256^3")
     m = nat.map_build(torch.from_numpy(child).to(dev))
+    assert torch.equal(nat.map_build(torch.from_numpy(child).to(dev), outputs="token",
+                                     dense=(1, 256)).token_major, m.token_major)
     pm = nat.map_build(torch.from_numpy(par).to(dev), outputs="token")
     derived = nat.subdivide_neighbors(pm.token_major, npar).token_major
     assert torch.equal(derived, m.token_major)
