@@ -1174,7 +1174,8 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
             const int c = tid + k * NT;
             const int q = c % UPR;
             if (tt[k] >= 0)
-                *reinterpret_cast<u32x4*>(yb + ((int64_t)tt[k] * a.cout + co0) * ES + q * 16) = vv[k];
+                __builtin_nontemporal_store(
+                    vv[k], reinterpret_cast<u32x4*>(yb + ((int64_t)tt[k] * a.cout + co0) * ES + q * 16));
         }
     }
 }
