@@ -17,7 +17,7 @@ namespace {
 constexpr int kNormMaxC = 2048;
 
 template <int DT>
-struct Elem;
+struct Elem;  // feature loads / stores (streaming outputs: non-temporal stores)
 template <>
 struct Elem<SPC_F32> {
     __device__ static void ld4(const void* p, int64_t i, float* v) {
@@ -25,7 +25,8 @@ struct Elem<SPC_F32> {
         v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
     }
     __device__ static void st4(void* p, int64_t i, const float* v) {
-        *reinterpret_cast<floatx4*>(static_cast<float*>(p) + i) = floatx4{v[0], v[1], v[2], v[3]};
+        __builtin_nontemporal_store(floatx4{v[0], v[1], v[2], v[3]},
+                                    reinterpret_cast<floatx4*>(static_cast<float*>(p) + i));
     }
     __device__ static float round(float v) { return v; }
 };
@@ -37,9 +38,10 @@ struct Elem<SPC_BF16> {
         v[2] = __uint_as_float(q.y << 16); v[3] = __uint_as_float(q.y & 0xffff0000u);
     }
     __device__ static void st4(void* p, int64_t i, const float* v) {
-        *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(p) + i) =
+        __builtin_nontemporal_store(
             u32x2{(uint32_t)f32_to_bf16_bits(v[0]) | ((uint32_t)f32_to_bf16_bits(v[1]) << 16),
-                  (uint32_t)f32_to_bf16_bits(v[2]) | ((uint32_t)f32_to_bf16_bits(v[3]) << 16)};
+                  (uint32_t)f32_to_bf16_bits(v[2]) | ((uint32_t)f32_to_bf16_bits(v[3]) << 16)},
+            reinterpret_cast<u32x2*>(static_cast<uint16_t*>(p) + i));
     }
     __device__ static float round(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
 };
@@ -51,9 +53,10 @@ struct Elem<SPC_F16> {
         v[2] = f16_bits_to_f32((uint16_t)q.y); v[3] = f16_bits_to_f32((uint16_t)(q.y >> 16));
     }
     __device__ static void st4(void* p, int64_t i, const float* v) {
-        *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(p) + i) =
+        __builtin_nontemporal_store(
             u32x2{(uint32_t)f32_to_f16_bits(v[0]) | ((uint32_t)f32_to_f16_bits(v[1]) << 16),
-                  (uint32_t)f32_to_f16_bits(v[2]) | ((uint32_t)f32_to_f16_bits(v[3]) << 16)};
+                  (uint32_t)f32_to_f16_bits(v[2]) | ((uint32_t)f32_to_f16_bits(v[3]) << 16)},
+            reinterpret_cast<u32x2*>(static_cast<uint16_t*>(p) + i));
     }
     __device__ static float round(float v) { return f16_bits_to_f32(f32_to_f16_bits(v)); }
 };
