@@ -931,7 +931,8 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
                         for (int q = 0; q < NMF; ++q) {
                             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                             if (q < NFR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                            __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+                            // Q8_0: room for the in-register dequantisation
+                            __builtin_amdgcn_sched_group_barrier(0x002, Q8 ? 6 : 2, 0);
                         }
                         __builtin_amdgcn_sched_group_barrier(0x020, FN * P::NG, 0);
                         // nothing crosses a step boundary: without this fence the
