@@ -51,7 +51,7 @@ __device__ inline int32_t wave_incl_scan(int32_t v, int lane) {
 template <typename K, int ITEMS>
 __global__ __launch_bounds__(kRsThreads) void rs_upsweep(const K* __restrict__ keys, int64_t n,
                                                          int shift, int32_t* __restrict__ counts,
-                                                         int nblocks) {
+                                                         int stride) {
     __shared__ int32_t hist[kRsBins];
 #pragma unroll
     for (int j = 0; j < kRsBinsPerThread; ++j) hist[j * kRsThreads + threadIdx.x] = 0;
@@ -69,7 +69,7 @@ __global__ __launch_bounds__(kRsThreads) void rs_upsweep(const K* __restrict__ k
 #pragma unroll
     for (int j = 0; j < kRsBinsPerThread; ++j) {
         const int d = j * kRsThreads + threadIdx.x;
-        counts[(int64_t)d * nblocks + blockIdx.x] = hist[d];
+        counts[(int64_t)d * stride + blockIdx.x] = hist[d];
     }
 }
 
@@ -84,7 +84,7 @@ template <typename K, bool FUSED, int ITEMS>
 __global__ __launch_bounds__(kRsThreads) void rs_downsweep(
     const K* __restrict__ keys_in, const int32_t* __restrict__ vals_in, K* __restrict__ keys_out,
     int32_t* __restrict__ vals_out, int64_t n, int shift, const int32_t* __restrict__ offsets,
-    int nblocks) {
+    int nblocks, int stride) {
     __shared__ int32_t wave_off[kRsWaves][kRsBins];
     __shared__ int32_t run[kRsBins];
     __shared__ int32_t wsum[kRsWaves];
@@ -97,13 +97,22 @@ __global__ __launch_bounds__(kRsThreads) void rs_downsweep(
         int32_t mine = 0;
 #pragma unroll
         for (int j = 0; j < kRsBinsPerThread; ++j) {
-            const int32_t* c = offsets + (int64_t)(kRsBinsPerThread * tid + j) * nblocks;
+            // the digit's row of per-block counts, four at a time (stride is a
+            // multiple of four; entries past nblocks are padding)
+            const int4* c = reinterpret_cast<const int4*>(
+                offsets + (int64_t)(kRsBinsPerThread * tid + j) * stride);
             int32_t t = 0, bsum = 0;
 #pragma unroll 8
-            for (int b = 0; b < nblocks; ++b) {  // eight loads in flight
-                const int32_t v = c[b];
-                t += v;
-                if (b < (int)blockIdx.x) bsum += v;
+            for (int q = 0; q < stride / 4; ++q) {  // eight 16-byte loads in flight
+                const int4 v4 = c[q];
+                const int32_t v[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int b = 4 * q + e;
+                    const int32_t vv = b < nblocks ? v[e] : 0;
+                    t += vv;
+                    if (b < (int)blockIdx.x) bsum += vv;
+                }
             }
             tot[j] = t;
             before[j] = bsum;
@@ -125,7 +134,7 @@ __global__ __launch_bounds__(kRsThreads) void rs_downsweep(
 #pragma unroll
         for (int j = 0; j < kRsBinsPerThread; ++j) {
             const int d = j * kRsThreads + tid;
-            run[d] = offsets[(int64_t)d * nblocks + blockIdx.x];
+            run[d] = offsets[(int64_t)d * stride + blockIdx.x];
         }
     }
     const int64_t base = (int64_t)blockIdx.x * (kRsThreads * ITEMS);
@@ -297,14 +306,17 @@ template <typename K, int ITEMS>
 hipError_t radix_sort_items(hipStream_t s, const K* keys_in, const int32_t* vals_in, K* keys_out,
                             int32_t* vals_out, int64_t n, int end_bit, void* ws, size_t ws_bytes) {
     const int nblocks = (int)ceil_div(n, (int64_t)kRsThreads * ITEMS);
+    const bool fused = nblocks <= kRsFusedBlocks;
+    // fused: digit rows padded to a multiple of four for 16-byte reads; the
+    // single-block scan walks the counts linearly, so no padding there
+    const int stride = fused ? (nblocks + 3) / 4 * 4 : nblocks;
     Carver c(ws, ws_bytes);
-    int32_t* counts = c.take<int32_t>((size_t)kRsBins * nblocks);
+    int32_t* counts = c.take<int32_t>((size_t)kRsBins * stride);
     K* tk[2] = {c.take<K>(n), c.take<K>(n)};
     int32_t* tv[2] = {c.take<int32_t>(n), c.take<int32_t>(n)};
     if (!c.ok) return hipErrorInvalidValue;
     int passes = (end_bit + kRsBits - 1) / kRsBits;
     if (passes < 1) passes = 1;
-    const bool fused = nblocks <= kRsFusedBlocks;
     const K* kin = keys_in;
     const int32_t* vin = vals_in;
     for (int p = 0; p < passes; ++p) {
@@ -312,14 +324,14 @@ hipError_t radix_sort_items(hipStream_t s, const K* keys_in, const int32_t* vals
         K* kout = last ? keys_out : tk[p & 1];
         int32_t* vout = last ? vals_out : tv[p & 1];
         const int shift = p * kRsBits;
-        rs_upsweep<K, ITEMS><<<nblocks, kRsThreads, 0, s>>>(kin, n, shift, counts, nblocks);
+        rs_upsweep<K, ITEMS><<<nblocks, kRsThreads, 0, s>>>(kin, n, shift, counts, stride);
         if (fused) {
-            rs_downsweep<K, true, ITEMS><<<nblocks, kRsThreads, 0, s>>>(kin, vin, kout, vout, n,
-                                                                        shift, counts, nblocks);
+            rs_downsweep<K, true, ITEMS><<<nblocks, kRsThreads, 0, s>>>(
+                kin, vin, kout, vout, n, shift, counts, nblocks, stride);
         } else {
             scan_one_block<<<1, 1024, 0, s>>>(counts, counts, nullptr, (int64_t)kRsBins * nblocks);
-            rs_downsweep<K, false, ITEMS><<<nblocks, kRsThreads, 0, s>>>(kin, vin, kout, vout, n,
-                                                                         shift, counts, nblocks);
+            rs_downsweep<K, false, ITEMS><<<nblocks, kRsThreads, 0, s>>>(
+                kin, vin, kout, vout, n, shift, counts, nblocks, stride);
         }
         kin = kout;
         vin = vout;
@@ -375,7 +387,7 @@ size_t radix_sort_ws_bytes(int64_t n, int key_bytes) {
     const int64_t m = n > 0 ? n : 1;
     const int64_t nblocks = ceil_div(m, (int64_t)kRsThreads * rs_items(m));
     Sizer z;
-    z.take<int32_t>((size_t)kRsBins * nblocks);
+    z.take<int32_t>((size_t)kRsBins * ((nblocks + 3) / 4 * 4));
     for (int i = 0; i < 2; ++i) z.take<char>((size_t)n * key_bytes);
     for (int i = 0; i < 2; ++i) z.take<int32_t>(n);
     return z.used + 256;
