@@ -210,51 +210,58 @@ inline int64_t gn_chunks(int64_t n_batch, int64_t max_rows) {
     return std::max<int64_t>(1, (max_rows + r - 1) / r);
 }
 
-template <int DT>
+// Lanes take runs of W = 4 * NV channels (16-byte loads for 2-byte types
+// with NV = 2); c / W run lanes x floor(256 / (c / W)) row lanes.
+template <int DT, int NV>
 __global__ __launch_bounds__(256) void gn_partial_kernel(const void* __restrict__ x, int c, int groups,
                                                          const int64_t* __restrict__ off, int rows_per,
                                                          double* __restrict__ part, int chunks) {
     using E = Elem<DT>;
-    __shared__ float ls[2 * kGnMaxC];     // [row lane][c] sums, then squares
+    constexpr int W = 4 * NV;
+    constexpr int LS = 256 * W;           // rl_n * c = rl_n * nrun * W <= 256 * W
+    __shared__ float ls[2 * LS];          // [row lane][c] sums, then squares
     __shared__ double cs[2 * kGnMaxC];
     const int b = blockIdx.y;
     const int64_t r0 = off[b] + (int64_t)blockIdx.x * rows_per;
     const int64_t r1 = min(off[b + 1], r0 + rows_per);
-    const int nvec = c / 4;
-    int np = 1;
-    while (np < nvec) np <<= 1;
-    const int rl_n = 256 / np;  // row lanes: rl_n * c <= 1024
+    const int nrun = c / W;
+    const int rl_n = 256 / nrun;          // row lanes
     const int tid = threadIdx.x;
-    const int v = tid % np, rl = tid / np;
-    float s[4] = {0.f, 0.f, 0.f, 0.f}, q[4] = {0.f, 0.f, 0.f, 0.f};
-    if (v < nvec) {
+    const int v = tid % nrun, rl = tid / nrun;
+    float s[W], q[W];
+#pragma unroll
+    for (int e = 0; e < W; ++e) s[e] = q[e] = 0.f;
+    if (rl < rl_n) {
         int64_t r = r0 + rl;
         // four rows in flight per lane
         for (; r + 3 * rl_n < r1; r += 4 * rl_n) {
-            float t[4][4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) E::ld4(x, (r + u * rl_n) * c + 4 * v, t[u]);
+            float t[4][W];
 #pragma unroll
             for (int u = 0; u < 4; ++u)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
+                for (int h = 0; h < NV; ++h) E::ld4(x, (r + u * rl_n) * c + W * v + 4 * h, t[u] + 4 * h);
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int e = 0; e < W; ++e) {
                     s[e] += t[u][e];
                     q[e] += t[u][e] * t[u][e];
                 }
         }
         for (; r < r1; r += rl_n) {
-            float t[4];
-            E::ld4(x, r * c + 4 * v, t);
+            float t[W];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
+            for (int h = 0; h < NV; ++h) E::ld4(x, r * c + W * v + 4 * h, t + 4 * h);
+#pragma unroll
+            for (int e = 0; e < W; ++e) {
                 s[e] += t[e];
                 q[e] += t[e] * t[e];
             }
         }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            ls[rl * c + 4 * v + e] = s[e];
-            ls[kGnMaxC + rl * c + 4 * v + e] = q[e];
+        for (int e = 0; e < W; ++e) {
+            ls[rl * c + W * v + e] = s[e];
+            ls[LS + rl * c + W * v + e] = q[e];
         }
     }
     __syncthreads();
@@ -262,7 +269,7 @@ __global__ __launch_bounds__(256) void gn_partial_kernel(const void* __restrict_
         double a = 0.0, aa = 0.0;
         for (int k = 0; k < rl_n; ++k) {
             a += ls[k * c + ch];
-            aa += ls[kGnMaxC + k * c + ch];
+            aa += ls[LS + k * c + ch];
         }
         cs[ch] = a;
         cs[kGnMaxC + ch] = aa;
@@ -386,8 +393,12 @@ hipError_t launch_gn_stats(hipStream_t s, const void* x, int c, int groups, cons
                            int n_batch, int64_t max_rows, double* part, float eps, float* stats) {
     const int rows_per = (int)gn_chunk_rows(n_batch, max_rows);
     const int chunks = (int)gn_chunks(n_batch, max_rows);
-    gn_partial_kernel<DT><<<dim3(chunks, n_batch), 256, 0, s>>>(x, c, groups, off, rows_per, part,
-                                                                chunks);
+    if (DT != SPC_F32 && c % 8 == 0)
+        gn_partial_kernel<DT, 2><<<dim3(chunks, n_batch), 256, 0, s>>>(x, c, groups, off, rows_per,
+                                                                       part, chunks);
+    else
+        gn_partial_kernel<DT, 1><<<dim3(chunks, n_batch), 256, 0, s>>>(x, c, groups, off, rows_per,
+                                                                       part, chunks);
     gn_finalize_kernel<<<n_batch * groups, 64, 0, s>>>(part, off, groups, chunks, rows_per,
                                                       c / groups, eps, stats);
     return hipGetLastError();
