@@ -1204,6 +1204,17 @@ hipError_t dispatch_tn(hipStream_t s, const ConvArgs& a) {
     const int64_t tiles_m = ceil_div(a.n_out, kTM);
     int tn = a.cout % 128 == 0 ? 128 : a.cout % 64 == 0 ? 64 : 32;
     while (tn > 32 && tiles_m * (a.cout / (tn / 2)) <= a.num_cu) tn /= 2;
+    // a ragged last round of 128-column tiles (e.g. 368 tiles on 256 compute
+    // units: two rounds, the second 44% full) costs a whole round; 64-column
+    // tiles (about 0.6 of the time each) pay off when they need fewer than
+    // 10/6 as many rounds (SubM 1024 -> 1024 over 11774 rows: 627 -> 591 us)
+    if constexpr (!Q8) {
+        if (tn == 128) {
+            const int64_t r128 = ceil_div(tiles_m * (a.cout / 128), a.num_cu);
+            const int64_t r64 = ceil_div(tiles_m * (a.cout / 64), a.num_cu);
+            if (r64 * 6 < r128 * 10) tn = 64;
+        }
+    }
     if (a.epi_mode == SPC_EPI_NORM_MOD_SILU) {
         if (a.cout > 128) return hipErrorInvalidValue;  // rows wider than one tile
         tn = a.cout;                                    // one tile covers the row
