@@ -101,8 +101,9 @@ int spc_map_build(spc_stream_t stream, const int32_t* coords, int64_t n, int32_t
  * coordinates: 0 <= b < n_batch and 0 <= x, y, z < R (others are BAD_COORD).
  * Same outputs, flags and duplicate rule (the first row owns a cell); each
  * lookup is one load.  The workspace holds the grid (4 bytes a cell, at
- * most 2^32 cells).  No reference counterpart (the reference's tables come
- * from a std::map). */
+ * most 2^32 cells; the size query returns 0 and the build BAD_SHAPE beyond
+ * that or for n_batch / resolution out of range).  No reference counterpart
+ * (the reference's tables come from a std::map). */
 size_t spc_map_dense_workspace_bytes(int64_t n, int64_t n_batch, int32_t resolution);
 int spc_map_build_dense(spc_stream_t stream, const int32_t* coords, int64_t n, int64_t n_batch,
                         int32_t resolution, uint32_t flags, int32_t* token_major,

@@ -544,8 +544,17 @@ int spc_map_build(spc_stream_t stream, const int32_t* coords, int64_t n, int32_t
                       offset_major, mask_sorted, argsort, mask_natural, w);
 }
 
+// n_batch * resolution^3 within 2^32 cells, tested by division: the product
+// itself reaches 2^63 at the domain's ends (2^18 batches of 32768^3)
+static bool dense_cells_ok(int64_t n_batch, int32_t resolution) {
+    if (n_batch <= 0 || n_batch > kBatchLimit || resolution <= 0 || resolution > kCoordLimit)
+        return false;
+    const int64_t r = resolution;
+    return n_batch <= ((int64_t)1 << 32) / (r * r * r);
+}
+
 size_t spc_map_dense_workspace_bytes(int64_t n, int64_t n_batch, int32_t resolution) {
-    if (n_batch <= 0 || resolution <= 0) return 0;
+    if (!dense_cells_ok(n_batch, resolution)) return 0;
     const int64_t r = resolution;
     Sizer z;
     carve_dense_ws(z, n > 0 ? n : 1, n_batch * r * r * r, nullptr, nullptr);
@@ -557,9 +566,7 @@ int spc_map_build_dense(spc_stream_t stream, const int32_t* coords, int64_t n, i
                         int32_t* offset_major, int32_t* mask_sorted, int32_t* argsort,
                         int32_t* mask_natural, void* workspace, size_t workspace_bytes) {
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (n <= 0 || n > INT32_MAX / 27 || n_batch <= 0 || n_batch > kBatchLimit || resolution <= 0 ||
-        resolution > kCoordLimit || n_batch * (int64_t)resolution * resolution * resolution >
-                                        ((int64_t)1 << 32)) {
+    if (n <= 0 || n > INT32_MAX / 27 || !dense_cells_ok(n_batch, resolution)) {
         set_last_error("spc_map_build_dense: n = %lld, n_batch = %lld, resolution = %d out of range "
                        "(at most 2^32 cells)", (long long)n, (long long)n_batch, resolution);
         return SPC_BAD_SHAPE;

@@ -81,3 +81,19 @@ def test_block_entries_validate_before_device_work(spc):
                                   0) == nat.BAD_ARG  # workspace too small
     assert L.spc_group_norm_silu(None, nat.BF16, fake, 10, 100, 32, fake, 1, fake, None, None, 1,
                                  None, 10, fake) == nat.BAD_SHAPE  # c not a multiple of groups
+
+
+def test_dense_map_bounds_the_grid_on_the_host(spc):
+    """spc_map_build_dense takes at most 2^32 grid cells; the bound holds at
+    the domain's ends, where n_batch * resolution^3 reaches 2^63 (2^18
+    batches of 32768^3), and is checked before any device work."""
+    nat = spc._native
+    L = nat.lib()
+    fake = 1 << 12
+    assert L.spc_map_dense_workspace_bytes(100, 4, 1024) >= 4 << 30  # 2^32 cells: the limit
+    for nb, res in ((5, 1024), (1 << 18, 1 << 15), (1, 1 << 15), (0, 64), (1, 0), (1 << 19, 1)):
+        assert L.spc_map_dense_workspace_bytes(100, nb, res) == 0
+        st = L.spc_map_build_dense(None, fake, 100, nb, res, 0, fake, None, None, None, None, fake,
+                                   1 << 40)
+        assert st == nat.BAD_SHAPE, (nb, res)
+        assert b"out of range" in L.spc_last_error()

@@ -90,6 +90,41 @@ def test_map_mesh_errors(spc, dev):
         assert e.value.status == nat.BAD_COORD
 
 
+def test_map_build_domain_edges(spc, orc, dev):
+    """Voxels at both ends of the accepted domain (x, y, z in [0, 32768), b in
+    [0, 262144)): a neighbour past an end is absent, no two keys alias (the
+    oracle keys on the full integers), and one past either end is
+    BAD_COORD."""
+    import torch
+
+    nat = spc._native
+    _case("map_build domain edges")
+    rng = np.random.default_rng(11)
+    vals = np.array([0, 1, 2, 32765, 32766, 32767])
+    pts = np.stack(np.meshgrid(vals, vals, vals, indexing="ij"), -1).reshape(-1, 3)
+    parts = []
+    for b in (0, 1, 262142, 262143):
+        keep = pts[rng.random(len(pts)) < 0.7]
+        parts.append(np.concatenate([np.full((len(keep), 1), b), keep], 1))
+    coords = np.ascontiguousarray(np.concatenate(parts), dtype=np.int32)
+    n = coords.shape[0]
+    tm_ref = orc.conv_table_slat(coords)
+    om_ref, ms_ref, ar_ref = orc.spconv_tables(tm_ref, n)
+    m = nat.map_build(torch.from_numpy(coords).to(dev))
+    assert np.array_equal(m.token_major.cpu().numpy(), tm_ref)
+    assert np.array_equal(m.offset_major.cpu().numpy(), om_ref)
+    assert np.array_equal(m.mask_sorted.cpu().numpy(), ms_ref)
+    assert np.array_equal(m.argsort.cpu().numpy(), ar_ref)
+    for bad in ([0, 32768, 0, 0], [0, 0, 32768, 0], [0, 0, 0, 32768], [262144, 0, 0, 0]):
+        c = np.array([[0, 5, 5, 5], bad], np.int32)
+        with pytest.raises(nat.SparseConvError) as e:
+            nat.map_build(torch.from_numpy(c).to(dev))
+        assert e.value.status == nat.BAD_COORD
+    with pytest.raises(nat.SparseConvError) as e:  # 2^63 cells: refused on the host
+        nat.map_build(torch.from_numpy(coords).to(dev), dense=(262144, 32768))
+    assert e.value.status == nat.BAD_SHAPE
+
+
 def test_mesh_levels_match_oracle(spc, orc, dev):
     """Config-4 subdivision (seeded 50% pruning) and the mesh conv tables."""
     import torch
