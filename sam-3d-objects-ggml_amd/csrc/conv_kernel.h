@@ -954,38 +954,63 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
             }
         }
     } else if (nt > 0) {
-        // Fallback (the union does not fit the stage): each tap's 256 source
-        // rows are staged separately, one synchronous step at a time.
+        // Fallback (the union does not fit the stage): the 256 source rows of
+        // up to G taps at a time are staged at rows g * TM + r of the whole A
+        // area (both buffers), with every global load of the round in flight
+        // together; the round's steps then run from LDS, each step's weights
+        // loaded while the previous step's MFMAs run.
+        constexpr int UPT = (TM * kSegs + NT - 1) / NT;
+        constexpr int GA = 2 * STAGE / (TM * kPitch);
+        constexpr int G = GA < 14 / UPT ? GA : 14 / UPT;  // taps per round (<= 56 VGPRs of loads)
+        static_assert(G >= 1 && G * TM * kPitch <= 2 * STAGE, "fallback rounds fit the A area");
         for (int kc = 0; kc < kch; ++kc) {
+            const int64_t koff = (int64_t)kc * KC * ES;
             uint32_t m = tile_mask;
             while (m) {
-                const int o = __ffs(m) - 1;
-                m &= m - 1;
-                lds_barrier();  // every wave is done reading the stage
-                {
-                    const int64_t koff = (int64_t)kc * KC * ES;
-                    constexpr int UPT = (TM * kSegs + NT - 1) / NT;
+                int og[G];  // the round's taps (-1 past the last)
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    og[g] = m ? __ffs(m) - 1 : -1;
+                    m &= m - 1;  // no-op once m is 0
+                }
+                u32x4 v[G][UPT];
+#pragma unroll
+                for (int g = 0; g < G; ++g)
 #pragma unroll
                     for (int j = 0; j < UPT; ++j) {
                         const int u = j * NT + tid;
-                        if (TM * kSegs % NT != 0 && u >= TM * kSegs) break;
-                        const int32_t src = src_of(o, u >> 2);
-                        u32x4 v = zero4;
+                        v[g][j] = zero4;
+                        if (og[g] < 0 || (TM * kSegs % NT != 0 && u >= TM * kSegs)) continue;
+                        const int32_t src = src_of(og[g], u >> 2);
                         if (src >= 0)
-                            v = *reinterpret_cast<const u32x4*>(xb + (int64_t)src * a.cin * ES + koff +
-                                                                (u & 3) * 16);
-                        Au[seg_pos(u >> 2, u & 3)] = v;
+                            v[g][j] = *reinterpret_cast<const u32x4*>(xb + (int64_t)src * a.cin * ES +
+                                                                      koff + (u & 3) * 16);
                     }
-                }
-                lds_barrier();
-                int sl[FM];
+                Slot bs[2];
+                load_b(og[0], kc, bs[0]);
+                lds_barrier();  // every wave is done reading the A area
 #pragma unroll
-                for (int i = 0; i < FM; ++i) sl[i] = slot_key(wm * WTM + i * 32 + (lane & 31));
-                AFrag af;
-                read_frags(0, sl, af);
-                Slot bs;
-                load_b(o, kc, bs);
-                mma_step(af, bs);
+                for (int g = 0; g < G; ++g)
+#pragma unroll
+                    for (int j = 0; j < UPT; ++j) {
+                        const int u = j * NT + tid;
+                        if (og[g] < 0 || (TM * kSegs % NT != 0 && u >= TM * kSegs)) continue;
+                        Au[seg_pos(g * TM + (u >> 2), u & 3)] = v[g][j];
+                    }
+                lds_barrier();
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    if (og[g] < 0) break;
+                    if (g + 1 < G && og[g + 1 < G ? g + 1 : g] >= 0)
+                        load_b(og[g + 1 < G ? g + 1 : g], kc, bs[(g + 1) & 1]);
+                    int sl[FM];
+#pragma unroll
+                    for (int i = 0; i < FM; ++i)
+                        sl[i] = slot_key(g * TM + wm * WTM + i * 32 + (lane & 31));
+                    AFrag af;
+                    read_frags(0, sl, af);
+                    mma_step(af, bs[g & 1]);
+                }
             }
         }
     }
