@@ -343,3 +343,64 @@ def test_plan_matches_in_kernel_setup(spc, orc, dev, case):
     torch.cuda.synchronize()
     assert torch.equal(y0, y1)
     assert torch.isfinite(y1.float()).all()
+
+
+@pytest.mark.parametrize("case,n_obj,cin,cout", [("bf16", 5, 64, 192), ("bf16", 2, 128, 128),
+                                                 ("f32", 2, 32, 64), ("q8_0", 2, 64, 128)])
+def test_fallback_tiles_match_fast_tiles(spc, orc, dev, case, n_obj, cin, cout):
+    """Rows in random order put each tile's 256 rows over thousands of
+    distinct source rows, beyond the stage: every tile takes the fallback,
+    which stages up to 7 taps' rows per round with 8 waves (3 with the
+    4-wave 192-column and Q8_0 tiles).  A row accumulates the same steps in
+    the same order on both paths (chunks outer, taps ascending; absent taps
+    add exact zeros), so the shuffled conv equals the sorted conv row for
+    row, bit for bit; sampled rows of the sorted conv match the oracle."""
+    import oracle
+    import torch
+
+    nat = spc._native
+    wl = spc.workloads
+    coords = wl.ellipsoid_batch(n_obj, seed=73)
+    n = coords.shape[0]
+    _case(f"fallback vs fast tiles: {case} N={n} {cin}->{cout}")
+    perm = np.random.default_rng(74).permutation(n)
+    wf = wl.normal((cout, 27, cin), 0.02, seed=76)
+    if case == "f32":
+        x, w, b = wl.normal((n, cin), 1.0, seed=75), wf, wl.normal((cout,), 0.01, seed=77)
+        to_dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+        pw = nat.pack_weights(to_dev(w))
+    else:
+        x = bf16_bits(orc, wl.normal((n, cin), 1.0, seed=75))
+        b = bf16_bits(orc, wl.normal((cout,), 0.01, seed=77))
+        to_dev = lambda a: to_dev_bf16(np.ascontiguousarray(a), dev)  # noqa: E731
+        if case == "q8_0":
+            blocks = orc.q8_0_quantize(wf)
+            qs, dsc = nat.q8_0_repack(torch.from_numpy(blocks).to(dev))
+            pw = nat.pack_weights(qs, dsc, cin=cin, cout=cout)
+            w = orc.q8_0_dequant(blocks, oracle.F16)
+        else:
+            w = bf16_bits(orc, wf)
+            pw = nat.pack_weights(to_dev(w))
+    bd = to_dev(b)
+
+    def conv(c, xx):
+        m = nat.map_build(torch.from_numpy(np.ascontiguousarray(c)).to(dev))
+        return nat.sparse_conv(to_dev(xx), pw, bd, m.token_major, ntaps=27, n_out=len(c)), m
+
+    y0, m0 = conv(coords, x)
+    y1, _ = conv(coords[perm], x[perm])
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y0[torch.from_numpy(perm).to(dev)])
+    rows = _sample_rows(n, 256, seed=78)
+    sub = row_subset(m0.token_major.cpu().numpy(), n, rows)
+    if case == "f32":
+        ref = orc.sparse_conv(x, w, b, sub, ntaps=27, n_out=len(rows), idx_layout=1,
+                              out_dtype=oracle.F32)
+        got = y0.cpu().numpy()[rows]
+        assert np.all(np.abs(got - ref) <= F32_ATOL + F32_RTOL * np.abs(ref))
+    else:
+        ref = orc.sparse_conv(x, w, b, sub, ntaps=27, n_out=len(rows), idx_layout=1,
+                              out_dtype=oracle.F32, x_dtype=oracle.BF16,
+                              w_dtype=oracle.F16 if case == "q8_0" else oracle.BF16,
+                              b_dtype=oracle.BF16)
+        assert max_rel(from_dev(y0)[rows], ref) <= MAXREL
