@@ -45,8 +45,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5, 6, 7, 8],
-                    help="2 = the headline workload; others print diagnostic lines")
+    ap.add_argument("--config", type=int, default=2, choices=[0, 1, 2, 3, 4, 5, 6, 7, 8, 9],
+                    help="2 = the headline workload; others print diagnostic lines (0 = one "
+                         "sphere shell, N = 21,766, bf16 C = 128; 9 = feature ops' HBM GB/s)")
     ap.add_argument("--order", choices=["natural", "mask"], default="natural",
                     help="row processing order of the conv kernel")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -185,7 +186,7 @@ def cpu_baseline(orc, x_bits, w_bits, b_bits, tm, coords, n, cin, cout, target_s
     t_all = median_of(5, lambda: run(rows, threads))
     t1 = run(64, 1)
     rows1 = int(min(n, max(64, 64 * (target_s / 10) / max(t1, 1e-6))))
-    t_one = median_of(3, lambda: run(rows1, 1))
+    t_one = median_of(5, lambda: run(rows1, 1))
 
     def build_map():
         t0 = time.perf_counter()
@@ -201,7 +202,7 @@ def cpu_baseline(orc, x_bits, w_bits, b_bits, tm, coords, n, cin, cout, target_s
                   f"partition), 1 warm-up + median of 5; host '{model}', {avail} CPUs "
                   "available",
         "single_thread": {"value": rows1 / t_one / 1e6, "unit": "Mvoxel/s", "cores": 1,
-                          "sample": f"first {rows1} rows, 1 thread, median of 3"},
+                          "sample": f"first {rows1} rows, 1 thread, 1 warm-up + median of 5"},
         "map_build_1thread_ms": {"value": t_map * 1e3, "cores": 1,
                                  "sample": f"std::map 27-offset table + stable mask argsort, "
                                            f"all {n} voxels, median of 5"},
@@ -254,6 +255,17 @@ def main():
         cin = cout = 128
         batch = 4
         workload = "subm3x3x3 bf16 C=128, 4 ellipsoid shells 64^3 (N=62,710)"
+    elif cfg == 0:
+        coords = wl.sphere_shell()
+        cin = cout = 128
+        batch = 1
+        workload = "subm3x3x3 bf16 C=128, one sphere shell r=24 in 64^3 (N=21,766)"
+    elif cfg == 9:
+        coords = wl.ellipsoid_batch()
+        cin = cout = 128
+        batch = 4
+        workload = ("feature ops of the SLAT IO blocks on the 4 ellipsoid shells (62,710 fine, "
+                    "11,774 coarse rows), bf16")
     elif cfg == 1:
         coords = wl.sphere_shell()
         cin = cout = 64
@@ -325,7 +337,7 @@ def main():
     map_bytes = 16 * n + 108 * n + 8 * n
 
     result = {}
-    if cfg in (2, 1, 5):
+    if cfg in (2, 0, 1, 5):
         torch.manual_seed(0)
         xf = wl.normal((n, cin), 1.0, seed=101)
         wf = wl.normal((cout, 27, cin), 0.02, seed=102)
@@ -350,7 +362,7 @@ def main():
             cpu_dt = (oracle.F32, oracle.F32)
             w_bytes = wf.nbytes
             es = 4
-        elif cfg == 2:
+        elif cfg in (2, 0):
             x, xb = bf16_dev(orc, xf, dev)
             w, wb = bf16_dev(orc, wf, dev)
             b, bb = bf16_dev(orc, bf, dev)
@@ -380,7 +392,8 @@ def main():
         tflops = flops / t / 1e12
         comp_bytes = n * cin * es + n * cout * es + w_bytes + 108 * n
         traffic = traffic_from_profile({2: "conv_bf16_ellipsoids4_c128", 1: "conv_f32_sphere_c64",
-                                        5: "conv_q8_0_sphere_c768"}[cfg])
+                                        5: "conv_q8_0_sphere_c768",
+                                        0: "conv_bf16_sphere64_c128"}[cfg])
         result = {
             "metric": METRIC if cfg == 2 else f"config {cfg}: {workload}",
             "value": n / t / 1e6, "unit": "Mvoxel/s", "n_gpus": 1, "steps": args.steps,
@@ -401,6 +414,8 @@ def main():
                          "kernel": "conv_kernel (gather -> MFMA implicit GEMM -> store)",
                          "algorithmic_flops_per_launch": flops},
         }
+        if cfg == 2:
+            result["single_shell"] = bench_single_shell(nat, wl, orc, dev, args)
         if dtype == "bf16":
             g = library_gemm_tflops(dev, torch.bfloat16)
             g["conv_fraction"] = tflops / g["tflops"]
@@ -446,6 +461,8 @@ def main():
                   "pct_peak_subm1024": 100 * f3 / (ms3 / 1e3) / 1e12 / PEAK_BF16_TFLOPS}
     elif cfg == 6:
         result = bench_res_block(spc, nat, wl, orc, coords, c_dev, dev, args, workload)
+    elif cfg == 9:
+        result = bench_feature_ops(spc, nat, wl, orc, coords, c_dev, dev, args, workload)
     elif cfg in (7, 8):
         result = bench_subdivide_block(spc, nat, wl, orc, coords, c_dev, dev, args, workload,
                                        cin, cout, res=64 if cfg == 7 else 128)
@@ -473,6 +490,98 @@ def main():
             cc = oc
         result = {"metric": f"config 4: {workload}", "levels": lv, "dtype": "bf16"}
     print(json.dumps(result))
+
+
+def bench_single_shell(nat, wl, orc, dev, args) -> dict:
+    """The metric's named shape beside the batch: one 64^3 sphere shell
+    (N = 21,766, 453,614 pairs), bf16 C = 128 -> 128, map and tile plan
+    built once, the conv timed like the headline step."""
+    import torch
+
+    coords = wl.sphere_shell()
+    n = coords.shape[0]
+    m = nat.map_build(torch.from_numpy(coords).to(dev))
+    pairs = m.pairs
+    x, _ = bf16_dev(orc, wl.normal((n, 128), 1.0, seed=111), dev)
+    w, _ = bf16_dev(orc, wl.normal((128, 27, 128), 0.02, seed=112), dev)
+    b, _ = bf16_dev(orc, wl.normal((128,), 0.01, seed=113), dev)
+    y = torch.empty((n, 128), dtype=torch.bfloat16, device=dev)
+    call = ConvCall(nat, x, nat.pack_weights(w), b, y, m.token_major, ntaps=27, n_out=n,
+                    layout=nat.IDX_TOKEN_MAJOR, plan=m.plan())
+    ms, _ = time_gpu(call, args.steps, args.warmup)
+    tf = 2.0 * pairs * 128 * 128 / (ms / 1e3) / 1e12
+    return {"workload": "subm3x3x3 bf16 C=128, one sphere shell r=24 in 64^3", "n_voxels": n,
+            "pairs": pairs, "ms": ms, "mvoxel_s": n / (ms / 1e3) / 1e6, "tflops": tf,
+            "pct_peak": 100.0 * tf / PEAK_BF16_TFLOPS}
+
+
+def bench_feature_ops(spc, nat, wl, orc, coords, c_dev, dev, args, workload) -> dict:
+    """HBM rates of the non-GEMM kernels of the SLAT IO blocks on the config-2
+    rows (bf16): the scatter-mean downsample (fine -> coarse), the upsample
+    gather (coarse -> fine), LayerNorm + SiLU, LayerNorm + modulation + SiLU
+    and the GroupNorm pair.  Algorithmic bytes per launch: every input row
+    read once and every output row written once (plus 4-byte row indices
+    and counts); GB/s = bytes / kernel time."""
+    import ctypes
+
+    import torch
+
+    n = coords.shape[0]
+    d = nat.downsample_map(c_dev, 4, 64)
+    nc = d.nc
+    L = nat.lib()
+    s = torch.cuda.current_stream().cuda_stream
+    BF = nat.BF16
+    p = lambda t: t.data_ptr()  # noqa: E731
+    out = []
+
+    def rec(name, fn, c_args, nbytes, **kw):
+        def call():
+            st = fn(*c_args)
+            if st != 0:
+                nat._check(name, st)
+        ms, _ = time_gpu(call, args.steps, args.warmup)
+        out.append({"op": name, "ms": ms, "bytes": nbytes, "gbs": nbytes / (ms / 1e3) / 1e9,
+                    "pct_hbm": 100.0 * nbytes / (ms / 1e3) / 1e9 / PEAK_HBM_GBS, **kw})
+
+    ws = torch.empty(L.spc_scatter_mean_workspace_bytes(n, nc), dtype=torch.uint8, device=dev)
+    f2c, cnt = d.fine_to_coarse.contiguous(), d.counts.contiguous()
+    keep = []
+    for c in (128, 1024):
+        xf, _ = bf16_dev(orc, wl.normal((n, c), 1.0, seed=900 + c), dev)
+        xc, _ = bf16_dev(orc, wl.normal((nc, c), 1.0, seed=901 + c), dev)
+        yc = torch.empty((nc, c), dtype=torch.bfloat16, device=dev)
+        yf = torch.empty((n, c), dtype=torch.bfloat16, device=dev)
+        sc = torch.randn(4, c, device=dev).bfloat16().float()
+        keep += [xf, xc, yc, yf, sc]
+        rec(f"scatter_mean {n}->{nc} C={c}", L.spc_scatter_mean,
+            (s, BF, p(xf), p(f2c), p(cnt), p(yc), c, n, nc, p(ws), ws.numel()),
+            n * c * 2 + nc * c * 2 + 4 * n + 4 * nc, rows_in=n, rows_out=nc, channels=c)
+        rec(f"gather (upsample) {nc}->{n} C={c}", L.spc_gather_rows,
+            (s, BF, p(xc), p(f2c), p(yf), n, nc, c), nc * c * 2 + n * c * 2 + 4 * n,
+            rows_in=nc, rows_out=n, channels=c)
+        rec(f"layernorm_silu N={n} C={c}", L.spc_layernorm_silu,
+            (s, BF, p(xf), n, c, None, None, ctypes.c_float(1e-6), 1, p(yf)), 2 * n * c * 2,
+            rows=n, channels=c)
+        rec(f"layernorm_mod_silu N={n} C={c}", L.spc_layernorm_mod_silu,
+            (s, BF, p(xf), n, c, ctypes.c_float(1e-6), p(sc), p(sc), p(c_dev), 4, p(yf)),
+            2 * n * c * 2 + 4 * n * 4, rows=n, channels=c)
+    xg, _ = bf16_dev(orc, wl.normal((n, 768), 1.0, seed=990), dev)
+    yg = torch.empty_like(xg)
+    offs = spc.sparse.batch_offsets(spc.sparse.SparseTensor(xg, c_dev)).contiguous()
+    rows_max = int((offs[1:] - offs[:-1]).max().item())
+    stt = torch.empty((4, 32, 2), dtype=torch.float32, device=dev)
+    gws = torch.empty(max(8, L.spc_group_norm_workspace_bytes(4, rows_max, 32)),
+                      dtype=torch.uint8, device=dev)
+    rec(f"group_norm_stats N={n} C=768", L.spc_group_norm_stats,
+        (s, BF, p(xg), 768, 32, p(offs), 4, rows_max, ctypes.c_float(1e-5), p(stt), p(gws),
+         gws.numel()), n * 768 * 2, rows=n, channels=768)
+    rec(f"group_norm_silu N={n} C=768", L.spc_group_norm_silu,
+        (s, BF, p(xg), n, 768, 32, p(offs), 4, p(stt), None, None, 1, None, n, p(yg)),
+        2 * n * 768 * 2, rows=n, channels=768)
+    del keep
+    return {"metric": f"config 9: {workload}", "dtype": "bf16", "ops": out,
+            "config": {"workload": workload, "n_fine": n, "n_coarse": nc}}
 
 
 def bench_res_block(spc, nat, wl, orc, coords, c_dev, dev, args, workload):

@@ -12,8 +12,11 @@
  *
  * Conventions
  *   - Every buffer is caller-owned device memory (hipMalloc / torch).  The
- *     library allocates nothing; scratch space comes from a caller-owned
- *     workspace whose size the *_workspace_bytes queries return.
+ *     library allocates nothing at run time; scratch space comes from a
+ *     caller-owned workspace whose size the *_workspace_bytes queries
+ *     return.  The exceptions are static device arrays, one per device for
+ *     the life of the process: the spconv bridge's 64 MiB weight-pack buffer
+ *     (sam3d_spconv_f16_forward) -- documented at their entry points.
  *   - Calls are asynchronous on `stream` (a hipStream_t; 0 = null stream)
  *     unless documented as synchronising.  Calls on one stream are ordered;
  *     separate workspaces make calls on different streams independent.
@@ -273,8 +276,15 @@ int spc_conv_pack_weights(spc_stream_t stream, int w_dtype, int w_layout, const 
  * permutation of spc_map_build, accepted and not needed: rows run in
  * natural order, which keeps each tile's gathered rows spatially coherent
  * (the output is the same in any order).  Accumulates in F32 (the
- * reference kernel accumulates in f16).  Returns nothing, like the
- * reference; failures are reported through spc_last_error(). */
+ * reference kernel accumulates in f16).  channels and output_channels must
+ * be multiples of 32.  The KRSC weights are packed on every call into a
+ * library-owned 64 MiB device buffer (one per device, held until the
+ * process ends) and the packed conv runs on them: bridge calls on one device
+ * share that buffer, so calls on different streams of one device must not
+ * overlap (the reference's bridge, too, assumes one stream).  Weights
+ * larger than the buffer run unpacked (same results, slower).  Returns
+ * nothing, like the reference: spc_last_error() is cleared on entry and
+ * is non-empty after the call exactly when it failed (output unwritten). */
 void sam3d_spconv_f16_forward(spc_stream_t stream, const void* input, const void* weight,
                               const void* bias, void* output, const int32_t* indices,
                               const uint32_t* mask, const int32_t* mask_argsort, int64_t tokens,
@@ -334,6 +344,19 @@ int spc_gather_rows(spc_stream_t stream, int dtype, const void* src, const int32
 int spc_layernorm_silu(spc_stream_t stream, int dtype, const void* x, int64_t n, int64_t c,
                        const float* gamma, const float* beta, float eps, int silu, void* y);
 
+/* The block's second activation over rows of any width c <= 2048 (a
+ * multiple of 4): u = dt(LayerNorm(x; eps)) without affine (norm2),
+ * m = dt(dt(u * dt(1 + scale[b])) + shift[b]), y = dt(silu(m)), b =
+ * coords[4 t] the row's batch (clamped to [0, n_batch)) -- the
+ * `norm2(h) * (1 + scale) + shift` and F.silu of structured_latent_flow.py:
+ * 70-71 (SRC/slat_flow_graph.cpp:350-355) in one read and one write of the
+ * rows.  scale / shift f32 [n_batch, c] holding dtype values, 16-byte
+ * aligned.  y may be x.  The conv epilogue SPC_EPI_NORM_MOD_SILU computes
+ * the same for cout 32, 64 and 128 without the extra pass. */
+int spc_layernorm_mod_silu(spc_stream_t stream, int dtype, const void* x, int64_t n, int64_t c,
+                           float eps, const float* scale, const float* shift,
+                           const int32_t* coords, int64_t n_batch, void* y);
+
 /* GroupNorm over each batch item's rows (SparseGroupNorm32,
  * modules/sparse/norm.py:15-55: per item, the statistics of each group of
  * c / groups channels over all of the item's rows; biased variance, eps
@@ -373,7 +396,8 @@ int spc_group_norm_silu(spc_stream_t stream, int dtype, const void* x, int64_t n
  * nothing): the subdivide block adds its skip computed on the parent rows
  * (decoder_mesh.py:82).  scale / shift: f32 [n_batch, cout]
  * holding dtype values (emb_out.type(x.dtype)).  NORM_MOD_SILU needs
- * cout <= 128 (one tile covers a whole output row). */
+ * cout 32, 64 or 128 (one tile covers a whole output row); other widths
+ * run the conv and then spc_layernorm_mod_silu. */
 typedef enum { SPC_EPI_NONE = 0, SPC_EPI_RESIDUAL = 1, SPC_EPI_NORM_MOD_SILU = 2 } spc_epilogue_mode;
 typedef struct {
     int32_t mode;

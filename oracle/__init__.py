@@ -75,6 +75,7 @@ class _Oracle:
         lib.orc_subdivide.restype = _I64
         lib.orc_sparse_conv.argtypes = [_INT, _P, _INT, _P, _INT, _INT, _P, _INT, _P, _P, _INT,
                                         _I64, _I64, _I64, _I64, _I64, _INT]
+        lib.orc_sparse_conv_blocked.argtypes = lib.orc_sparse_conv.argtypes
         lib.orc_scatter_mean.argtypes = [_INT, _P, _P, _P, _P, _I64, _I64, _I64, _INT]
         lib.orc_q8_0_quantize.argtypes = [_P, _I64, _P]
         lib.orc_q8_0_dequant.argtypes = [_P, _I64, _INT, _P]
@@ -146,9 +147,12 @@ class _Oracle:
     # -- feature ops ----------------------------------------------------------
     def sparse_conv(self, x, w, bias, idx, *, ntaps: int, n_out: int, idx_layout: int,
                     out_dtype: int, x_dtype: int | None = None, w_dtype: int | None = None,
-                    b_dtype: int | None = None, w_layout: int = 0, nthreads: int = 1):
+                    b_dtype: int | None = None, w_layout: int = 0, nthreads: int = 1,
+                    blocked: bool = False):
         """F32-accumulate sparse conv (the ggml CPU op). Returns a numpy array
-        of float32 (out_dtype F32), float16 (F16) or uint16 bf16 bits (BF16)."""
+        of float32 (out_dtype F32), float16 (F16) or uint16 bf16 bits (BF16).
+        blocked: the vectorised restatement (bit-identical results; the
+        scalar loop is the one timed as the CPU baseline)."""
         x = np.ascontiguousarray(x)
         w = np.ascontiguousarray(w)
         idx = np.ascontiguousarray(idx, dtype=np.int32)
@@ -162,10 +166,10 @@ class _Oracle:
             bias = np.ascontiguousarray(bias)
             bptr = _ptr(bias)
             bcode = _dtype_code(bias, b_dtype)
-        st = self.lib.orc_sparse_conv(_dtype_code(x, x_dtype), _ptr(x), _dtype_code(w, w_dtype),
-                                      _ptr(w), w_layout, bcode, bptr, out_dtype, _ptr(y),
-                                      _ptr(idx), idx_layout, ntaps, n_out, n_in, cin, cout,
-                                      nthreads)
+        fn = self.lib.orc_sparse_conv_blocked if blocked else self.lib.orc_sparse_conv
+        st = fn(_dtype_code(x, x_dtype), _ptr(x), _dtype_code(w, w_dtype), _ptr(w), w_layout,
+                bcode, bptr, out_dtype, _ptr(y), _ptr(idx), idx_layout, ntaps, n_out, n_in, cin,
+                cout, nthreads)
         if st != OK:
             raise ValueError(f"orc_sparse_conv status {st}")
         return y
@@ -336,10 +340,12 @@ def silu(a: np.ndarray) -> np.ndarray:
 
 
 def res_block(o: "_Oracle", x: np.ndarray, table: np.ndarray, p: dict, scale: np.ndarray,
-              shift: np.ndarray, batch: np.ndarray, dtype: int = BF16) -> np.ndarray:
-    """SparseResBlock3d.forward without up/down sampling
-    (structured_latent_flow.py:61-74), every intermediate rounded to the
-    feature dtype where the reference's tensors are:
+              shift: np.ndarray, batch: np.ndarray, dtype: int = BF16,
+              nthreads: int = 1) -> np.ndarray:
+    """SparseResBlock3d.forward after its up/down sampling
+    (structured_latent_flow.py:61-74; io_res_block adds the sampling), every
+    intermediate rounded to the feature dtype where the reference's tensors
+    are:
         h = dt(silu(dt(LN(x) * g + b)));  h = dt(conv1(h))
         h = dt(silu(dt(dt(dt(LN(h)) * dt(1 + scale)) + shift)))
         out = dt(dt(conv2(h)) + skip(x)),  skip = x or dt(x W^T + b).
@@ -353,7 +359,8 @@ def res_block(o: "_Oracle", x: np.ndarray, table: np.ndarray, p: dict, scale: np
     def conv(h, w, b):
         bits = {F32: lambda a: a, BF16: o.f32_to_bf16, F16: o.f32_to_f16}[dtype]
         y = o.sparse_conv(bits(h), bits(w), bits(b), table, ntaps=27, n_out=n, idx_layout=1,
-                          out_dtype=F32, x_dtype=dtype, w_dtype=dtype, b_dtype=dtype)
+                          out_dtype=F32, x_dtype=dtype, w_dtype=dtype, b_dtype=dtype,
+                          nthreads=nthreads, blocked=True)
         return r(y)
 
     h = r(silu(r(layernorm(x, p["norm1_w"], p["norm1_b"]))))
@@ -364,6 +371,48 @@ def res_block(o: "_Oracle", x: np.ndarray, table: np.ndarray, p: dict, scale: np
     h = conv(h, p["conv2_w"], p["conv2_b"])
     skip = x if "skip_w" not in p else r(x @ p["skip_w"].T.astype(np.float32) + p["skip_b"])
     return r(h + skip)
+
+
+def io_res_block(o: "_Oracle", x: np.ndarray, coords: np.ndarray, p: dict, scale: np.ndarray,
+                 shift: np.ndarray, dtype: int = BF16, mode: str | None = None,
+                 fine_coords: np.ndarray | None = None, nthreads: int = 1):
+    """SparseResBlock3d.forward with its sampling step (structured_latent_
+    flow.py:61-65; the SLAT IO blocks built at :140-200, native graph
+    SRC/slat_flow_graph.cpp:286-380, 395-396), then res_block:
+      mode None    x on `coords`;
+      mode "down"  x on the fine `coords` -> SparseDownsample(2): coarse rows
+                   in lexicographic (b, x/2, y/2, z/2) order, each the mean
+                   of its children with the sum kept in the dtype and
+                   divided by |children| + 1 (orc_downsample_map +
+                   orc_scatter_mean: the reference's scatter-mean op,
+                   PATCH:151-215; SP/spatial.py:20-65);
+      mode "up"    x on the coarse rows of `fine_coords`' downsample ->
+                   SparseUpsample(2): fine row i takes coarse row
+                   fine_to_coarse[i] (SP/spatial.py:75-105).
+    Returns (output coords, output features)."""
+    if mode == "down":
+        d = o.downsample_map(coords)
+        bits = {F32: lambda a: np.ascontiguousarray(a, np.float32), BF16: o.f32_to_bf16,
+                F16: o.f32_to_f16}[dtype]
+        xs = o.scatter_mean(bits(x), d["fine_to_coarse"], d["counts"], d["nc"], dtype=dtype,
+                            nthreads=nthreads)
+        if dtype == BF16:
+            x = (xs.astype(np.uint32) << 16).view(np.float32)
+        elif dtype == F16:
+            x = xs.view(np.float16).astype(np.float32)
+        else:
+            x = xs
+        coords = d["coarse_coords"]
+    elif mode == "up":
+        d = o.downsample_map(fine_coords)
+        assert np.array_equal(d["coarse_coords"], coords), "x must sit on fine_coords' coarse rows"
+        x = x[d["fine_to_coarse"]]
+        coords = fine_coords
+    elif mode is not None:
+        raise ValueError(f"unknown mode {mode}")
+    table = o.conv_table_slat(coords)
+    out = res_block(o, x, table, p, scale, shift, coords[:, 0].astype(np.int64), dtype, nthreads)
+    return coords, out
 
 
 def batch_offsets(batch: np.ndarray, n_batch: int | None = None) -> np.ndarray:

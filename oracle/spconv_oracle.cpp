@@ -21,6 +21,9 @@
 //   orc_sparse_conv
 //       -> closed forms (identity kernel, single-tap shift, linearity) and a
 //          dense torch conv3d brute force on small grids (tests/).
+//   orc_sparse_conv_blocked
+//       -> bit-identical to orc_sparse_conv on random problems of every
+//          dtype, layout and tap count (tests/test_oracle_conv.py).
 //   orc_stride2_taps
 //       -> dense torch conv3d(stride=2) brute force on small grids.
 //   orc_scatter_mean
@@ -215,6 +218,74 @@ void conv_rows_dispatch(int x_dtype, int w_dtype, const ConvProblem& p, int64_t 
         case ORC_BF16: conv_rows_w<LoadBF16>(w_dtype, p, b, e); break;
         default: conv_rows_w<LoadF32>(w_dtype, p, b, e); break;
     }
+}
+
+// The same conv with the loops reordered for speed: blocks of kRowBlock
+// output rows x kOutBlock output channels, weights pre-converted to F32 in
+// [tap][cin][cout] order.  Every output element still sees exactly the
+// scalar loop's operations in the same order -- acc = bias, then for taps
+// ascending (valid ones) and channels ascending acc = acc + w * x, the
+// product and the sum each rounded to F32 (-ffp-contract=off keeps them
+// separate) -- so the results are bit-identical to conv_rows; only
+// independent elements are interleaved, which lets the compiler vectorise
+// across output channels.
+constexpr int64_t kRowBlock = 32;
+constexpr int64_t kOutBlock = 256;
+
+template <typename LX>
+void conv_rows_blocked(const ConvProblem& p, const float* wt, int64_t begin, int64_t end) {
+    const auto* x = static_cast<const typename LX::T*>(p.x);
+    const int64_t C = p.channels, Co = p.out_channels;
+    std::vector<float> acc((size_t)(kRowBlock * kOutBlock));
+    int64_t rows[kRowBlock];
+    const typename LX::T* src[kRowBlock];
+    for (int64_t t0 = begin; t0 < end; t0 += kRowBlock) {
+        const int64_t rb = std::min(kRowBlock, end - t0);
+        for (int64_t o0 = 0; o0 < Co; o0 += kOutBlock) {
+            const int64_t ob = std::min(kOutBlock, Co - o0);
+            for (int64_t r = 0; r < rb; ++r)
+                for (int64_t j = 0; j < ob; ++j)
+                    acc[(size_t)(r * kOutBlock + j)] =
+                        p.bias ? load_as_f32(p.b_dtype, p.bias, o0 + j) : 0.0f;
+            for (int64_t o = 0; o < p.ntaps; ++o) {
+                int64_t nv = 0;
+                for (int64_t r = 0; r < rb; ++r) {
+                    const int64_t t = t0 + r;
+                    const int32_t s = p.idx_layout == 0 ? p.idx[o * p.n_out + t] : p.idx[t * p.ntaps + o];
+                    if (s < 0 || s >= p.n_in) continue;
+                    rows[nv] = r;
+                    src[nv] = x + (int64_t)s * C;
+                    ++nv;
+                }
+                if (nv == 0) continue;
+                const float* wo = wt + (size_t)(o * C * Co + o0);
+                for (int64_t c = 0; c < C; ++c) {
+                    const float* __restrict__ wc = wo + (size_t)(c * Co);
+                    for (int64_t k = 0; k < nv; ++k) {
+                        const float xv = LX::f(src[k][c]);
+                        float* __restrict__ a = acc.data() + rows[k] * kOutBlock;
+                        for (int64_t j = 0; j < ob; ++j) a[j] = a[j] + wc[j] * xv;
+                    }
+                }
+            }
+            for (int64_t r = 0; r < rb; ++r)
+                for (int64_t j = 0; j < ob; ++j)
+                    store_from_f32(p.y_dtype, p.y, (t0 + r) * Co + o0 + j,
+                                   acc[(size_t)(r * kOutBlock + j)]);
+        }
+    }
+}
+
+// Weights as F32 [tap][cin][cout] (exact conversions from any storage dtype).
+template <typename LW>
+void transpose_weights(const ConvProblem& p, float* wt) {
+    const auto* w = static_cast<const typename LW::T*>(p.w);
+    const int64_t C = p.channels, Co = p.out_channels;
+    for (int64_t co = 0; co < Co; ++co)
+        for (int64_t o = 0; o < p.ntaps; ++o) {
+            const int64_t wbase = p.w_layout == 0 ? (co * p.ntaps + o) * C : (o * Co + co) * C;
+            for (int64_t c = 0; c < C; ++c) wt[(size_t)((o * C + c) * Co + co)] = LW::f(w[wbase + c]);
+        }
 }
 
 }  // namespace
@@ -420,6 +491,38 @@ int orc_sparse_conv(int x_dtype, const void* x, int w_dtype, const void* w, int 
         const int64_t begin = std::min(n_out, (int64_t)ith * per);
         const int64_t end = std::min(n_out, begin + per);
         conv_rows_dispatch(x_dtype, w_dtype, p, begin, end);
+    };
+    run_partitioned(n_out, nthreads, body);
+    return ORC_OK;
+}
+
+// orc_sparse_conv with blocked, vectorisable loops: same arguments, results
+// bit-identical to orc_sparse_conv (see conv_rows_blocked; pinned by
+// tests/test_oracle_conv.py), fast enough to check every output row of the
+// wide (C = 768 / 1024) convs.
+int orc_sparse_conv_blocked(int x_dtype, const void* x, int w_dtype, const void* w, int w_layout,
+                            int b_dtype, const void* bias, int y_dtype, void* y,
+                            const int32_t* idx, int idx_layout, int64_t ntaps, int64_t n_out,
+                            int64_t n_in, int64_t channels, int64_t out_channels, int nthreads) {
+    if (ntaps <= 0 || n_out < 0 || n_in < 0 || channels <= 0 || out_channels <= 0)
+        return ORC_BAD_SHAPE;
+    ConvProblem p{x, w, w_layout, b_dtype, bias, y_dtype, y, idx, idx_layout, ntaps, n_out,
+                  n_in, channels, out_channels};
+    std::vector<float> wt((size_t)(ntaps * channels * out_channels));
+    switch (w_dtype) {
+        case ORC_F16: transpose_weights<LoadF16>(p, wt.data()); break;
+        case ORC_BF16: transpose_weights<LoadBF16>(p, wt.data()); break;
+        default: transpose_weights<LoadF32>(p, wt.data()); break;
+    }
+    auto body = [&](int ith, int nth) {
+        const int64_t per = (n_out + nth - 1) / nth;
+        const int64_t begin = std::min(n_out, (int64_t)ith * per);
+        const int64_t end = std::min(n_out, begin + per);
+        switch (x_dtype) {
+            case ORC_F16: conv_rows_blocked<LoadF16>(p, wt.data(), begin, end); break;
+            case ORC_BF16: conv_rows_blocked<LoadBF16>(p, wt.data(), begin, end); break;
+            default: conv_rows_blocked<LoadF32>(p, wt.data(), begin, end); break;
+        }
     };
     run_partitioned(n_out, nthreads, body);
     return ORC_OK;

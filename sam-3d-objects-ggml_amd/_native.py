@@ -94,6 +94,8 @@ def lib() -> ctypes.CDLL:
     L.spc_scatter_mean.argtypes = [_P, _INT, _P, _P, _P, _P, _I64, _I64, _I64, _P, _SZ]
     L.spc_gather_rows.argtypes = [_P, _INT, _P, _P, _P, _I64, _I64, _I64]
     L.spc_layernorm_silu.argtypes = [_P, _INT, _P, _I64, _I64, _P, _P, ctypes.c_float, _INT, _P]
+    L.spc_layernorm_mod_silu.argtypes = [_P, _INT, _P, _I64, _I64, ctypes.c_float, _P, _P, _P,
+                                         _I64, _P]
     L.spc_group_norm_workspace_bytes.restype = _SZ
     L.spc_group_norm_workspace_bytes.argtypes = [_I64, _I64, _I64]
     L.spc_group_norm_stats.argtypes = [_P, _INT, _P, _I64, _I64, _P, _I64, _I64, ctypes.c_float,
@@ -529,6 +531,31 @@ def layernorm_silu(x: torch.Tensor, weight: torch.Tensor | None = None,
     st = lib().spc_layernorm_silu(_stream(x.device), dtype_code(x.dtype), _ptr(x), n, c, _ptr(w),
                                   _ptr(b), float(eps), int(bool(silu)), _ptr(out))
     _check("spc_layernorm_silu", st)
+    return out
+
+
+def layernorm_mod_silu(x: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor,
+                       coords: torch.Tensor, eps: float = 1e-6,
+                       out: torch.Tensor | None = None) -> torch.Tensor:
+    """silu(LayerNorm32(x) * (1 + scale[b]) + shift[b]) over the rows of x
+    [n, c], b = coords[:, 0] (spc_layernorm_mod_silu); scale / shift
+    [n_batch, c] holding feature-dtype values."""
+    _need_gpu(x, scale, shift, coords)
+    x = x.contiguous()
+    n, c = x.shape
+    scale = scale.to(torch.float32).contiguous()
+    shift = shift.to(torch.float32).contiguous()
+    coords = coords.contiguous()
+    if scale.shape != shift.shape or scale.dim() != 2 or scale.shape[1] != c:
+        raise ValueError("scale / shift must be [n_batch, c]")
+    if coords.dtype != torch.int32 or coords.shape != (n, 4):
+        raise ValueError("coords must be int32 [n, 4]")
+    if out is None:
+        out = torch.empty_like(x)
+    st = lib().spc_layernorm_mod_silu(_stream(x.device), dtype_code(x.dtype), _ptr(x), n, c,
+                                      float(eps), _ptr(scale), _ptr(shift), _ptr(coords),
+                                      scale.shape[0], _ptr(out))
+    _check("spc_layernorm_mod_silu", st)
     return out
 
 

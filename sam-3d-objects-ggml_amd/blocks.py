@@ -11,8 +11,9 @@ structured_latent_flow.py:15-74; native graph SRC/slat_flow_graph.cpp:
 
 with (scale, shift) = chunk(emb_layers(emb)).  Here it runs as three
 kernels: spc_layernorm_silu (norm1 + SiLU), conv1 with the norm2 /
-modulation / SiLU epilogue (whole output rows in one tile, Cout <= 128) and
-conv2 with the residual epilogue.  Every intermediate is rounded to the
+modulation / SiLU epilogue (whole output rows in one tile: Cout 32, 64 or
+128; other widths run conv1 and then one spc_layernorm_mod_silu row pass)
+and conv2 with the residual epilogue.  Every intermediate is rounded to the
 feature dtype where the reference's tensors are (LayerNorm32 casts back,
 bf16 / f16 elementwise ops round per op).  Parameters and state-dict keys
 are the reference's.
@@ -94,14 +95,16 @@ class SparseResBlock3d(nn.Module):
         x = self._updown(x)
         h = x.replace(nat.layernorm_silu(x.feats, self.norm1.weight, self.norm1.bias,
                                          eps=self.norm1.eps))
-        if self.out_channels <= 128 and self.out_channels % 32 == 0:
+        if self.out_channels in (32, 64, 128):
+            # one conv tile holds whole output rows: norm2 / modulation / SiLU
+            # in the conv's epilogue
             h = self.conv1.forward_fused(h, norm_mod=(scale.float(), shift.float(),
                                                       self.norm2.eps))
         else:
+            # wider rows: the conv, then one row pass for norm2 / modulation / SiLU
             h = self.conv1(h)
-            h = h.replace(nat.layernorm_silu(h.feats, eps=self.norm2.eps, silu=False))
-            h = h * (1 + scale) + shift
-            h = h.replace(torch.nn.functional.silu(h.feats))
+            h = h.replace(nat.layernorm_mod_silu(h.feats, scale.float(), shift.float(), h.coords,
+                                                 eps=self.norm2.eps))
         skip = self.skip_connection(x)
         if self.out_channels % 32 == 0:
             return self.conv2.forward_fused(h, residual=skip.feats)

@@ -150,6 +150,7 @@ struct Sizer {
 constexpr int kStatusBytes = 256;
 
 void set_last_error(const char* fmt, ...);
+void clear_last_error();
 int hip_status(hipError_t e, const char* what);
 
 // Shared device utilities (maps.hip / sort.hip).

@@ -168,6 +168,32 @@ int device_cu_count() {
     return n;
 }
 
+// Packed f16 weights of the spconv bridge: the largest pack it holds is
+// 64 MiB (27 x 1024 x 1184 f16 weights; the SLAT IO convs need 27 x 1024 x
+// 1024).  One buffer per device, held until the process ends; bridge calls
+// on one device share it, so they must not overlap (one stream, as the
+// reference's bridge assumes).
+constexpr size_t kBridgePackBytes = (size_t)64 << 20;
+__device__ __attribute__((aligned(256))) uint8_t bridge_pack[kBridgePackBytes];
+
+// Device address of bridge_pack on the current device, looked up once per
+// device with that device current (the host-side symbol is a stand-in, not
+// a device address); null when the lookup fails.
+void* bridge_pack_addr() {
+    static std::atomic<void*> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    void* p = cache[dev].load(std::memory_order_acquire);
+    if (p == nullptr) {
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(bridge_pack)) != hipSuccess || p == nullptr) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        cache[dev].store(p, std::memory_order_release);
+    }
+    return p;
+}
+
 int check_shape(const char* fn, int64_t ntaps, int64_t cin, int64_t cout, bool any_taps = false) {
     const bool taps_ok = any_taps ? (ntaps >= 1 && ntaps <= 4096) : (ntaps == 27 || ntaps == 8 || ntaps == 1);
     if (!taps_ok || cin <= 0 || cout <= 0 || cin % 32 != 0 ||
@@ -335,7 +361,7 @@ int conv_entry(spc_stream_t stream, int dtype, const void* x, int w_dtype, int w
         set_last_error("spc_sparse_conv: idx may be NULL only for ntaps 1 with n_in == n_out");
         return SPC_BAD_ARG;
     }
-    if (!x || !w || !y || !aligned16(x) || !aligned16(w) ||
+    if (!x || !w || !y || !aligned16(x) || !aligned16(w) || !aligned16(y) ||
         (idx_layout != SPC_IDX_TOKEN_MAJOR && idx_layout != SPC_IDX_OFFSET_MAJOR) ||
         (w_layout != SPC_W_KRSC && w_layout != SPC_W_PACKED)) {
         set_last_error("spc_sparse_conv: null / misaligned pointer or bad layout enum");
@@ -393,9 +419,12 @@ int conv_entry(spc_stream_t stream, int dtype, const void* x, int w_dtype, int w
                 a.n_residual = epi->n_residual;
             }
         } else if (epi->mode == SPC_EPI_NORM_MOD_SILU) {
-            if (cout > 128) {
-                set_last_error("spc_sparse_conv_fused: the norm epilogue needs cout <= 128 (got %lld)",
-                               (long long)cout);
+            // one tile must hold whole output rows with a power-of-two lane
+            // group per row: widths 32, 64 and 128 (wider or other rows take
+            // spc_layernorm_mod_silu after the conv)
+            if (cout != 32 && cout != 64 && cout != 128) {
+                set_last_error("spc_sparse_conv_fused: the norm epilogue needs cout 32, 64 or 128 "
+                               "(got %lld)", (long long)cout);
                 return SPC_BAD_SHAPE;
             }
             if (!epi->scale || !epi->shift || !epi->coords || !aligned16(epi->scale) ||
@@ -478,6 +507,23 @@ void sam3d_spconv_f16_forward(spc_stream_t stream, const void* input, const void
     // every output row is computed the same way in any order
     (void)mask;
     (void)mask_argsort;
+    clear_last_error();  // spc_last_error() reports this call only
+    if (check_shape("sam3d_spconv_f16_forward", 27, channels, output_channels) != SPC_OK) return;
+    // The weights arrive in KRSC order on every call (the ggml shim passes
+    // its weight tensor).  Packed into the MFMA fragment order first, each
+    // B operand is one contiguous 1 KB load instead of 32 strided 32-byte
+    // pieces: one pack kernel (weight bytes read and written once) buys the
+    // packed conv.  Weights beyond the pack buffer run unpacked.
+    const size_t wbytes = spc_conv_packed_bytes(SPC_F16, 27, channels, output_channels);
+    void* pk = wbytes <= kBridgePackBytes ? bridge_pack_addr() : nullptr;
+    if (pk && spc_conv_pack_weights(stream, SPC_F16, SPC_W_KRSC, weight, nullptr, 27, channels,
+                                    output_channels, pk) == SPC_OK) {
+        spc_sparse_conv(stream, SPC_F16, input, SPC_F16, SPC_W_PACKED, pk, nullptr, bias, output,
+                        indices, SPC_IDX_OFFSET_MAJOR, nullptr, 27, tokens, tokens, channels,
+                        output_channels);
+        return;
+    }
+    clear_last_error();
     spc_sparse_conv(stream, SPC_F16, input, SPC_F16, SPC_W_KRSC, weight, nullptr, bias, output,
                     indices, SPC_IDX_OFFSET_MAJOR, nullptr, 27, tokens, tokens, channels,
                     output_channels);

@@ -1241,8 +1241,9 @@ hipError_t dispatch_tn(hipStream_t s, const ConvArgs& a) {
         }
     }
     if (a.epi_mode == SPC_EPI_NORM_MOD_SILU) {
-        if (a.cout > 128) return hipErrorInvalidValue;  // rows wider than one tile
-        tn = a.cout;                                    // one tile covers the row
+        // one tile covers the row; the epilogue's lane groups need 32, 64 or 128
+        if (a.cout != 32 && a.cout != 64 && a.cout != 128) return hipErrorInvalidValue;
+        tn = a.cout;
     }
     // widths 128 does not divide but 192 does (the mesh decoder's 768 / 4):
     // one 192-column tile of 4 waves (2 x 2, 128x96 wave tiles, one per

@@ -68,6 +68,17 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// Per-batch modulation after the norm (SparseResBlock3d's `norm2(h) * (1 +
+// scale) + shift`, structured_latent_flow.py:70): scale / shift f32
+// [n_batch, c] holding feature-dtype values, the row's batch b = coords[4 t]
+// (clamped to [0, n_batch)).
+struct NormMod {
+    const float* scale;
+    const float* shift;
+    const int32_t* coords;
+    int64_t n_batch;
+};
+
 // G lanes per row, NV runs of 4 per lane (c <= 4 * G * NV), R rows per lane
 // group (rows r, r + groups, ...: R independent reductions in flight)
 template <int DT, int G, int NV, int R>
@@ -75,7 +86,7 @@ __global__ __launch_bounds__(256) void layernorm_silu_kernel(const void* __restr
                                                              int c, const float* __restrict__ gamma,
                                                              const float* __restrict__ beta,
                                                              float eps, int silu,
-                                                             void* __restrict__ y) {
+                                                             void* __restrict__ y, NormMod mod) {
     using E = Elem<DT>;
     const int lane = threadIdx.x & 63;
     constexpr int GPB = 256 / G;  // row groups per block
@@ -138,17 +149,31 @@ __global__ __launch_bounds__(256) void layernorm_silu_kernel(const void* __restr
         const int64_t row = row0 + (int64_t)r * GPB;
         if (row >= n) continue;
         const float rstd = 1.0f / sqrtf(q[r] / (float)c + eps);
+        const float* msc = nullptr;
+        const float* msh = nullptr;
+        if (mod.scale) {
+            const int64_t b = min(max((int64_t)mod.coords[row * 4], (int64_t)0), mod.n_batch - 1);
+            msc = mod.scale + b * c;
+            msh = mod.shift + b * c;
+        }
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
             const int c0 = 4 * (gl + G * k);
             if (c0 >= c) continue;
             float o[4];
+            floatx4 sc4 = {0.f, 0.f, 0.f, 0.f}, sh4 = {0.f, 0.f, 0.f, 0.f};
+            if (msc) {
+                sc4 = *reinterpret_cast<const floatx4*>(msc + c0);
+                sh4 = *reinterpret_cast<const floatx4*>(msh + c0);
+            }
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 float u = v[r][k][e] * rstd;
                 if (gamma) u *= gv[k][e];
                 if (beta) u += bv[k][e];
                 u = E::round(u);  // LayerNorm32 casts back to the feature dtype
+                if (msc)          // * (1 + scale) + shift, each op rounded to the dtype
+                    u = E::round(E::round(u * E::round(1.0f + sc4[e])) + sh4[e]);
                 if (silu) u = silu_f32(u);
                 o[e] = u;
             }
@@ -159,31 +184,32 @@ __global__ __launch_bounds__(256) void layernorm_silu_kernel(const void* __restr
 
 template <int DT, int G, int NV, int R>
 void launch_g(hipStream_t s, const void* x, int64_t n, int c, const float* gamma, const float* beta,
-              float eps, int silu, void* y) {
+              float eps, int silu, void* y, const NormMod& mod) {
     const dim3 grid((unsigned)ceil_div(n, (int64_t)(256 / G) * R));
-    layernorm_silu_kernel<DT, G, NV, R><<<grid, dim3(256), 0, s>>>(x, n, c, gamma, beta, eps, silu, y);
+    layernorm_silu_kernel<DT, G, NV, R><<<grid, dim3(256), 0, s>>>(x, n, c, gamma, beta, eps, silu,
+                                                                   y, mod);
 }
 
 template <int DT>
 hipError_t launch_norm(hipStream_t s, const void* x, int64_t n, int c, const float* gamma,
-                       const float* beta, float eps, int silu, void* y) {
+                       const float* beta, float eps, int silu, void* y, const NormMod& mod) {
     const int runs = c / 4;
     if (runs <= 64) {
         // G = smallest power of two >= runs: several rows per wave
         int g = 1;
         while (g < runs) g <<= 1;
         switch (g) {
-            case 1: launch_g<DT, 1, 1, 1>(s, x, n, c, gamma, beta, eps, silu, y); break;
-            case 2: launch_g<DT, 2, 1, 1>(s, x, n, c, gamma, beta, eps, silu, y); break;
-            case 4: launch_g<DT, 4, 1, 1>(s, x, n, c, gamma, beta, eps, silu, y); break;
-            case 8: launch_g<DT, 8, 1, 1>(s, x, n, c, gamma, beta, eps, silu, y); break;
-            case 16: launch_g<DT, 16, 1, 1>(s, x, n, c, gamma, beta, eps, silu, y); break;
-            case 32: launch_g<DT, 32, 1, 1>(s, x, n, c, gamma, beta, eps, silu, y); break;
-            default: launch_g<DT, 64, 1, 1>(s, x, n, c, gamma, beta, eps, silu, y); break;
+            case 1: launch_g<DT, 1, 1, 1>(s, x, n, c, gamma, beta, eps, silu, y, mod); break;
+            case 2: launch_g<DT, 2, 1, 1>(s, x, n, c, gamma, beta, eps, silu, y, mod); break;
+            case 4: launch_g<DT, 4, 1, 1>(s, x, n, c, gamma, beta, eps, silu, y, mod); break;
+            case 8: launch_g<DT, 8, 1, 1>(s, x, n, c, gamma, beta, eps, silu, y, mod); break;
+            case 16: launch_g<DT, 16, 1, 1>(s, x, n, c, gamma, beta, eps, silu, y, mod); break;
+            case 32: launch_g<DT, 32, 1, 1>(s, x, n, c, gamma, beta, eps, silu, y, mod); break;
+            default: launch_g<DT, 64, 1, 1>(s, x, n, c, gamma, beta, eps, silu, y, mod); break;
         }
     } else {
         // one row per wave, up to 8 runs of 4 per lane
-        launch_g<DT, 64, kNormMaxC / 256, 1>(s, x, n, c, gamma, beta, eps, silu, y);
+        launch_g<DT, 64, kNormMaxC / 256, 1>(s, x, n, c, gamma, beta, eps, silu, y, mod);
     }
     return hipGetLastError();
 }
@@ -430,36 +456,60 @@ hipError_t launch_gn_apply(hipStream_t s, const void* x, int64_t n_src, int c, i
 
 using namespace spc;
 
-extern "C" {
+namespace {
 
-int spc_layernorm_silu(spc_stream_t stream, int dtype, const void* x, int64_t n, int64_t c,
-                       const float* gamma, const float* beta, float eps, int silu, void* y) {
+int layernorm_entry(const char* fn, spc_stream_t stream, int dtype, const void* x, int64_t n,
+                    int64_t c, const float* gamma, const float* beta, float eps, int silu,
+                    void* y, const NormMod& mod) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (n < 0 || c <= 0 || c > kNormMaxC || c % 4 != 0 || !(eps >= 0.0f)) {
-        set_last_error("spc_layernorm_silu: unsupported shape n=%lld c=%lld (c a multiple of 4, "
-                       "at most %d) or eps", (long long)n, (long long)c, kNormMaxC);
+        set_last_error("%s: unsupported shape n=%lld c=%lld (c a multiple of 4, at most %d) or eps",
+                       fn, (long long)n, (long long)c, kNormMaxC);
         return SPC_BAD_SHAPE;
     }
     if (n == 0) return SPC_OK;
     const size_t align = dtype == SPC_F32 ? 16 : 8;
     if (!x || !y || ((uintptr_t)x % align) || ((uintptr_t)y % align) || ((uintptr_t)gamma % 16) ||
         ((uintptr_t)beta % 16)) {
-        set_last_error("spc_layernorm_silu: null or misaligned pointer (gamma / beta 16-byte aligned)");
+        set_last_error("%s: null or misaligned pointer (gamma / beta 16-byte aligned)", fn);
         return SPC_BAD_ARG;
     }
     hipError_t e;
-    if (dtype == SPC_BF16) e = launch_norm<SPC_BF16>(s, x, n, (int)c, gamma, beta, eps, silu, y);
-    else if (dtype == SPC_F16) e = launch_norm<SPC_F16>(s, x, n, (int)c, gamma, beta, eps, silu, y);
-    else if (dtype == SPC_F32) e = launch_norm<SPC_F32>(s, x, n, (int)c, gamma, beta, eps, silu, y);
+    if (dtype == SPC_BF16) e = launch_norm<SPC_BF16>(s, x, n, (int)c, gamma, beta, eps, silu, y, mod);
+    else if (dtype == SPC_F16) e = launch_norm<SPC_F16>(s, x, n, (int)c, gamma, beta, eps, silu, y, mod);
+    else if (dtype == SPC_F32) e = launch_norm<SPC_F32>(s, x, n, (int)c, gamma, beta, eps, silu, y, mod);
     else {
-        set_last_error("spc_layernorm_silu: unknown dtype %d", dtype);
+        set_last_error("%s: unknown dtype %d", fn, dtype);
         return SPC_BAD_ARG;
     }
     if (e != hipSuccess) {
-        set_last_error("spc_layernorm_silu: launch failed: %s", hipGetErrorString(e));
+        set_last_error("%s: launch failed: %s", fn, hipGetErrorString(e));
         return SPC_HIP_ERROR;
     }
     return SPC_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int spc_layernorm_silu(spc_stream_t stream, int dtype, const void* x, int64_t n, int64_t c,
+                       const float* gamma, const float* beta, float eps, int silu, void* y) {
+    return layernorm_entry("spc_layernorm_silu", stream, dtype, x, n, c, gamma, beta, eps, silu,
+                           y, NormMod{nullptr, nullptr, nullptr, 0});
+}
+
+int spc_layernorm_mod_silu(spc_stream_t stream, int dtype, const void* x, int64_t n, int64_t c,
+                           float eps, const float* scale, const float* shift,
+                           const int32_t* coords, int64_t n_batch, void* y) {
+    if (!scale || !shift || !coords || ((uintptr_t)scale % 16) || ((uintptr_t)shift % 16) ||
+        n_batch < 1) {
+        set_last_error("spc_layernorm_mod_silu: needs 16-byte aligned scale and shift, coords and "
+                       "n_batch >= 1");
+        return SPC_BAD_ARG;
+    }
+    return layernorm_entry("spc_layernorm_mod_silu", stream, dtype, x, n, c, nullptr, nullptr, eps,
+                           1, y, NormMod{scale, shift, coords, n_batch});
 }
 
 size_t spc_group_norm_workspace_bytes(int64_t n_batch, int64_t max_rows, int64_t groups) {

@@ -360,6 +360,8 @@ void set_last_error(const char* fmt, ...) {
     va_end(ap);
 }
 
+void clear_last_error() { g_last_error[0] = '\0'; }
+
 int hip_status(hipError_t e, const char* what) {
     set_last_error("%s failed: %s", what, hipGetErrorString(e));
     return SPC_HIP_ERROR;

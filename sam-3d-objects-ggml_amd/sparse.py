@@ -259,23 +259,13 @@ class SparseTensor:
         return SparseTensor(feats=feats, coords=coords)
 
     # -- arithmetic ---------------------------------------------------------
-    def _merge_cache(self, other: "SparseTensor") -> dict:
-        out = {}
-        for k in set(self._spatial_cache) | set(other._spatial_cache):
-            if k in self._spatial_cache:
-                out[k] = self._spatial_cache[k]
-            if k in other._spatial_cache:
-                if k not in out:
-                    out[k] = other._spatial_cache[k]
-                else:
-                    out[k].update(other._spatial_cache[k])
-        return out
-
     def __neg__(self) -> "SparseTensor":
         return self.replace(-self.feats)
 
     def _elemwise(self, other, op) -> "SparseTensor":
-        src = other
+        # SP/basic.py:349-364: a SparseTensor operand is replaced by its feats
+        # before the cache check there, so the result keeps self's spatial
+        # cache only (replace) and the operands' caches are never merged
         if isinstance(other, torch.Tensor):
             try:
                 other = sparse_batch_broadcast(self, torch.broadcast_to(other, self.shape))
@@ -283,10 +273,7 @@ class SparseTensor:
                 pass
         if isinstance(other, SparseTensor):
             other = other.feats
-        out = self.replace(op(self.feats, other))
-        if isinstance(src, SparseTensor):
-            out._spatial_cache = self._merge_cache(src)
-        return out
+        return self.replace(op(self.feats, other))
 
     def __add__(self, other):
         return self._elemwise(other, torch.add)
@@ -632,7 +619,7 @@ class SparseConv3d(nn.Module, _ConvCore):
         residual[residual_rows[t]] from a [R, Cout] residual --
         `norm_mod` = (scale, shift, eps) with
         per-batch [B, Cout] scale / shift gives silu(norm(y) * (1 + scale)
-        + shift) (structured_latent_flow.py:69-71; Cout <= 128)."""
+        + shift) (structured_latent_flow.py:69-71; Cout 32, 64 or 128)."""
         spatial_changed = any(s != 1 for s in self.stride) or (self.padding is not None)
         new_shape = torch.Size([x.shape[0], self.conv.out_channels])
         scale = tuple(s * k for s, k in zip(x._scale, self.stride))

@@ -103,14 +103,52 @@ def test_conv_norm_mod_silu_epilogue(spc, orc, dev, cout):
     assert np.mean(a == b) >= 0.98
 
 
-def test_norm_epilogue_rejects_wide_rows(spc, orc, dev):
+@pytest.mark.parametrize("cout", [256, 96])
+def test_norm_epilogue_rejects_other_widths(spc, orc, dev, cout):
+    """Only 32-, 64- and 128-channel rows fit the epilogue's lane groups;
+    other widths are refused (the block runs spc_layernorm_mod_silu)."""
     import torch
 
-    coords, n, x, xt, conv = _subm_setup(spc, orc, dev, 500, 10, 1, 64, 256, 51)
-    _case("norm epilogue with cout=256 is refused")
-    s = torch.zeros(1, 256, device=dev)
-    with pytest.raises(spc._native.SparseConvError, match="cout <= 128"):
+    coords, n, x, xt, conv = _subm_setup(spc, orc, dev, 500, 10, 1, 64, cout, 51)
+    _case(f"norm epilogue with cout={cout} is refused")
+    s = torch.zeros(1, cout, device=dev)
+    with pytest.raises(spc._native.SparseConvError, match="cout 32, 64 or 128"):
         conv.forward_fused(xt, norm_mod=(s, s, 1e-6))
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("c", [96, 1024, 2048])
+def test_layernorm_mod_silu(spc, orc, dev, dt, c):
+    """spc_layernorm_mod_silu against the oracle's composition:
+    dt(silu(dt(dt(dt(LN(x)) * dt(1 + scale[b])) + shift[b])))."""
+    import oracle
+    import torch
+
+    _case(f"layernorm_mod_silu {dt} c={c}")
+    nat = spc._native
+    rng = np.random.default_rng(c + 7)
+    sizes = [400, 3, 520]
+    n = sum(sizes)
+    coords = np.zeros((n, 4), np.int32)
+    coords[:, 0] = np.repeat(np.arange(3), sizes)
+    x = (rng.standard_normal((n, c)) * 2 + 0.3).astype(np.float32)
+    code = {"bf16": oracle.BF16, "f16": oracle.F16, "f32": oracle.F32}[dt]
+    r = lambda a: oracle.round_to(orc, a, code)  # noqa: E731
+    xr = r(x)
+    scale = r(rng.standard_normal((3, c)).astype(np.float32) * 0.3)
+    shift = r(rng.standard_normal((3, c)).astype(np.float32) * 0.3)
+    y = nat.layernorm_mod_silu(_dev_feats(orc, x, dt, dev), torch.from_numpy(scale).to(dev),
+                               torch.from_numpy(shift).to(dev), torch.from_numpy(coords).to(dev),
+                               eps=1e-6)
+    b = coords[:, 0]
+    u = r(oracle.layernorm(xr, None, None, 1e-6))
+    ref = r(oracle.silu(r(r(u * r(1.0 + scale[b])) + shift[b])))
+    got = from_dev(y)
+    if dt == "f32":
+        assert np.allclose(got, ref, rtol=1e-5, atol=1e-5)
+    else:
+        assert max_rel(got, ref) <= 1e-2
+        assert np.mean(got == ref) >= 0.98
 
 
 def _block_params(blk):
@@ -129,11 +167,12 @@ def _block_params(blk):
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
-@pytest.mark.parametrize("cin,cout", [(128, 128), (64, 128), (128, 256)])
+@pytest.mark.parametrize("cin,cout", [(128, 128), (64, 128), (128, 256), (64, 96), (96, 32)])
 def test_res_block(spc, orc, dev, cin, cout, dt):
-    """SparseResBlock3d on the fused kernels (the 256-channel block runs the
-    unfused norm path) against the oracle's block with the reference's
-    rounding points."""
+    """SparseResBlock3d on the fused kernels (32-, 64- and 128-channel
+    blocks take the conv's norm epilogue; 96 and 256 the conv plus the
+    spc_layernorm_mod_silu row pass) against the oracle's block with the
+    reference's rounding points."""
     import oracle
     import torch
 
@@ -165,7 +204,73 @@ def test_res_block(spc, orc, dev, cin, cout, dt):
                            coords[:, 0].astype(np.int64), code)
     got = from_dev(y.feats)
     assert got.shape == ref.shape
-    assert max_rel(got, ref) <= MAXREL
+    mr = max_rel(got, ref)
+    print(f"[parity] SparseResBlock3d {dt} {cin}->{cout}: max_rel={mr:.3e}", flush=True)
+    assert mr <= MAXREL
+
+
+@pytest.mark.parametrize("mode", ["down", "up"])
+def test_io_res_block(spc, orc, dev, mode):
+    """The SLAT flow model's IO blocks at their real widths (structured_
+    latent_flow.py:140-200; native SRC/slat_flow_graph.cpp:286-380, 395-396),
+    bf16:
+      down  SparseResBlock3d(128, 1024, 1024, downsample=True) on the 4
+            ellipsoid shells (62,710 fine -> 11,774 coarse rows): scatter-mean
+            downsample, LayerNorm + SiLU, conv 128 -> 1024, norm2 /
+            modulation / SiLU (the row pass), conv 1024 -> 1024, + the
+            128 -> 1024 skip;
+      up    SparseResBlock3d(2048, 1024, 128, upsample=True) (out_blocks[0]:
+            the 2 x 1024 concatenation of the skip) on 2 shells: coarse ->
+            fine gather, conv 2048 -> 128 at the fine rows, the fused norm
+            epilogue, conv 128 -> 128, + the 2048 -> 128 skip.
+    Against oracle.io_res_block, max-rel <= 2e-2."""
+    import oracle
+    import torch
+    from helpers import oracle_threads
+
+    sp = spc.sparse
+    fine = spc.workloads.ellipsoid_batch(4 if mode == "down" else 2)
+    cin, cout = (128, 1024) if mode == "down" else (2048, 128)
+    torch.manual_seed(7 + cin)
+    blk = spc.blocks.SparseResBlock3d(cin, 1024, cout, downsample=mode == "down",
+                                      upsample=mode == "up").to(dev)
+    with torch.no_grad():
+        for prm in blk.conv2.parameters():  # the reference zero-initialises conv2
+            prm.normal_(0, 0.02)
+        blk.norm1.weight.normal_(1, 0.1)
+        blk.norm1.bias.normal_(0, 0.1)
+    blk = blk.to(torch.bfloat16)
+    blk.norm1.float()
+    fd = torch.from_numpy(fine).to(dev)
+    if mode == "down":
+        x = spc.workloads.normal((fine.shape[0], cin), 1.0, seed=81)
+        xt = sp.SparseTensor(_dev_feats(orc, x, "bf16", dev), fd)
+        coords_in = fine
+    else:
+        # a coarse tensor with the upsample cache of its fine rows
+        ft = sp.SparseTensor(torch.zeros((fine.shape[0], 32), dtype=torch.bfloat16, device=dev),
+                             fd)
+        ct = sp.SparseDownsample(2)(ft)
+        coords_in = ct.coords.cpu().numpy()
+        x = spc.workloads.normal((coords_in.shape[0], cin), 1.0, seed=82)
+        xt = ct.replace(_dev_feats(orc, x, "bf16", dev))
+    _case(f"IO res block {mode} bf16 N_in={coords_in.shape[0]} {cin}->{cout}")
+    emb = torch.randn(len(np.unique(fine[:, 0])), 1024, device=dev).bfloat16()
+    with torch.no_grad():
+        y = blk(xt, emb)
+        emb_out = blk.emb_layers(emb).float().cpu().numpy()
+    torch.cuda.synchronize()
+    scale, shift = emb_out[:, :cout], emb_out[:, cout:]
+    oc, ref = oracle.io_res_block(orc, oracle.round_to(orc, x, oracle.BF16), coords_in,
+                                  _block_params(blk), scale, shift, oracle.BF16, mode=mode,
+                                  fine_coords=fine if mode == "up" else None,
+                                  nthreads=oracle_threads())
+    assert np.array_equal(y.coords.cpu().numpy(), oc)
+    got = from_dev(y.feats)
+    mr = max_rel(got, ref)
+    print(f"[parity] IO res block {mode} {cin}->{cout}: rows={ref.shape[0]} max_rel={mr:.3e}",
+          flush=True)
+    assert mr <= MAXREL
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f32"])

@@ -112,3 +112,49 @@ def oracle_voxels(rng):
         v = np.unique(rng.integers(0, 6, size=(60, 3)), axis=0)
         pts.append(np.hstack([np.full((v.shape[0], 1), b), v]))
     return np.ascontiguousarray(np.vstack(pts), dtype=np.int32)
+
+
+def _io_params(rng, ci, co):
+    f = lambda *s: (rng.standard_normal(s) * 0.05).astype(np.float32)  # noqa: E731
+    p = {"norm1_w": 1 + f(ci), "norm1_b": f(ci), "conv1_w": f(co, 27, ci), "conv1_b": f(co),
+         "conv2_w": f(co, 27, co), "conv2_b": f(co)}
+    if ci != co:
+        p["skip_w"], p["skip_b"] = f(co, ci), f(co)
+    return p
+
+
+def test_io_res_block_sampling_closed_forms(orc, spc):
+    """io_res_block's sampling step, F32: "down" runs res_block on the
+    coarse rows np.unique gives (lexicographic (b, x//2, y//2, z//2)) with
+    features sum(children) / (|children| + 1) -- torch scatter_reduce 'mean'
+    over a zero-initialised output counts the initial zero (SP/spatial.py:
+    37-49); "up" runs it on the fine rows with each fine row's coarse
+    parent's features (SP/spatial.py:92)."""
+    import oracle
+
+    rng = np.random.default_rng(5)
+    fine = spc.workloads.random_voxels(900, 12, batches=2, seed=5)
+    nf = fine.shape[0]
+    x = rng.standard_normal((nf, 32)).astype(np.float32)
+    p = _io_params(rng, 32, 64)
+    scale = (rng.standard_normal((2, 64)) * 0.2).astype(np.float32)
+    shift = (rng.standard_normal((2, 64)) * 0.2).astype(np.float32)
+    key = np.concatenate([fine[:, :1], fine[:, 1:] // 2], 1)
+    cc, inv = np.unique(key, axis=0, return_inverse=True)
+    inv = inv.reshape(-1)
+    sums = np.zeros((cc.shape[0], 32), np.float64)
+    np.add.at(sums, inv, x)
+    xc = (sums / (np.bincount(inv, minlength=cc.shape[0]) + 1)[:, None]).astype(np.float32)
+    oc, got = oracle.io_res_block(orc, x, fine, p, scale, shift, oracle.F32, mode="down")
+    assert np.array_equal(oc, cc.astype(np.int32))
+    want = oracle.res_block(orc, xc, orc.conv_table_slat(oc), p, scale, shift,
+                            oc[:, 0].astype(np.int64), oracle.F32)
+    assert np.allclose(got, want, rtol=1e-4, atol=1e-5)
+    # up: coarse features broadcast to the fine rows
+    xu = rng.standard_normal((cc.shape[0], 32)).astype(np.float32)
+    oc2, got2 = oracle.io_res_block(orc, xu, cc.astype(np.int32), p, scale, shift, oracle.F32,
+                                    mode="up", fine_coords=fine)
+    assert np.array_equal(oc2, fine)
+    want2 = oracle.res_block(orc, xu[inv], orc.conv_table_slat(fine), p, scale, shift,
+                             fine[:, 0].astype(np.int64), oracle.F32)
+    assert np.array_equal(got2, want2)

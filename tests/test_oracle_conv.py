@@ -156,3 +156,44 @@ def test_f16_bf16_conversions_exhaustive(orc):
     pos = np.sort(f[fin & (f > 0)].astype(np.float64))
     mids = ((pos[:-1] + pos[1:]) / 2).astype(np.float32)
     assert np.array_equal(orc.f32_to_f16(mids).view(np.float16), mids.astype(np.float16))
+
+
+@pytest.mark.parametrize("x_dt,w_dt,out_dt,w_layout,idx_layout,ntaps,cin,cout", [
+    (oracle.F32, oracle.F32, oracle.F32, 0, 1, 27, 64, 96),
+    (oracle.BF16, oracle.BF16, oracle.F32, 0, 1, 27, 128, 320),
+    (oracle.BF16, oracle.F16, oracle.BF16, 1, 0, 27, 32, 64),
+    (oracle.F16, oracle.F16, oracle.F16, 0, 0, 8, 64, 32),
+    (oracle.BF16, oracle.BF16, oracle.F32, 1, 1, 1, 96, 288),
+])
+def test_blocked_conv_is_bit_identical(spc, orc, x_dt, w_dt, out_dt, w_layout, idx_layout,
+                                       ntaps, cin, cout):
+    """orc_sparse_conv_blocked reorders the loops (row and output-channel
+    blocks, vectorised over output channels) without changing any output
+    element's sequence of roundings: its results equal orc_sparse_conv's
+    bit for bit, with missing taps, out-of-range sources, a ragged last row
+    block and several thread counts."""
+    wl = spc.workloads
+    rng = np.random.default_rng(ntaps * 1000 + cin + cout)
+    n_in, n_out = 700, 530
+    idx = rng.integers(-50, n_in + 50, size=n_out * ntaps).astype(np.int32)
+    idx[rng.random(idx.size) < 0.3] = n_in  # the sentinel
+
+    def enc(a, dt):
+        return {oracle.F32: lambda v: v, oracle.BF16: orc.f32_to_bf16,
+                oracle.F16: orc.f32_to_f16}[dt](np.ascontiguousarray(a, np.float32))
+
+    x = enc(wl.normal((n_in, cin), 1.0, seed=1), x_dt)
+    wshape = (cout, ntaps, cin) if w_layout == 0 else (ntaps, cout, cin)
+    w = enc(wl.normal(wshape, 0.05, seed=2), w_dt)
+    b = enc(wl.normal((cout,), 0.1, seed=3), x_dt)
+    kw = dict(ntaps=ntaps, n_out=n_out, idx_layout=idx_layout, out_dtype=out_dt, x_dtype=x_dt,
+              w_dtype=w_dt, b_dtype=x_dt, w_layout=w_layout)
+    ref = orc.sparse_conv(x, w, b, idx, nthreads=1, **kw)
+    for th in (1, 3):
+        got = orc.sparse_conv(x, w, b, idx, nthreads=th, blocked=True, **kw)
+        assert got.dtype == ref.dtype
+        assert np.array_equal(got.view(np.uint8), ref.view(np.uint8))
+    # no bias
+    kw.pop("b_dtype")
+    assert np.array_equal(orc.sparse_conv(x, w, None, idx, blocked=True, **kw).view(np.uint8),
+                          orc.sparse_conv(x, w, None, idx, **kw).view(np.uint8))

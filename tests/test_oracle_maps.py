@@ -228,3 +228,33 @@ def test_stride2_taps_closed_form(spc, orc):
         k = (x & 1) * 4 + (y & 1) * 2 + (z & 1)
         assert taps[d["fine_to_coarse"][i], k] == i
     assert (taps < c.shape[0]).sum() == c.shape[0]
+
+
+def test_subdivide_keep_closed_form(spc, orc):
+    """orc_subdivide with a keep mask is the unpruned subdivision (itself
+    pinned by MeshTables::build above: torch.nonzero child order, row p*8 +
+    c) filtered by the mask in row order, with each survivor's parent =
+    unpruned row // 8 -- for random masks, the all-kept and all-dropped
+    masks and the config-4 seeded masks."""
+    c0 = spc.workloads.random_voxels(700, 20, batches=3, seed=21)
+    full, fpar = orc.subdivide(c0)
+    assert np.array_equal(fpar, np.arange(full.shape[0]) // 8)
+    rng = np.random.default_rng(22)
+    for keep in (rng.random(full.shape[0]) < 0.5, rng.random(full.shape[0]) < 0.05,
+                 np.ones(full.shape[0], bool)):
+        k = keep.astype(np.uint8)
+        got_c, got_p = orc.subdivide(c0, k)
+        sel = np.nonzero(keep)[0]
+        assert np.array_equal(got_c, full[sel])
+        assert np.array_equal(got_p, sel // 8)
+    got_c, got_p = orc.subdivide(c0, np.zeros(full.shape[0], np.uint8))  # nothing survives
+    assert got_c.shape == (0, 4) and got_p.shape == (0,)
+    # the config-4 levels: the seeded masks, level by level
+    lvl = spc.workloads.sphere_shell()
+    for keep in spc.workloads.prune_masks(lvl.shape[0]):
+        full, _ = orc.subdivide(lvl)
+        got_c, got_p = orc.subdivide(lvl, keep)
+        sel = np.nonzero(keep)[0]
+        assert np.array_equal(got_c, full[sel]) and np.array_equal(got_p, sel // 8)
+        lvl = got_c
+    assert lvl.shape[0] == 347860

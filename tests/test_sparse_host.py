@@ -55,6 +55,22 @@ def test_spatial_cache_is_keyed_by_scale(sp):
     assert x._spatial_cache == {"(1, 1, 1)": {"a": 1}, "(2, 2, 2)": {"a": 2}}
 
 
+def test_elemwise_keeps_only_the_left_operands_cache(sp):
+    """SP/basic.py:349-364 replaces a SparseTensor operand by its feats
+    before its cache check, so `x + y` carries x's spatial cache alone and
+    neither operand's cache dicts change."""
+    x, y = _toy(sp), _toy(sp)
+    x.register_spatial_cache("a", 1)
+    y.register_spatial_cache("b", 2)
+    before_x = {k: dict(v) for k, v in x._spatial_cache.items()}
+    z = x + y
+    assert torch.equal(z.feats, 2 * x.feats)
+    assert z.get_spatial_cache("a") == 1 and z.get_spatial_cache("b") is None
+    assert x._spatial_cache == before_x and y.get_spatial_cache() == {"b": 2}
+    w = x * 3.0 - y
+    assert torch.equal(w.feats, 2 * x.feats) and w.get_spatial_cache("b") is None
+
+
 def test_map_cache_validates_coordinates(sp):
     x = _toy(sp)
     calls = []
