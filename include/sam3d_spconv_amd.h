@@ -16,7 +16,8 @@
  *     caller-owned workspace whose size the *_workspace_bytes queries
  *     return.  The exceptions are static device arrays, one per device for
  *     the life of the process: the spconv bridge's 64 MiB weight-pack buffer
- *     (sam3d_spconv_f16_forward) -- documented at their entry points.
+ *     (sam3d_spconv_f16_forward) and the 56 MiB map scratch of
+ *     spc_map_build_noalloc -- documented at their entry points.
  *   - Calls are asynchronous on `stream` (a hipStream_t; 0 = null stream)
  *     unless documented as synchronising.  Calls on one stream are ordered;
  *     separate workspaces make calls on different streams independent.
@@ -98,6 +99,22 @@ int spc_map_build(spc_stream_t stream, const int32_t* coords, int64_t n, int32_t
                   uint32_t flags, int32_t* token_major, int32_t* offset_major,
                   int32_t* mask_sorted, int32_t* argsort, int32_t* mask_natural,
                   void* workspace, size_t workspace_bytes);
+
+/* spc_map_build without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  No reference counterpart.  The
+ * scratch is a library-owned static device array of 56 MiB per device,
+ * held until the process ends; n must be at most 1,048,576 (2^20) voxels,
+ * larger n is SPC_BAD_SHAPE.  Same outputs, flags and semantics as
+ * spc_map_build; device-side errors (BAD_COORD / DUP_COORD) are returned
+ * with SPC_MAP_SYNC only (the status word lives in the shared scratch and
+ * the next call rewrites it).  All calls on one device share the scratch:
+ * calls that overlap on one device (other streams, other threads) race.
+ * Calls no hipMalloc / hipFree. */
+int spc_map_build_noalloc(spc_stream_t stream, const int32_t* coords, int64_t n,
+                          int32_t resolution, uint32_t flags, int32_t* token_major,
+                          int32_t* offset_major, int32_t* mask_sorted, int32_t* argsort,
+                          int32_t* mask_natural);
 
 /* spc_map_build over a dense grid [n_batch][R][R][R] of row ids (R =
  * resolution) instead of the hash table, for callers that bound the

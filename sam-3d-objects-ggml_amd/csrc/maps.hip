@@ -17,6 +17,7 @@
 #include <climits>
 
 #include <algorithm>
+#include <atomic>
 
 #include "common.h"
 
@@ -495,6 +496,37 @@ inline unsigned grid_for(int64_t n, int threads) { return (unsigned)((n + thread
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// ---- the map build's scratch for callers that cannot allocate ------------
+// (spc_map_build_noalloc).  One 56 MiB array per device, held until the
+// process ends: the hash-table map workspace of up to kNoAllocMaxN voxels
+// (spc_map_workspace_bytes(2^20) is about 53 MiB).  Every call on a device
+// shares it; the build's init kernel rewrites everything the build reads
+// (hash slots, status word) before use, so nothing carries over between
+// calls, but calls that overlap on one device race.
+constexpr int64_t kNoAllocMaxN = (int64_t)1 << 20;
+constexpr size_t kScratchBytes = (size_t)56 << 20;
+__device__ __attribute__((aligned(256))) uint8_t scratch[kScratchBytes];
+
+// Device address of `scratch` on the current device, looked up once per
+// device with that device current.  In host code `scratch` is a stand-in
+// symbol, not a device address: kernels and copies get this pointer only.
+void* scratch_addr() {
+    static std::atomic<void*> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    void* p = cache[dev].load(std::memory_order_acquire);
+    if (p == nullptr) {
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) {
+            set_last_error("spc_map_build_noalloc: hipGetSymbolAddress(scratch) failed on "
+                           "device %d: %s", dev, hipGetErrorString(e));
+            return nullptr;
+        }
+        cache[dev].store(p, std::memory_order_release);
+    }
+    return p;
+}
+
 }  // namespace
 }  // namespace spc
 
@@ -542,6 +574,22 @@ int spc_map_build(spc_stream_t stream, const int32_t* coords, int64_t n, int32_t
                                                         w.hkeys, w.hvals, cap_mask, w.status);
     return finish_map(s, c4, n, mesh, HashLookup{w.hkeys, w.hvals, cap_mask}, flags, token_major,
                       offset_major, mask_sorted, argsort, mask_natural, w);
+}
+
+int spc_map_build_noalloc(spc_stream_t stream, const int32_t* coords, int64_t n,
+                          int32_t resolution, uint32_t flags, int32_t* token_major,
+                          int32_t* offset_major, int32_t* mask_sorted, int32_t* argsort,
+                          int32_t* mask_natural) {
+    if (n > kNoAllocMaxN || spc_map_workspace_bytes(n) > kScratchBytes) {
+        set_last_error("spc_map_build_noalloc: n = %lld above the maximum %lld of the library's "
+                       "static scratch (use spc_map_build with a workspace)", (long long)n,
+                       (long long)kNoAllocMaxN);
+        return SPC_BAD_SHAPE;
+    }
+    void* ws = scratch_addr();
+    if (ws == nullptr) return SPC_HIP_ERROR;
+    return spc_map_build(stream, coords, n, resolution, flags, token_major, offset_major,
+                         mask_sorted, argsort, mask_natural, ws, kScratchBytes);
 }
 
 // n_batch * resolution^3 within 2^32 cells, tested by division: the product
