@@ -57,6 +57,8 @@ def parse():
                     help="target duration of the all-core CPU baseline sample (5 runs)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only time a 256 MiB device copy (PMC traffic calibration)")
+    ap.add_argument("--tiles", choices=["auto", "wide", "small"], default="auto",
+                    help="conv tile geometry (auto: each conv picks by shape)")
     return ap.parse_args()
 
 
@@ -249,6 +251,8 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
 
+    nat.set_tile_geometry({"auto": nat.TILES_AUTO, "wide": nat.TILES_WIDE,
+                           "small": nat.TILES_SMALL}[args.tiles])
     cfg = args.config
     if cfg == 2:
         coords = wl.ellipsoid_batch()
@@ -401,6 +405,7 @@ def main():
             "scaling": "weak", "vs_baseline": None, "dtype": dtype, "data": "synthetic",
             "config": {"workload": workload, "n_voxels": n, "pairs": pairs, "cin": cin,
                        "cout": cout, "batch": batch, "ntaps": 27, "row_order": args.order,
+                       "tiles": args.tiles,
                        "shell_rule": "|dist to surface| <= 1.5 voxel"},
             "tflops": tflops, "pct_peak": 100.0 * tflops / peak,
             "dense_equiv_tflops": 2.0 * 27 * n * cin * cout / t / 1e12,

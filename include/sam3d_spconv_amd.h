@@ -252,9 +252,11 @@ int spc_sparse_conv(spc_stream_t stream, int dtype, const void* x, int w_dtype, 
                     const int32_t* idx, int idx_layout, const int32_t* row_perm, int64_t ntaps,
                     int64_t n_out, int64_t n_in, int64_t cin, int64_t cout);
 
-/* Tile plan: the per-256-row-tile setup of the conv kernel (active tap
- * set, deduplicated source rows, slot table), built once per index table
- * and reused by every conv over it -- like the map, it depends only on
+/* Tile plan: the per-tile setup of the conv kernel (active tap set,
+ * deduplicated source rows, slot table) for both tile geometries (the
+ * 256-row tiles, then the small ones; see spc_conv_set_tile_geometry),
+ * built once per index table and reused by every conv over it -- like the
+ * map, it depends only on
  * (idx, idx_layout, row_perm, ntaps, n_out, n_in), not on channels or
  * weights.  spc_sparse_conv_plan takes the same arguments as
  * spc_sparse_conv plus a plan built from those same arguments (256-byte
@@ -270,6 +272,23 @@ int spc_sparse_conv_plan(spc_stream_t stream, int dtype, const void* x, int w_dt
                          void* y, const int32_t* idx, int idx_layout, const int32_t* row_perm,
                          const void* plan, int64_t ntaps, int64_t n_out, int64_t n_in,
                          int64_t cin, int64_t cout);
+
+/* Tile geometry of the conv kernel.  Every conv runs on one of two:
+ *   SPC_TILES_WIDE   256-row tiles over an 895-row double-buffered stage,
+ *                    one 8-wave workgroup per CU (long tiles: wide channels);
+ *   SPC_TILES_SMALL  128-row tiles (64 for 8 taps) over a 511-row stage,
+ *                    two or three 4-wave workgroups per CU (short tiles: small
+ *                    channel counts, few rows, the stride-2 conv).
+ * Both give the same results.  By default (SPC_TILES_AUTO) each conv picks
+ * by shape; spc_conv_set_tile_geometry forces one for every later conv of
+ * the process (measurements, tests; initially from the environment
+ * variable SPC_CONV_GEOMETRY = "wide" / "small").  The small tiles apply to
+ * packed weights with 27 or 8 taps.  Plans (spc_conv_plan) hold both.  No
+ * reference counterpart. */
+#define SPC_TILES_AUTO 0
+#define SPC_TILES_WIDE 1
+#define SPC_TILES_SMALL 2
+int spc_conv_set_tile_geometry(int geometry);
 
 /* Bytes of the SPC_W_PACKED form of ntaps x cout x cin weights of w_dtype
  * (Q8_0: quants then f32 scales), and the packer.  w_layout (SPC_W_KRSC,

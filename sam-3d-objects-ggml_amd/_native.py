@@ -94,6 +94,8 @@ def lib() -> ctypes.CDLL:
     L.spc_scatter_mean.argtypes = [_P, _INT, _P, _P, _P, _P, _I64, _I64, _I64, _P, _SZ]
     L.spc_gather_rows.argtypes = [_P, _INT, _P, _P, _P, _I64, _I64, _I64]
     L.spc_layernorm_silu.argtypes = [_P, _INT, _P, _I64, _I64, _P, _P, ctypes.c_float, _INT, _P]
+    L.spc_conv_set_tile_geometry.argtypes = [_INT]
+    L.spc_map_build_noalloc.argtypes = [_P, _P, _I64, _I32, _U32, _P, _P, _P, _P, _P]
     L.spc_layernorm_mod_silu.argtypes = [_P, _INT, _P, _I64, _I64, ctypes.c_float, _P, _P, _P,
                                          _I64, _P]
     L.spc_group_norm_workspace_bytes.restype = _SZ
@@ -398,6 +400,16 @@ def pack_weights(weight: torch.Tensor, w_scale: torch.Tensor | None = None, *,
                                  _ptr(w_scale), ntaps, cin, cout, _ptr(out))
     _check("spc_conv_pack_weights", st)
     return PackedWeights(out, wdt, ntaps, cin, cout)
+
+
+TILES_AUTO, TILES_WIDE, TILES_SMALL = 0, 1, 2
+
+
+def set_tile_geometry(geometry: int) -> None:
+    """spc_conv_set_tile_geometry: TILES_WIDE / TILES_SMALL force the conv
+    kernel's tile geometry for every later conv of the process; TILES_AUTO
+    (the default) lets each conv pick by shape.  Results are the same."""
+    _check("spc_conv_set_tile_geometry", lib().spc_conv_set_tile_geometry(int(geometry)))
 
 
 def conv_plan(idx: torch.Tensor | None, *, ntaps: int, n_out: int, n_in: int | None = None,

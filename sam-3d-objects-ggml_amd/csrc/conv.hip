@@ -2,6 +2,8 @@
 // argument checks, dispatch by dtype, the MFMA-fragment weight packer, the
 // Q8_0 block repacker and the reference-compatible spconv bridge.
 #include <atomic>
+#include <cstdlib>
+#include <cstring>
 
 #include "conv_kernel.h"
 
@@ -194,6 +196,16 @@ void* bridge_pack_addr() {
     return p;
 }
 
+// Tile-geometry override (spc_conv_set_tile_geometry; initially from
+// SPC_CONV_GEOMETRY=wide / small): 0 = each conv picks by shape.
+std::atomic<int> g_geometry{[] {
+    const char* e = getenv("SPC_CONV_GEOMETRY");
+    if (e && strcmp(e, "wide") == 0) return SPC_TILES_WIDE;
+    if (e && strcmp(e, "small") == 0) return SPC_TILES_SMALL;
+    return SPC_TILES_AUTO;
+}()};
+int geometry_override() { return g_geometry.load(std::memory_order_relaxed); }
+
 int check_shape(const char* fn, int64_t ntaps, int64_t cin, int64_t cout, bool any_taps = false) {
     const bool taps_ok = any_taps ? (ntaps >= 1 && ntaps <= 4096) : (ntaps == 27 || ntaps == 8 || ntaps == 1);
     if (!taps_ok || cin <= 0 || cout <= 0 || cin % 32 != 0 ||
@@ -285,7 +297,7 @@ int spc_conv_pack_weights(spc_stream_t stream, int w_dtype, int w_layout, const 
 
 size_t spc_conv_plan_bytes(int64_t n_out, int64_t ntaps) {
     if (n_out <= 0 || (ntaps != 27 && ntaps != 8 && ntaps != 1)) return 0;
-    return (size_t)(ceil_div(n_out, kTM) * plan_tile_bytes((int)ntaps));
+    return (size_t)(plan_wide_bytes(n_out, (int)ntaps) + plan_small_bytes(n_out, (int)ntaps));
 }
 
 int spc_conv_plan(spc_stream_t stream, const int32_t* idx, int idx_layout,
@@ -315,11 +327,20 @@ int spc_conv_plan(spc_stream_t stream, const int32_t* idx, int idx_layout,
     a.n_in = n_in;
     a.idx_layout = idx_layout;
     a.ntaps = (int32_t)ntaps;
-    const unsigned grid = (unsigned)ceil_div(n_out, kTM);
+    // the wide tiles' plans, then the small tiles' (a conv uses one of them)
     char* pl = static_cast<char*>(plan);
-    if (ntaps == 27) conv_plan_kernel<27><<<grid, 512, 0, s>>>(a, pl);
-    else if (ntaps == 8) conv_plan_kernel<8><<<grid, 512, 0, s>>>(a, pl);
-    else conv_plan_kernel<1><<<grid, 512, 0, s>>>(a, pl);
+    char* ps = pl + plan_wide_bytes(n_out, (int)ntaps);
+    const unsigned gw = (unsigned)ceil_div(n_out, GeoWide::TM);
+    if (ntaps == 27) {
+        conv_plan_kernel<27, GeoWide><<<gw, 512, 0, s>>>(a, pl);
+        conv_plan_kernel<27, GeoSmall<27>><<<(unsigned)ceil_div(n_out, GeoSmall<27>::TM), 512, 0, s>>>(a, ps);
+    } else if (ntaps == 8) {
+        conv_plan_kernel<8, GeoWide><<<gw, 512, 0, s>>>(a, pl);
+        conv_plan_kernel<8, GeoSmall<8>><<<(unsigned)ceil_div(n_out, GeoSmall<8>::TM), 512, 0, s>>>(a, ps);
+    } else {
+        conv_plan_kernel<1, GeoWide><<<gw, 512, 0, s>>>(a, pl);
+        conv_plan_kernel<1, GeoSmall<1>><<<(unsigned)ceil_div(n_out, GeoSmall<1>::TM), 512, 0, s>>>(a, ps);
+    }
     SPC_HIP(hipGetLastError());
     return SPC_OK;
 }
@@ -383,13 +404,13 @@ int conv_entry(spc_stream_t stream, int dtype, const void* x, int w_dtype, int w
     a.cout = (int32_t)cout;
     a.packed = w_layout == SPC_W_PACKED;
     if (class_rows > 0) {
-        if (class_rows % kTM != 0 || n_classes < 1 || n_classes * ntaps > 4096 ||
+        if (class_rows % GeoWide::TM != 0 || n_classes < 1 || n_classes * ntaps > 4096 ||
             n_classes * ntaps * cin * cout * 4 >= ((int64_t)1 << 31) ||
             n_out > class_rows * n_classes || !a.packed || w_dtype != dtype || w_dtype == SPC_Q8_0) {
             set_last_error("spc_sparse_conv_classes: class_rows must be a positive multiple of %d "
                            "with n_out <= class_rows * n_classes, weights packed in the feature "
                            "dtype (got class_rows=%lld n_classes=%lld n_out=%lld)",
-                           kTM, (long long)class_rows, (long long)n_classes, (long long)n_out);
+                           GeoWide::TM, (long long)class_rows, (long long)n_classes, (long long)n_out);
             return SPC_BAD_ARG;
         }
         a.class_rows = class_rows;
@@ -401,6 +422,7 @@ int conv_entry(spc_stream_t stream, int dtype, const void* x, int w_dtype, int w
     }
     a.plan = plan;
     a.num_cu = device_cu_count();
+    a.geometry = geometry_override();
     if (epi && epi->mode != SPC_EPI_NONE) {
         a.epi_mode = epi->mode;
         if (epi->mode == SPC_EPI_RESIDUAL) {
@@ -496,6 +518,15 @@ int spc_sparse_conv_classes(spc_stream_t stream, int dtype, const void* x, const
     }
     return conv_entry(stream, dtype, x, dtype, SPC_W_PACKED, w, nullptr, bias, y, idx, idx_layout,
                       row_perm, plan, ntaps, n_out, n_in, cin, cout, class_rows, n_classes, epi);
+}
+
+int spc_conv_set_tile_geometry(int geometry) {
+    if (geometry != SPC_TILES_AUTO && geometry != SPC_TILES_WIDE && geometry != SPC_TILES_SMALL) {
+        set_last_error("spc_conv_set_tile_geometry: unknown geometry %d", geometry);
+        return SPC_BAD_ARG;
+    }
+    g_geometry.store(geometry, std::memory_order_relaxed);
+    return SPC_OK;
 }
 
 void sam3d_spconv_f16_forward(spc_stream_t stream, const void* input, const void* weight,

@@ -85,6 +85,7 @@ struct ConvArgs {
     const float* epi_shift;   // [n_batch, cout]
     const int32_t* coords;    // [n_out, 4]: batch of each output row
     int64_t n_batch;          // rows of epi_scale / epi_shift
+    int32_t geometry;         // tile geometry: 0 by shape, 1 wide, 2 small
 };
 
 // MFMA operand traits per activation type.
@@ -155,22 +156,60 @@ struct Panel {
     static_assert(KS % G == 0, "panel geometry");
 };
 
-constexpr int kTM = 256;        // output rows per tile
-constexpr int kUMax = 895;      // capacity of the deduplicated source-row stage
-constexpr int kURowCap = (kUMax + 3) / 4 * 4;  // union-row table entries (16-byte multiple)
 constexpr int kWinWords = 1024; // dedupe bitmap: 32768 source rows
 constexpr int kHashBits = 11;    // wider spans: LDS hash of the tile's source rows
 constexpr int kHashSlots = 1 << kHashBits;  // 64-bit slots: row | rank << 32
-constexpr int kSortCap = 1024;   // distinct rows collected after hashing (> kUMax)
+constexpr int kSortCap = 1024;   // distinct rows collected after hashing (> any stage's UMAX)
 constexpr int kSetupScratchWords = 2 * kWinWords > 2 * kHashSlots + 2 * kSortCap
                                        ? 2 * kWinWords
                                        : 2 * kHashSlots + 2 * kSortCap;
 constexpr int kSegs = 4;        // 16-byte segments per staged 64-byte row chunk
 constexpr int kPitch = 5;       // staged row pitch in 16-byte units (64 bytes + 16 of padding)
-// 16-byte units per A stage buffer: whole 64-unit blocks (one LDS-DMA
-// instruction each) holding the kUMax union rows and the zero row
-constexpr int kStageUnits = ((kUMax + 1) * kPitch + 63) / 64 * 64;
-static_assert(kStageUnits == 4480, "stage geometry");
+
+// Tile geometry: TM output rows per tile, a deduplicated source-row stage of
+// UMAX rows (+ the zero row), NBUF A buffers.
+//   GeoWide   256 rows, 895-row stage, double-buffered (the next chunk lands
+//             while the MFMAs run): 159 KB of LDS, one workgroup of 8 waves
+//             per CU -- the wide convs, where every tile is long.
+//   GeoSmall  128 rows (64 for the 8-tap stride-2 conv, whose 128 coarse
+//             rows reference ~680 fine rows), 511-row stage, one buffer:
+//             ~51 KB of LDS, three workgroups of 4 waves per CU, which hide
+//             each other's staging and setup latency -- the short tiles of
+//             small channel counts, small row counts and stride-2.
+template <int TM_, int UMAX_, int NBUF_>
+struct Geo {
+    static constexpr int TM = TM_;
+    static constexpr int UMAX = UMAX_;
+    static constexpr int NBUF = NBUF_;
+    static constexpr int UROWCAP = (UMAX + 3) / 4 * 4;  // union-row table (16-byte multiple)
+    // 16-byte units per A buffer: whole 64-unit blocks (one LDS-DMA
+    // instruction each) holding the UMAX union rows and the zero row
+    static constexpr int STAGE = ((UMAX + 1) * kPitch + 63) / 64 * 64;
+    // One row tile's plan: header (U, tap mask, fast flag, tap words),
+    // output rows, union rows, slot keys.  It depends only on the index
+    // table, its layout, the row order and NTAPS -- not on channels or
+    // weights.
+    static constexpr int PLAN_SROW = 64;
+    static constexpr int PLAN_UROW = PLAN_SROW + 4 * TM;
+    static constexpr int PLAN_SIDX = PLAN_UROW + 4 * UROWCAP;
+    __host__ __device__ static constexpr int64_t plan_tile_bytes(int ntaps) {
+        return (PLAN_SIDX + 2 * (int64_t)(ntaps + 1) * TM + 255) / 256 * 256;
+    }
+};
+using GeoWide = Geo<256, 895, 2>;
+template <int NTAPS>
+using GeoSmall = Geo<NTAPS == 8 ? 64 : 128, 511, 1>;
+static_assert(GeoWide::STAGE == 4480 && GeoSmall<27>::STAGE == 2560, "stage geometry");
+
+// Plan buffer: the GeoWide plan of every 256-row tile, then the GeoSmall
+// plan of every small tile (a conv picks its geometry by shape).
+__host__ __device__ constexpr int64_t plan_wide_bytes(int64_t n_out, int ntaps) {
+    return (n_out + GeoWide::TM - 1) / GeoWide::TM * GeoWide::plan_tile_bytes(ntaps);
+}
+__host__ __device__ constexpr int64_t plan_small_bytes(int64_t n_out, int ntaps) {
+    return ntaps == 8 ? (n_out + 63) / 64 * Geo<64, 511, 1>::plan_tile_bytes(8)
+                      : (n_out + 127) / 128 * Geo<128, 511, 1>::plan_tile_bytes(ntaps);
+}
 
 // LDS position (in 16-byte units) of segment s of staged row r.  The 80-byte
 // pitch puts one segment of 8 (and of 16) consecutive rows on distinct banks,
@@ -183,23 +222,13 @@ __device__ __forceinline__ int seg_pos(int r, int s) { return r * kPitch + s; }
 
 constexpr int kTapWords = 8;  // step taps, four per word: up to 28 steps per chunk
 
-// Bytes of one row tile's plan: header (U, tap mask, fast flag, tap words),
-// output rows, union rows, slot keys.  The plan depends only on the index
-// table, its layout, the row order and NTAPS -- not on channels or weights.
-__host__ __device__ constexpr int64_t plan_tile_bytes(int ntaps) {
-    return (64 + 4 * kTM + 4 * kURowCap + 2 * (int64_t)(ntaps + 1) * kTM + 255) / 256 * 256;
-}
-constexpr int kPlanSrow = 64;
-constexpr int kPlanUrow = kPlanSrow + 4 * kTM;
-constexpr int kPlanSidx = kPlanUrow + 4 * kURowCap;
-
 // Shared-memory arrays of one tile's setup.
 struct TileLds {
     uint32_t* scratch;  // 2 * kWinWords words: dedupe bitmap + word ranks
-    uint16_t* sidx;     // (NTAPS + 1) x kTM slot keys; row NTAPS = the zero slot
+    uint16_t* sidx;     // (NTAPS + 1) x TM slot keys; row NTAPS = the zero slot
     uint32_t* tlw;      // kTapWords
-    int32_t* urow;      // kUMax source rows of the union slots
-    int32_t* srow;      // kTM output rows of the tile rows
+    int32_t* urow;      // UMAX source rows of the union slots
+    int32_t* srow;      // TM output rows of the tile rows
     int32_t* wsum;      // one per wave
     int32_t* misc;      // [0] tap mask [1] min source row [2] wide span [3] U [4] fast
                         // [5] distinct rows (hash path)
@@ -214,9 +243,10 @@ struct TileLds {
 // spatially coherent tile references ~3.2 x 256 distinct rows instead of
 // ~21 x 256, and ranks by popcount number them in ascending row order.
 // Ends with a barrier; results in L (misc[0], misc[3], misc[4]).
-template <int NTAPS, int NT, int PD>
+template <int NTAPS, int NT, int PD, typename GEO>
 __device__ __forceinline__ void tile_setup(const ConvArgs& a, int64_t r0, const TileLds& L) {
-    constexpr int TM = kTM;
+    constexpr int TM = GEO::TM;
+    constexpr int kUMax = GEO::UMAX;
     constexpr int NW = NT / 64;
     constexpr int NQ = NTAPS * TM;
     constexpr int EPT = (NQ + NT - 1) / NT;
@@ -468,39 +498,47 @@ __device__ __forceinline__ void tile_setup(const ConvArgs& a, int64_t r0, const 
     lds_barrier();
 }
 
-// One block per 256-row tile: runs the tile setup once and stores it, so
-// every conv over the same index table skips it.
-template <int NTAPS>
+// One block per row tile of geometry GEO: runs the tile setup once and
+// stores it, so every conv over the same index table skips it.
+template <int NTAPS, typename GEO>
 __global__ __launch_bounds__(512) void conv_plan_kernel(ConvArgs a, char* plan) {
+    constexpr int TM = GEO::TM;
     __shared__ __attribute__((aligned(16))) uint32_t scratch[kSetupScratchWords];
-    __shared__ __attribute__((aligned(16))) uint16_t sidx[(NTAPS + 1) * kTM];
+    __shared__ __attribute__((aligned(16))) uint16_t sidx[(NTAPS + 1) * TM];
     __shared__ __attribute__((aligned(16))) uint32_t tlw[kTapWords];
-    __shared__ __attribute__((aligned(16))) int32_t urow[kURowCap];
-    __shared__ __attribute__((aligned(16))) int32_t srow[kTM];
+    __shared__ __attribute__((aligned(16))) int32_t urow[GEO::UROWCAP];
+    __shared__ __attribute__((aligned(16))) int32_t srow[TM];
     __shared__ int32_t wsum[8];
     __shared__ int32_t misc[8];
     const TileLds L{scratch, sidx, tlw, urow, srow, wsum, misc};
     const int64_t tm = blockIdx.x;
-    tile_setup<NTAPS, 512, 4>(a, tm * kTM, L);
-    char* pt = plan + tm * plan_tile_bytes(NTAPS);
+    tile_setup<NTAPS, 512, 4, GEO>(a, tm * TM, L);
+    char* pt = plan + tm * GEO::plan_tile_bytes(NTAPS);
     int32_t* hdr = reinterpret_cast<int32_t*>(pt);
     const int U = misc[3];
     const int tid = threadIdx.x;
     if (tid < 8) hdr[tid] = tid == 0 ? U : tid == 1 ? misc[0] : tid == 2 ? misc[4] : 0;
     else if (tid < 16) hdr[tid] = (int32_t)tlw[tid - 8];
-    for (int i = tid; i < kTM; i += 512) reinterpret_cast<int32_t*>(pt + kPlanSrow)[i] = srow[i];
+    for (int i = tid; i < TM; i += 512) reinterpret_cast<int32_t*>(pt + GEO::PLAN_SROW)[i] = srow[i];
     if (misc[4]) {
-        for (int i = tid; i < U; i += 512) reinterpret_cast<int32_t*>(pt + kPlanUrow)[i] = urow[i];
-        for (int i = tid; i < (NTAPS + 1) * kTM; i += 512)
-            reinterpret_cast<uint16_t*>(pt + kPlanSidx)[i] = sidx[i];
+        for (int i = tid; i < U; i += 512)
+            reinterpret_cast<int32_t*>(pt + GEO::PLAN_UROW)[i] = urow[i];
+        for (int i = tid; i < (NTAPS + 1) * TM; i += 512)
+            reinterpret_cast<uint16_t*>(pt + GEO::PLAN_SIDX)[i] = sidx[i];
     }
 }
 
-template <typename T, bool Q8, bool PACKED, int NTAPS, int TN, int WM, int WN, int PD>
-__global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
+// Workgroups per CU a geometry is built for: GeoWide fills the CU's LDS
+// with one; GeoSmall's ~51 KB admit three (register budget 168 per wave),
+// two for 128-column tiles, whose 64 x 64 wave tiles need ~226 registers.
+template <typename GEO, int TN>
+constexpr int geo_blocks_per_cu() { return GEO::NBUF == 1 ? (TN >= 128 ? 2 : 3) : 1; }
+
+template <typename T, bool Q8, bool PACKED, int NTAPS, int TN, int WM, int WN, int PD, typename GEO>
+__global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void conv_kernel(ConvArgs a) {
     using M = Mfma<T>;
     using P = Panel<T, Q8>;
-    constexpr int TM = kTM;
+    constexpr int TM = GEO::TM;
     constexpr int NW = WM * WN;
     constexpr int NT = NW * 64;
     constexpr int ES = sizeof(T);
@@ -510,18 +548,21 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
     constexpr int FM = WTM / 32;
     constexpr int FN = WTN / 32;
     constexpr int NQ = NTAPS * TM;
-    constexpr int STAGE = kStageUnits;          // 16-byte units per A buffer
+    constexpr int STAGE = GEO::STAGE;           // 16-byte units per A buffer
+    constexpr int NBUF = GEO::NBUF;             // A buffers
+    constexpr int ABYTES = NBUF * STAGE * 16;   // the A area (reused by the setup and epilogue)
     constexpr int NPART = 4;                    // parts of a chunk's staging
-    static_assert(FM >= 1 && FN >= 1, "wave geometry");
+    static_assert(FM >= 1 && FN >= 1 && WTM * WM == TM && WTN * WN == TN, "wave geometry");
     static_assert(!Q8 || ES == 2, "Q8_0 weights feed 16-bit MFMA operands");
     static_assert(NTAPS <= 32, "tap mask is 32-bit");
-    static_assert(kSetupScratchWords * 4 <= 2 * STAGE * 16, "setup scratch aliases the A stage");
+    static_assert(kSetupScratchWords * 4 <= ABYTES, "setup scratch aliases the A stage");
     static_assert(PD == 4, "the step groups pack four taps per word");
+    static_assert(NBUF == 1 || NBUF == 2, "one or two A buffers");
 
-    __shared__ u32x4 Au[2 * STAGE];    // two A buffers: (U + 1) rows x 64 bytes each
+    __shared__ u32x4 Au[NBUF * STAGE];  // A buffers: (U + 1) rows x 64 bytes each
     __shared__ __attribute__((aligned(16))) uint16_t sidx[NQ + TM];  // slot keys; row NTAPS = zeros
     __shared__ __attribute__((aligned(16))) uint32_t tlw[kTapWords]; // step taps, 4 per word
-    __shared__ __attribute__((aligned(16))) int32_t urow[kURowCap];  // source row of each union slot
+    __shared__ __attribute__((aligned(16))) int32_t urow[GEO::UROWCAP];  // source row of each union slot
     __shared__ __attribute__((aligned(16))) int32_t srow[TM];        // output row of each tile row
     __shared__ int32_t wsum[NW];
     __shared__ __attribute__((aligned(16))) int32_t misc[8];
@@ -560,15 +601,15 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
         // whole plan tile (header, tap words, output rows, union rows, slot
         // keys -- contiguous in the plan) into LDS, all loads in flight at once
         const u32x4* pt = reinterpret_cast<const u32x4*>(static_cast<const char*>(a.plan) +
-                                                         tm * plan_tile_bytes(NTAPS));
+                                                         tm * GEO::plan_tile_bytes(NTAPS));
         constexpr int NHD = 2, NTW = 2;              // header and tap-word units
         constexpr int NSR = TM / 4;                  // srow units
-        constexpr int NUR = kURowCap / 4;            // urow units
+        constexpr int NUR = GEO::UROWCAP / 4;        // urow units
         constexpr int NSI = (NTAPS + 1) * TM / 8;    // sidx units
         constexpr int TOTAL = NHD + NTW + NSR + NUR + NSI;
         constexpr int IT = (TOTAL + NT - 1) / NT;
-        static_assert(kPlanSrow == 16 * (NHD + NTW) && kPlanUrow == kPlanSrow + 16 * NSR &&
-                          kPlanSidx == kPlanUrow + 16 * NUR,
+        static_assert(GEO::PLAN_SROW == 16 * (NHD + NTW) && GEO::PLAN_UROW == GEO::PLAN_SROW + 16 * NSR &&
+                          GEO::PLAN_SIDX == GEO::PLAN_UROW + 16 * NUR,
                       "plan sections are contiguous");
         u32x4 pv[IT];
 #pragma unroll
@@ -595,7 +636,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
     } else {
         if constexpr (kWinWords % NT == 0) {
             const TileLds L{reinterpret_cast<uint32_t*>(Au), sidx, tlw, urow, srow, wsum, misc};
-            tile_setup<NTAPS, NT, PD>(a, r0, L);
+            tile_setup<NTAPS, NT, PD, GEO>(a, r0, L);
             tile_mask = (uint32_t)misc[0];
             U = misc[3];
             fast = misc[4] != 0;
@@ -773,7 +814,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
     // The fast path stages through LDS DMA with 32-bit offsets from the
     // tile's lowest source row.
     const int64_t rowbytes = (int64_t)a.cin * ES;
-    const bool dma = fast && nt > 0 && U > 0 && U <= kUMax &&
+    const bool dma = fast && nt > 0 && U > 0 && U <= GEO::UMAX &&
                      (int64_t)(urow[U - 1] - urow[0] + 1) * rowbytes <= 0x7fffffffLL;
 
     if (dma) {
@@ -855,10 +896,12 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
         int has_row = 0;
         for (int k = lane; k < WTM; k += 64) has_row |= srow[wm * WTM + k] >= 0;
         if (__builtin_amdgcn_ballot_w64(has_row != 0) == 0) {
+            // the same barriers as the working waves, in the same order
             for (int h = 0; h < NPART; ++h) stage_part_rt(0, 0, h);
             dma_barrier<0>();
             for (int kc = 0; kc + 1 < kch; ++kc) {
-                for (int h = 0; h < NPART; ++h) stage_part_rt(kc + 1, (kc & 1) ^ 1, h);
+                if constexpr (NBUF == 1) lds_barrier();  // the buffer is free
+                for (int h = 0; h < NPART; ++h) stage_part_rt(kc + 1, NBUF == 1 ? 0 : (kc & 1) ^ 1, h);
                 dma_barrier<0>();
             }
         } else {
@@ -884,13 +927,24 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
             }
 
             for (int kc = 0; kc < kch; ++kc) {
-                const int buf = kc & 1;
-                const bool more = kc + 1 < kch;
+                const int buf = NBUF == 1 ? 0 : kc & 1;
+                // two buffers: the next chunk is staged while this one runs
+                const bool more = NBUF == 2 && kc + 1 < kch;
                 if (kc > 0) {
-                    // chunk staged; every wave done with the other buffer.  With
-                    // ngr >= NPART the last part preceded a whole group's loads.
-                    if (ngr >= NPART && LPS > 0) dma_barrier<PD * LPS>();
-                    else dma_barrier<0>();
+                    if constexpr (NBUF == 1) {
+                        // one buffer: once every wave is done reading the last
+                        // chunk (the barrier's fence waits for this wave's LDS
+                        // reads), stage this one and wait for it; the weight
+                        // prefetches of its first steps are older and land too
+                        lds_barrier();
+                        for (int h = 0; h < NPART; ++h) stage_part_rt(kc, 0, h);
+                        dma_barrier<0>();
+                    } else {
+                        // chunk staged; every wave done with the other buffer.  With
+                        // ngr >= NPART the last part preceded a whole group's loads.
+                        if (ngr >= NPART && LPS > 0) dma_barrier<PD * LPS>();
+                        else dma_barrier<0>();
+                    }
                     read_frags(buf, sreg[0], afr[0]);
                 }
 #pragma unroll
@@ -960,9 +1014,9 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
         // together; the round's steps then run from LDS, each step's weights
         // loaded while the previous step's MFMAs run.
         constexpr int UPT = (TM * kSegs + NT - 1) / NT;
-        constexpr int GA = 2 * STAGE / (TM * kPitch);
+        constexpr int GA = NBUF * STAGE / (TM * kPitch);
         constexpr int G = GA < 14 / UPT ? GA : 14 / UPT;  // taps per round (<= 56 VGPRs of loads)
-        static_assert(G >= 1 && G * TM * kPitch <= 2 * STAGE, "fallback rounds fit the A area");
+        static_assert(G >= 1 && G * TM * kPitch <= NBUF * STAGE, "fallback rounds fit the A area");
         for (int kc = 0; kc < kch; ++kc) {
             const int64_t koff = (int64_t)kc * KC * ES;
             uint32_t m = tile_mask;
@@ -1020,9 +1074,9 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
     // conv outputs go to an F32 LDS tile; groups of TN/4 lanes then take one
     // row each (four channels per lane, four rows in flight per lane group),
     // with group-local shuffles for the mean and the biased variance.
-    if constexpr (TN <= 128) if (a.epi_mode == SPC_EPI_NORM_MOD_SILU) {
+    if constexpr (TN <= 128 && TM * (TN + 4) * 4 <= ABYTES) if (a.epi_mode == SPC_EPI_NORM_MOD_SILU) {
         constexpr int FP = TN + 4;           // f32 row pitch (16-byte multiple)
-        static_assert(TM * FP * 4 <= 2 * STAGE * 16, "f32 output tile fits the A stage");
+        static_assert(TM * FP * 4 <= ABYTES, "f32 output tile fits the A stage");
         constexpr int G = TN / 4;            // lanes per row
         constexpr int RW = 64 / G;           // rows per wave at a time
         constexpr int RB = 4;                // row groups in flight per lane
@@ -1108,9 +1162,9 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
     // tile (8-byte writes, 16 in f32), then whole rows leave with coalesced
     // 16-byte stores.
     constexpr int OPITCH = TN * ES + 8;  // bytes per output-tile row in LDS
-    constexpr int NPASS = TM * OPITCH <= 2 * STAGE * 16 ? 1 : 2;  // f32 tiles go in two halves
+    constexpr int NPASS = TM * OPITCH <= ABYTES ? 1 : 2;  // f32 tiles go in two halves
     constexpr int RPP = TM / NPASS;      // tile rows per pass
-    static_assert(RPP * OPITCH <= 2 * STAGE * 16 && RPP % 32 == 0, "output tile fits the A stage");
+    static_assert(RPP * OPITCH <= ABYTES && RPP % 32 == 0, "output tile fits the A stage");
     constexpr int UPR = TN * ES / 16;    // 16-byte units per output row
     char* ob = reinterpret_cast<char*>(Au);
     char* yb = static_cast<char*>(a.y);
@@ -1206,27 +1260,90 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void conv_kernel(ConvArgs a) {
     }
 }
 
-template <typename T, bool Q8, bool PACKED, int NTAPS, int TN, int WM, int WN>
+template <typename T, bool Q8, bool PACKED, int NTAPS, int TN, int WM, int WN, typename GEO = GeoWide>
 hipError_t launch_conv(hipStream_t s, ConvArgs a) {
-    const int64_t tiles_m = ceil_div(a.n_out, kTM);
+    constexpr int TM = GEO::TM;
+    const int64_t tiles_m = ceil_div(a.n_out, TM);
     a.tiles_n = a.cout / TN;
     a.total_tiles = tiles_m * a.tiles_n;
-    a.heavy_tiles = (a.n_out % kTM ? tiles_m - 1 : tiles_m) * a.tiles_n;
+    a.heavy_tiles = (a.n_out % TM ? tiles_m - 1 : tiles_m) * a.tiles_n;
     a.tiles_per_xcd = ceil_div(a.heavy_tiles, 8);
     const int64_t grid = a.tiles_per_xcd * 8 + (a.total_tiles - a.heavy_tiles);
     if (grid == 0) return hipSuccess;
-    conv_kernel<T, Q8, PACKED, NTAPS, TN, WM, WN, 4><<<(unsigned)grid, WM * WN * 64, 0, s>>>(a);
+    // the plan buffer holds the wide plans, then the small ones
+    if (a.plan && !std::is_same<GEO, GeoWide>::value)
+        a.plan = static_cast<const char*>(a.plan) + plan_wide_bytes(a.n_out, NTAPS);
+    conv_kernel<T, Q8, PACKED, NTAPS, TN, WM, WN, 4, GEO><<<(unsigned)grid, WM * WN * 64, 0, s>>>(a);
     return hipGetLastError();
 }
 
-// TN = largest of {128, 64, 32} dividing cout, halved while the narrower
-// tiles still fit on the device in one round (small row counts would leave
-// compute units idle); 8 waves as 4x2 (64x64 wave tiles), 4x2 (64x32) or
-// 8x1 (32x32).  Q8_0 weights use 4 waves of 128x64: each in-register
-// dequantised B fragment then feeds four MFMAs instead of two.
+// Small tiles (GeoSmall: 128 rows, 64 for stride-2; three 4-wave
+// workgroups per CU, two at TN = 128): TN = largest of {128, 64, 32} dividing cout, halved
+// while the narrower tiles still fit on the device in one round; waves 2 x 2
+// (64 x 64 / 64 x 32 wave tiles; 32 x 64 / 32 x 32 for 64-row tiles), 4 x 1
+// (32 x 32) at TN = 32, 2 x 1 for 64-row tiles.
+template <typename T, bool Q8, bool PACKED, int NTAPS>
+hipError_t dispatch_small(hipStream_t s, const ConvArgs& a) {
+    using G = GeoSmall<NTAPS>;
+    const int64_t tiles_m = ceil_div(a.n_out, G::TM);
+    int tn = a.cout % 128 == 0 ? 128 : a.cout % 64 == 0 ? 64 : 32;
+    while (tn > 32 && tiles_m * (a.cout / (tn / 2)) <= a.num_cu) tn /= 2;
+    if (a.epi_mode == SPC_EPI_NORM_MOD_SILU) tn = a.cout;  // 32 or 64 here (one tile per row)
+    if (tn == 128) return launch_conv<T, Q8, PACKED, NTAPS, 128, 2, 2, G>(s, a);
+    if (tn == 64) return launch_conv<T, Q8, PACKED, NTAPS, 64, 2, 2, G>(s, a);
+    if constexpr (G::TM == 128) return launch_conv<T, Q8, PACKED, NTAPS, 32, 4, 1, G>(s, a);
+    else return launch_conv<T, Q8, PACKED, NTAPS, 32, 2, 1, G>(s, a);
+}
+
+// Which geometry a conv runs.  a.geometry forces one (1 wide, 2 small);
+// otherwise the small tiles take the shapes where their single stage buffer
+// costs nothing because co-resident workgroups hide each other's staging:
+//   - the 8-tap stride-2 conv (256 coarse rows reference ~1,360 fine rows,
+//     beyond the wide stage: 29.8 -> 11.6 us for 128 -> 128 over 62,710
+//     fine rows);
+//   - one or two channel chunks per tile (C_in <= 64 in 16-bit, <= 32 in
+//     f32), where a wide tile is mostly setup and staging latency (the
+//     mesh levels: 31.8 -> 23.3 us at 128^3 C=64, 50.8 -> 38.7 us at 256^3
+//     C=32);
+//   - 128-column tiles that need more than one round of the CUs, so the
+//     workgroups sharing a CU drift apart (SubM 1024 -> 1024 over 11,774
+//     rows: 627 -> 572 us; 128 -> 1024: 105 -> 89 us).
+// A single round of long wide tiles stays wide: the double-buffered stage
+// overlaps every chunk's staging with the MFMAs, which the small tiles'
+// synchronised workgroups cannot (C=128 over 62,710 rows: 57 vs 104 us;
+// f32 C=64 over 21,766 rows: 62.9 vs 65.2 us).
+// Packed weights, 27 or 8 taps (the dense 1 x 1 x 1 conv keeps the wide
+// tiles, as do weight classes, the 96- / 192-column tiles and the norm
+// epilogue over 128 channels).
+template <typename T, bool Q8, bool PACKED, int NTAPS>
+bool use_small_tiles(const ConvArgs& a) {
+    if constexpr (!PACKED || NTAPS == 1) {
+        return false;
+    } else {
+        if (a.epi_mode == SPC_EPI_NORM_MOD_SILU && a.cout > 64) return false;
+        if (a.geometry != 0) return a.geometry == 2;
+        if (a.class_rows > 0) return false;
+        if (NTAPS == 8) return true;
+        const int64_t kch = (int64_t)a.cin * (int64_t)sizeof(T) / 64;
+        if (kch <= 2) return true;
+        const int64_t tiles_m = ceil_div(a.n_out, GeoWide::TM);
+        return a.cout % 128 == 0 && tiles_m * (a.cout / 128) > a.num_cu;
+    }
+}
+
+// Wide tiles: TN = largest of {128, 64, 32} dividing cout, halved while the
+// narrower tiles still fit on the device in one round (small row counts
+// would leave compute units idle); 8 waves as 4x2 (64x64 wave tiles), 4x2
+// (64x32) or 8x1 (32x32).  Q8_0 weights use 4 waves of 128x64: each
+// in-register dequantised B fragment then feeds four MFMAs instead of two.
 template <typename T, bool Q8, bool PACKED, int NTAPS>
 hipError_t dispatch_tn(hipStream_t s, const ConvArgs& a) {
-    const int64_t tiles_m = ceil_div(a.n_out, kTM);
+    if (a.epi_mode == SPC_EPI_NORM_MOD_SILU && a.cout != 32 && a.cout != 64 && a.cout != 128)
+        return hipErrorInvalidValue;  // the epilogue's lane groups need one 32/64/128-column tile
+    if constexpr (PACKED && NTAPS != 1) {
+        if (use_small_tiles<T, Q8, PACKED, NTAPS>(a)) return dispatch_small<T, Q8, PACKED, NTAPS>(s, a);
+    }
+    const int64_t tiles_m = ceil_div(a.n_out, GeoWide::TM);
     int tn = a.cout % 128 == 0 ? 128 : a.cout % 64 == 0 ? 64 : 32;
     while (tn > 32 && tiles_m * (a.cout / (tn / 2)) <= a.num_cu) tn /= 2;
     // a ragged last round of 128-column tiles (e.g. 368 tiles on 256 compute
@@ -1240,11 +1357,7 @@ hipError_t dispatch_tn(hipStream_t s, const ConvArgs& a) {
             if (r64 * 6 < r128 * 10) tn = 64;
         }
     }
-    if (a.epi_mode == SPC_EPI_NORM_MOD_SILU) {
-        // one tile covers the row; the epilogue's lane groups need 32, 64 or 128
-        if (a.cout != 32 && a.cout != 64 && a.cout != 128) return hipErrorInvalidValue;
-        tn = a.cout;
-    }
+    if (a.epi_mode == SPC_EPI_NORM_MOD_SILU) tn = a.cout;  // one tile covers the row
     // widths 128 does not divide but 192 does (the mesh decoder's 768 / 4):
     // one 192-column tile of 4 waves (2 x 2, 128x96 wave tiles, one per
     // SIMD) instead of three 64-column tiles of 64x32 wave tiles, which read

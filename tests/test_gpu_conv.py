@@ -303,8 +303,10 @@ def test_wide_span_tiles_stay_on_the_fast_path(spc, orc, dev):
     _case(f"wide-span tiles N={n} bf16 32->32")
     m = nat.map_build(torch.from_numpy(coords).to(dev))
     plan = nat.conv_plan(m.token_major, ntaps=27, n_out=n)
+    # the plan's first section: one 19,200-byte plan per 256-row tile
     tiles = (n + 255) // 256
-    hdr = plan.view(torch.int32).cpu().numpy().reshape(tiles, -1)
+    wide_tile = (64 + 4 * 256 + 4 * 896 + 2 * 28 * 256 + 255) // 256 * 256
+    hdr = plan[: tiles * wide_tile].view(torch.int32).cpu().numpy().reshape(tiles, -1)
     assert (hdr[:, 2] == 1).all() and (hdr[:, 0] <= 895).all()
     tm = m.token_major.cpu().numpy().reshape(n, 27)
     span = np.where(tm < n, tm, -1).max(1).max() - np.where(tm < n, tm, n).min(1).min()

@@ -1,0 +1,230 @@
+"""The conv kernel's two tile geometries (SPC_TILES_WIDE: 256-row tiles over a
+double-buffered 895-row stage; SPC_TILES_SMALL: 128-row tiles, 64 for 8
+taps, over a single 511-row stage, several workgroups per CU) compute every
+output row with the same sequence of MFMA steps -- chunks outer, active taps
+ascending, absent taps adding exact zeros -- so their outputs are equal
+value for value, with and without a tile plan, for every dtype, epilogue and
+staging path.  The small tiles are also checked against the oracle."""
+import numpy as np
+import pytest
+
+from helpers import bf16_bits, check_16bit, from_dev, oracle_threads, to_dev_bf16
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(name):
+    print(f"[case] {name}", flush=True)
+
+
+@pytest.fixture()
+def geo(spc):
+    nat = spc._native
+    yield nat
+    nat.set_tile_geometry(nat.TILES_AUTO)
+
+
+def _both(nat, fn):
+    """fn() under the wide, then the small tiles (with a fresh plan each)."""
+    import torch
+
+    out = []
+    for g in (nat.TILES_WIDE, nat.TILES_SMALL):
+        nat.set_tile_geometry(g)
+        out.append(fn())
+    torch.cuda.synchronize()
+    nat.set_tile_geometry(nat.TILES_AUTO)
+    return out
+
+
+def _inputs(spc, orc, n_in, cin, cout, ntaps, seed, dt="bf16"):
+    import torch
+
+    wl = spc.workloads
+    x = wl.normal((n_in, cin), 1.0, seed=seed)
+    w = wl.normal((cout, ntaps, cin), 0.05, seed=seed + 1)
+    b = wl.normal((cout,), 0.1, seed=seed + 2)
+    if dt == "bf16":
+        x, w, b = (bf16_bits(orc, a) for a in (x, w, b))
+        return (x, w, b), tuple(to_dev_bf16(a, "cuda:0") for a in (x, w, b))
+    if dt == "f16":
+        x, w, b = (a.astype(np.float16) for a in (x, w, b))
+    return (x, w, b), tuple(torch.from_numpy(a).to("cuda:0") for a in (x, w, b))
+
+
+@pytest.mark.parametrize("dt,cin,cout,nvox,grid", [
+    ("bf16", 32, 32, 40000, 48), ("bf16", 64, 64, 30000, 40), ("bf16", 64, 128, 30000, 40),
+    ("bf16", 128, 128, 12000, 30), ("bf16", 128, 256, 12000, 30), ("bf16", 96, 160, 9000, 28),
+    ("f32", 64, 64, 20000, 36), ("f32", 32, 96, 20000, 36), ("f16", 64, 128, 15000, 32)])
+def test_subm_wide_equals_small(spc, orc, dev, geo, dt, cin, cout, nvox, grid):
+    import oracle
+    import torch
+
+    nat = geo
+    coords = spc.workloads.random_voxels(nvox, grid, batches=2, seed=cin + cout)
+    n = coords.shape[0]
+    _case(f"subm {dt} N={n} {cin}->{cout}: wide vs small tiles")
+    (xh, wh, bh), (x, w, b) = _inputs(spc, orc, n, cin, cout, 27, seed=cin * 7 + cout, dt=dt)
+    m = nat.map_build(torch.from_numpy(coords).to(dev))
+    pw = nat.pack_weights(w)
+
+    def run():
+        plan = nat.conv_plan(m.token_major, ntaps=27, n_out=n)
+        return (nat.sparse_conv(x, pw, b, m.token_major, ntaps=27, n_out=n, plan=plan),
+                nat.sparse_conv(x, pw, b, m.token_major, ntaps=27, n_out=n))
+
+    (wp, wn), (sp_, sn) = _both(nat, run)
+    assert torch.equal(wp, wn) and torch.equal(sp_, sn)
+    assert torch.equal(wp, sp_)
+    tm = m.token_major.cpu().numpy()
+    code = {"bf16": oracle.BF16, "f16": oracle.F16, "f32": oracle.F32}[dt]
+    ref = orc.sparse_conv(xh, wh, bh, tm, ntaps=27, n_out=n, idx_layout=1, out_dtype=oracle.F32,
+                          x_dtype=code, w_dtype=code, b_dtype=code, nthreads=oracle_threads(),
+                          blocked=True)
+    if dt == "f32":
+        assert np.all(np.abs(sp_.cpu().numpy() - ref) <= 1e-5 + 1e-4 * np.abs(ref))
+    else:
+        check_16bit(f"small tiles {dt} {cin}->{cout}", from_dev(sp_), ref)
+
+
+@pytest.mark.parametrize("cin,cout", [(128, 128), (64, 64), (64, 32), (128, 1024)])
+def test_stride2_wide_equals_small(spc, orc, dev, geo, cin, cout):
+    """The 2x2x2 stride-2 conv on the config-2 coords: the wide tiles' 256
+    coarse rows overflow their stage (per-tap fallback), the small tiles'
+    64 coarse rows (about 340 fine rows) take the staged path."""
+    import oracle
+    import torch
+
+    nat = geo
+    coords = spc.workloads.ellipsoid_batch()
+    nf = coords.shape[0]
+    d = nat.downsample_map(torch.from_numpy(coords).to(dev), 4, 64)
+    _case(f"stride-2 nf={nf} nc={d.nc} {cin}->{cout}: wide vs small tiles")
+    (xh, wh, bh), (x, w, b) = _inputs(spc, orc, nf, cin, cout, 8, seed=cin + 3 * cout)
+    pw = nat.pack_weights(w)
+
+    def run():
+        plan = nat.conv_plan(d.stride2_taps, ntaps=8, n_out=d.nc, n_in=nf)
+        return nat.sparse_conv(x, pw, b, d.stride2_taps, ntaps=8, n_out=d.nc, plan=plan)
+
+    yw, ys = _both(nat, run)
+    assert torch.equal(yw, ys)
+    ref = orc.sparse_conv(xh, wh, bh, d.stride2_taps.cpu().numpy(), ntaps=8, n_out=d.nc,
+                          idx_layout=1, out_dtype=oracle.F32, x_dtype=oracle.BF16,
+                          w_dtype=oracle.BF16, b_dtype=oracle.BF16, nthreads=oracle_threads(),
+                          blocked=True)
+    check_16bit(f"small tiles stride-2 {cin}->{cout}", from_dev(ys), ref)
+
+
+@pytest.mark.parametrize("n", [1, 5, 127, 130, 300])
+def test_ragged_and_tiny(spc, orc, dev, geo, n):
+    """Row counts below and just past a tile; rows with no neighbours."""
+    import torch
+
+    nat = geo
+    coords = spc.workloads.random_voxels(n, 5 if n < 100 else 9, batches=1, seed=n)[:n]
+    n = coords.shape[0]
+    _case(f"ragged N={n}: wide vs small tiles")
+    _, (x, w, b) = _inputs(spc, orc, n, 64, 64, 27, seed=n + 11)
+    m = nat.map_build(torch.from_numpy(np.ascontiguousarray(coords)).to(dev))
+    pw = nat.pack_weights(w)
+    yw, ys = _both(nat, lambda: nat.sparse_conv(x, pw, b, m.token_major, ntaps=27, n_out=n,
+                                                plan=nat.conv_plan(m.token_major, ntaps=27,
+                                                                   n_out=n)))
+    assert torch.equal(yw, ys)
+
+
+def test_q8_0_wide_equals_small(spc, orc, dev, geo):
+    import torch
+
+    nat = geo
+    coords = spc.workloads.random_voxels(15000, 32, batches=2, seed=5)
+    n = coords.shape[0]
+    _case(f"Q8_0 N={n} 64->128: wide vs small tiles")
+    g = torch.Generator(device="cpu").manual_seed(3)
+    x = torch.randn((n, 64), generator=g).to(dev, torch.bfloat16)
+    blocks = nat.q8_0_quantize((torch.randn((128, 27, 64), generator=g) * 0.02).to(dev))
+    qs, dsc = nat.q8_0_repack(blocks)
+    pw = nat.pack_weights(qs, dsc, cin=64, cout=128)
+    m = nat.map_build(torch.from_numpy(coords).to(dev))
+    yw, ys = _both(nat, lambda: nat.sparse_conv(x, pw, None, m.token_major, ntaps=27, n_out=n,
+                                                plan=nat.conv_plan(m.token_major, ntaps=27,
+                                                                   n_out=n)))
+    assert torch.equal(yw, ys)
+
+
+def test_wide_span_and_fallback_small(spc, orc, dev, geo):
+    """Small tiles whose sources span beyond the bitmap window (the LDS hash
+    dedupe) and tiles in random row order (union beyond the 511-row stage:
+    the per-tap fallback) equal the wide tiles."""
+    import torch
+
+    nat = geo
+    g = np.stack(np.meshgrid([0], [0, 1], np.arange(2048), np.arange(16), indexing="ij"), -1)
+    slabs = np.ascontiguousarray(g.reshape(-1, 4), dtype=np.int32)
+    shell = spc.workloads.ellipsoid_batch(1, seed=5)
+    shuffled = np.ascontiguousarray(shell[np.random.default_rng(6).permutation(len(shell))])
+    for name, coords in (("two slabs", slabs), ("shuffled shell", shuffled)):
+        n = coords.shape[0]
+        _case(f"{name} N={n}: wide vs small tiles")
+        _, (x, w, b) = _inputs(spc, orc, n, 32, 64, 27, seed=n % 1000)
+        m = nat.map_build(torch.from_numpy(coords).to(dev))
+        pw = nat.pack_weights(w)
+        yw, ys = _both(nat, lambda: nat.sparse_conv(
+            x, pw, b, m.token_major, ntaps=27, n_out=n,
+            plan=nat.conv_plan(m.token_major, ntaps=27, n_out=n)))
+        assert torch.equal(yw, ys)
+
+
+@pytest.mark.parametrize("cout", [32, 64])
+def test_epilogues_wide_equal_small(spc, orc, dev, geo, cout):
+    """Residual and norm / modulation / SiLU epilogues on the small tiles."""
+    import torch
+
+    nat = geo
+    coords = spc.workloads.random_voxels(20000, 36, batches=3, seed=cout)
+    n = coords.shape[0]
+    _case(f"epilogues N={n} 64->{cout}: wide vs small tiles")
+    _, (x, w, b) = _inputs(spc, orc, n, 64, cout, 27, seed=cout + 1)
+    cd = torch.from_numpy(coords).to(dev)
+    m = nat.map_build(cd)
+    pw = nat.pack_weights(w)
+    r = torch.randn((n, cout), device=dev).bfloat16()
+    sc = (torch.randn((3, cout), device=dev) * 0.3).bfloat16().float()
+    sh = (torch.randn((3, cout), device=dev) * 0.3).bfloat16().float()
+
+    def run():
+        plan = nat.conv_plan(m.token_major, ntaps=27, n_out=n)
+        return (nat.sparse_conv(x, pw, b, m.token_major, ntaps=27, n_out=n, plan=plan,
+                                residual=r),
+                nat.sparse_conv(x, pw, b, m.token_major, ntaps=27, n_out=n, plan=plan,
+                                norm_mod=(sc, sh, cd, 1e-6)))
+
+    (rw, nw), (rs, ns) = _both(nat, run)
+    assert torch.equal(rw, rs) and torch.equal(nw, ns)
+
+
+def test_weight_classes_small(spc, orc, dev, geo):
+    """The merged-tap child conv (8 taps, 8 weight classes, class-major row
+    order) on the small tiles equals the wide tiles."""
+    import torch
+
+    nat = geo
+    coords = spc.workloads.random_voxels(3000, 24, batches=1, seed=9)
+    n = coords.shape[0]
+    _case(f"weight classes N_parent={n}: wide vs small tiles")
+    m = nat.map_build(torch.from_numpy(coords).to(dev))
+    idx, perm, class_rows = nat.subdivide_tap_classes(m.token_major, n)
+    g = torch.Generator(device="cpu").manual_seed(4)
+    x = torch.randn((n, 64), generator=g).to(dev, torch.bfloat16)
+    w = (torch.randn((64, 64, 64), generator=g) * 0.05).to(dev, torch.bfloat16)
+    pw = nat.pack_weights(w)
+
+    def run():
+        plan = nat.conv_plan(idx, ntaps=8, n_out=8 * class_rows, n_in=n, row_perm=perm)
+        return nat.sparse_conv(x, pw, None, idx, ntaps=8, n_out=8 * class_rows, row_perm=perm,
+                               plan=plan, class_rows=class_rows, n_classes=8,
+                               out=torch.empty((8 * n, 64), dtype=torch.bfloat16, device=dev))
+
+    yw, ys = _both(nat, run)
+    assert torch.equal(yw, ys)
