@@ -267,6 +267,16 @@ size_t spc_conv_plan_bytes(int64_t n_out, int64_t ntaps);
 int spc_conv_plan(spc_stream_t stream, const int32_t* idx, int idx_layout,
                   const int32_t* row_perm, int64_t ntaps, int64_t n_out, int64_t n_in, void* plan,
                   size_t plan_bytes);
+/* spc_conv_plan building only the given sections (SPC_PLAN_WIDE and / or
+ * SPC_PLAN_SMALL) of a plan of the same size: a conv whose tile geometry
+ * finds its section unbuilt sets its tiles up itself (same results,
+ * slower), so callers that rebuild plans often (per call) build only the
+ * geometry their convs run. */
+#define SPC_PLAN_WIDE 1u
+#define SPC_PLAN_SMALL 2u
+int spc_conv_plan_sections(spc_stream_t stream, const int32_t* idx, int idx_layout,
+                           const int32_t* row_perm, int64_t ntaps, int64_t n_out, int64_t n_in,
+                           uint32_t sections, void* plan, size_t plan_bytes);
 int spc_sparse_conv_plan(spc_stream_t stream, int dtype, const void* x, int w_dtype,
                          int w_layout, const void* w, const void* w_scale, const void* bias,
                          void* y, const int32_t* idx, int idx_layout, const int32_t* row_perm,
@@ -289,6 +299,11 @@ int spc_sparse_conv_plan(spc_stream_t stream, int dtype, const void* x, int w_dt
 #define SPC_TILES_WIDE 1
 #define SPC_TILES_SMALL 2
 int spc_conv_set_tile_geometry(int geometry);
+/* The geometry (SPC_TILES_WIDE / SPC_TILES_SMALL) a conv with packed weights
+ * and these arguments runs now (epi_mode a spc_epilogue_mode, class_rows 0
+ * without weight classes): which plan section it reads. */
+int spc_conv_tile_geometry(int dtype, int w_dtype, int64_t ntaps, int64_t n_out, int64_t cin,
+                           int64_t cout, int64_t class_rows, int epi_mode);
 
 /* Bytes of the SPC_W_PACKED form of ntaps x cout x cin weights of w_dtype
  * (Q8_0: quants then f32 scales), and the packer.  w_layout (SPC_W_KRSC,

@@ -81,6 +81,7 @@ def lib() -> ctypes.CDLL:
     L.spc_conv_plan_bytes.restype = _SZ
     L.spc_conv_plan_bytes.argtypes = [_I64, _I64]
     L.spc_conv_plan.argtypes = [_P, _P, _INT, _P, _I64, _I64, _I64, _P, _SZ]
+    L.spc_conv_plan_sections.argtypes = [_P, _P, _INT, _P, _I64, _I64, _I64, _U32, _P, _SZ]
     L.spc_conv_packed_bytes.restype = _SZ
     L.spc_conv_packed_bytes.argtypes = [_INT, _I64, _I64, _I64]
     L.spc_conv_pack_weights.argtypes = [_P, _INT, _INT, _P, _P, _I64, _I64, _I64, _P]
@@ -95,6 +96,7 @@ def lib() -> ctypes.CDLL:
     L.spc_gather_rows.argtypes = [_P, _INT, _P, _P, _P, _I64, _I64, _I64]
     L.spc_layernorm_silu.argtypes = [_P, _INT, _P, _I64, _I64, _P, _P, ctypes.c_float, _INT, _P]
     L.spc_conv_set_tile_geometry.argtypes = [_INT]
+    L.spc_conv_tile_geometry.argtypes = [_INT, _INT, _I64, _I64, _I64, _I64, _I64, _INT]
     L.spc_map_build_noalloc.argtypes = [_P, _P, _I64, _I32, _U32, _P, _P, _P, _P, _P]
     L.spc_layernorm_mod_silu.argtypes = [_P, _INT, _P, _I64, _I64, ctypes.c_float, _P, _P, _P,
                                          _I64, _P]
@@ -403,6 +405,17 @@ def pack_weights(weight: torch.Tensor, w_scale: torch.Tensor | None = None, *,
 
 
 TILES_AUTO, TILES_WIDE, TILES_SMALL = 0, 1, 2
+PLAN_WIDE, PLAN_SMALL = 1, 2
+
+
+def plan_section(dtype: torch.dtype, *, ntaps: int, n_out: int, cin: int, cout: int,
+                 q8: bool = False, class_rows: int = 0, epi_mode: int = 0) -> int:
+    """The plan section (PLAN_WIDE / PLAN_SMALL) a packed-weight conv with
+    these arguments reads (spc_conv_tile_geometry)."""
+    dt = dtype_code(dtype)
+    g = lib().spc_conv_tile_geometry(dt, Q8_0 if q8 else dt, ntaps, n_out, cin, cout,
+                                     class_rows, epi_mode)
+    return PLAN_SMALL if g == TILES_SMALL else PLAN_WIDE
 
 
 def set_tile_geometry(geometry: int) -> None:
@@ -414,9 +427,11 @@ def set_tile_geometry(geometry: int) -> None:
 
 def conv_plan(idx: torch.Tensor | None, *, ntaps: int, n_out: int, n_in: int | None = None,
               idx_layout: int = IDX_TOKEN_MAJOR,
-              row_perm: torch.Tensor | None = None, device=None) -> torch.Tensor:
-    """spc_conv_plan: the conv kernel's per-tile setup for this index table
-    (reusable by every conv over it)."""
+              row_perm: torch.Tensor | None = None, device=None,
+              sections: int = PLAN_WIDE | PLAN_SMALL) -> torch.Tensor:
+    """spc_conv_plan_sections: the conv kernel's per-tile setup for this
+    index table (reusable by every conv over it), for the tile geometries in
+    `sections` (a conv whose geometry finds no plan sets its tiles up)."""
     _need_gpu(idx, row_perm)
     dev = idx.device if idx is not None else device
     if dev is None or torch.device(dev).type != "cuda":
@@ -425,8 +440,8 @@ def conv_plan(idx: torch.Tensor | None, *, ntaps: int, n_out: int, n_in: int | N
     L = lib()
     nbytes = L.spc_conv_plan_bytes(n_out, ntaps)
     plan = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
-    st = L.spc_conv_plan(_stream(dev), _ptr(idx), idx_layout, _ptr(row_perm), ntaps, n_out, n_in,
-                         _ptr(plan), nbytes)
+    st = L.spc_conv_plan_sections(_stream(dev), _ptr(idx), idx_layout, _ptr(row_perm), ntaps,
+                                  n_out, n_in, int(sections), _ptr(plan), nbytes)
     _check("spc_conv_plan", st)
     return plan
 

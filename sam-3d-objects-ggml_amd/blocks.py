@@ -27,7 +27,7 @@ import torch.nn as nn
 
 from . import _native as nat
 from .sparse import (SparseConv3d, SparseDownsample, SparseGroupNorm32, SparseLinear, SparseSiLU,
-                     SparseSubdivide, SparseTensor, SparseUpsample, _run, _subm_map,
+                     SparseSubdivide, SparseTensor, SparseUpsample, _pad32, _run, _subm_map,
                      batch_offsets, max_item_rows)
 
 __all__ = ["LayerNorm32", "SparseResBlock3d", "SparseSubdivideBlock3d"]
@@ -202,10 +202,15 @@ class SparseSubdivideBlock3d(nn.Module):
         n_par = x.feats.shape[0]
         pm = _subm_map(x).token_major
         cm = nat.subdivide_neighbors(pm, n_par)
-        c1 = conv1.conv
+        c1, c2 = conv1.conv, conv2.conv
+        dt = x.feats.dtype
+        # the plans are rebuilt per call: only the tile geometry each conv runs
         if self.merged_taps and c1.in_channels % 32 == 0 and c1.out_channels % 32 == 0:
             idx8, perm, crows = nat.subdivide_tap_classes(pm, n_par)
-            plan8 = nat.conv_plan(idx8, ntaps=8, n_out=8 * crows, n_in=n_par, row_perm=perm)
+            plan8 = nat.conv_plan(idx8, ntaps=8, n_out=8 * crows, n_in=n_par, row_perm=perm,
+                                  sections=nat.plan_section(
+                                      dt, ntaps=8, n_out=8 * crows, cin=c1.in_channels,
+                                      cout=c1.out_channels, class_rows=crows))
             hp = h_par.detach()
             y1 = _run(lambda: nat.sparse_conv(
                 hp, self._merged_weights(hp.dtype, hp.device), conv1._bias_operand(hp.dtype, hp.device),
@@ -213,10 +218,17 @@ class SparseSubdivideBlock3d(nn.Module):
                 n_classes=8)[:nc], h_par, c1.weight, c1.bias)
         else:
             composed = nat.compose_rows(cm.token_major, parent)
-            plan1 = nat.conv_plan(composed, ntaps=27, n_out=nc, n_in=n_par)
+            plan1 = nat.conv_plan(composed, ntaps=27, n_out=nc, n_in=n_par,
+                                  sections=nat.plan_section(dt, ntaps=27, n_out=nc,
+                                                            cin=_pad32(c1.in_channels),
+                                                            cout=_pad32(c1.out_channels)))
             y1 = conv1._conv(h_par, composed, nc, plan1)
         h = self.sub.assemble(x, coords, y1)
         h.data.cached("subm3", lambda c: cm)  # conv2's map: the same child coordinates
+        h.data.cached(("plan", "subm3"), lambda c: nat.conv_plan(
+            cm.token_major, ntaps=27, n_out=nc, device=c.device, sections=nat.plan_section(
+                dt, ntaps=27, n_out=nc, cin=_pad32(c2.in_channels), cout=_pad32(c2.out_channels),
+                epi_mode=nat.EPI_RESIDUAL)))
         h = h.replace(nat.group_norm_silu(h.feats, 8 * offs, gn1.num_groups, gn1.weight, gn1.bias,
                                           gn1.eps, silu=True, max_rows=8 * rows_max))
         # the skip on the parent rows (a 1x1x1 conv is row-wise), added to

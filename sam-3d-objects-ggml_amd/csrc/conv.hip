@@ -13,6 +13,13 @@ namespace {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// Clears the marker of `tiles` plan tiles (a section its builder skipped):
+// convs over them set their tiles up themselves.
+__global__ void plan_unmark_kernel(char* plan, int64_t tiles, int64_t tile_bytes) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t < tiles) reinterpret_cast<int32_t*>(plan + t * tile_bytes)[3] = 0;
+}
+
 template <typename T, bool Q8>
 size_t packed_quant_bytes(int64_t ntaps, int64_t cin, int64_t cout) {
     return (size_t)ntaps * cin * cout * Panel<T, Q8>::WB;
@@ -303,6 +310,13 @@ size_t spc_conv_plan_bytes(int64_t n_out, int64_t ntaps) {
 int spc_conv_plan(spc_stream_t stream, const int32_t* idx, int idx_layout,
                   const int32_t* row_perm, int64_t ntaps, int64_t n_out, int64_t n_in, void* plan,
                   size_t plan_bytes) {
+    return spc_conv_plan_sections(stream, idx, idx_layout, row_perm, ntaps, n_out, n_in,
+                                  SPC_PLAN_WIDE | SPC_PLAN_SMALL, plan, plan_bytes);
+}
+
+int spc_conv_plan_sections(spc_stream_t stream, const int32_t* idx, int idx_layout,
+                           const int32_t* row_perm, int64_t ntaps, int64_t n_out, int64_t n_in,
+                           uint32_t sections, void* plan, size_t plan_bytes) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     if ((ntaps != 27 && ntaps != 8 && ntaps != 1) || n_out < 0 || n_in < 0 ||
         n_out > INT32_MAX || n_in > INT32_MAX) {
@@ -312,8 +326,10 @@ int spc_conv_plan(spc_stream_t stream, const int32_t* idx, int idx_layout,
     }
     if (n_out == 0) return SPC_OK;
     if ((!idx && (ntaps != 1 || n_in != n_out)) || !plan || ((uintptr_t)plan & 255u) != 0 ||
-        (idx_layout != SPC_IDX_TOKEN_MAJOR && idx_layout != SPC_IDX_OFFSET_MAJOR)) {
-        set_last_error("spc_conv_plan: null / misaligned (256 bytes) pointer or bad layout");
+        (idx_layout != SPC_IDX_TOKEN_MAJOR && idx_layout != SPC_IDX_OFFSET_MAJOR) ||
+        (sections & ~(SPC_PLAN_WIDE | SPC_PLAN_SMALL)) != 0) {
+        set_last_error("spc_conv_plan: null / misaligned (256 bytes) pointer, bad layout or "
+                       "unknown section bits");
         return SPC_BAD_ARG;
     }
     if (plan_bytes < spc_conv_plan_bytes(n_out, ntaps)) {
@@ -327,19 +343,30 @@ int spc_conv_plan(spc_stream_t stream, const int32_t* idx, int idx_layout,
     a.n_in = n_in;
     a.idx_layout = idx_layout;
     a.ntaps = (int32_t)ntaps;
-    // the wide tiles' plans, then the small tiles' (a conv uses one of them)
+    // the wide tiles' plans, then the small tiles'; a section not asked for
+    // has its tiles' markers cleared (its convs set their tiles up themselves)
     char* pl = static_cast<char*>(plan);
     char* ps = pl + plan_wide_bytes(n_out, (int)ntaps);
-    const unsigned gw = (unsigned)ceil_div(n_out, GeoWide::TM);
+    auto section = [&](auto ntaps_c, auto geo_c, char* base, bool build) {
+        constexpr int NT_ = decltype(ntaps_c)::value;
+        using G = decltype(geo_c);
+        const int64_t tiles = ceil_div(n_out, G::TM);
+        if (build)
+            conv_plan_kernel<NT_, G><<<(unsigned)tiles, 512, 0, s>>>(a, base);
+        else
+            plan_unmark_kernel<<<(unsigned)ceil_div(tiles, 256), 256, 0, s>>>(
+                base, tiles, G::plan_tile_bytes(NT_));
+    };
+    const bool w = sections & SPC_PLAN_WIDE, sm = sections & SPC_PLAN_SMALL;
     if (ntaps == 27) {
-        conv_plan_kernel<27, GeoWide><<<gw, 512, 0, s>>>(a, pl);
-        conv_plan_kernel<27, GeoSmall<27>><<<(unsigned)ceil_div(n_out, GeoSmall<27>::TM), 512, 0, s>>>(a, ps);
+        section(std::integral_constant<int, 27>{}, GeoWide{}, pl, w);
+        section(std::integral_constant<int, 27>{}, GeoSmall<27>{}, ps, sm);
     } else if (ntaps == 8) {
-        conv_plan_kernel<8, GeoWide><<<gw, 512, 0, s>>>(a, pl);
-        conv_plan_kernel<8, GeoSmall<8>><<<(unsigned)ceil_div(n_out, GeoSmall<8>::TM), 512, 0, s>>>(a, ps);
+        section(std::integral_constant<int, 8>{}, GeoWide{}, pl, w);
+        section(std::integral_constant<int, 8>{}, GeoSmall<8>{}, ps, sm);
     } else {
-        conv_plan_kernel<1, GeoWide><<<gw, 512, 0, s>>>(a, pl);
-        conv_plan_kernel<1, GeoSmall<1>><<<(unsigned)ceil_div(n_out, GeoSmall<1>::TM), 512, 0, s>>>(a, ps);
+        section(std::integral_constant<int, 1>{}, GeoWide{}, pl, w);
+        section(std::integral_constant<int, 1>{}, GeoSmall<1>{}, ps, sm);
     }
     SPC_HIP(hipGetLastError());
     return SPC_OK;
@@ -518,6 +545,30 @@ int spc_sparse_conv_classes(spc_stream_t stream, int dtype, const void* x, const
     }
     return conv_entry(stream, dtype, x, dtype, SPC_W_PACKED, w, nullptr, bias, y, idx, idx_layout,
                       row_perm, plan, ntaps, n_out, n_in, cin, cout, class_rows, n_classes, epi);
+}
+
+int spc_conv_tile_geometry(int dtype, int w_dtype, int64_t ntaps, int64_t n_out, int64_t cin,
+                           int64_t cout, int64_t class_rows, int epi_mode) {
+    ConvArgs a{};
+    a.n_out = n_out;
+    a.ntaps = (int32_t)ntaps;
+    a.cin = (int32_t)cin;
+    a.cout = (int32_t)cout;
+    a.class_rows = class_rows;
+    a.epi_mode = epi_mode;
+    a.num_cu = device_cu_count();
+    a.geometry = geometry_override();
+    bool small = false;
+    auto pick = [&](auto t_c, auto q8_c) {
+        using T = decltype(t_c);
+        constexpr bool Q8 = decltype(q8_c)::value;
+        if (ntaps == 27) small = use_small_tiles<T, Q8, true, 27>(a);
+        else if (ntaps == 8) small = use_small_tiles<T, Q8, true, 8>(a);
+    };
+    if (w_dtype == SPC_Q8_0) pick(__bf16{}, std::true_type{});
+    else if (dtype == SPC_F32) pick(float{}, std::false_type{});
+    else pick(__bf16{}, std::false_type{});  // bf16 and f16: 2-byte rows
+    return small ? SPC_TILES_SMALL : SPC_TILES_WIDE;
 }
 
 int spc_conv_set_tile_geometry(int geometry) {

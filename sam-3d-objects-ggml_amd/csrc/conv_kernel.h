@@ -221,6 +221,7 @@ __device__ __forceinline__ int slot_key(int r) { return r * kPitch; }
 __device__ __forceinline__ int seg_pos(int r, int s) { return r * kPitch + s; }
 
 constexpr int kTapWords = 8;  // step taps, four per word: up to 28 steps per chunk
+constexpr int32_t kPlanMagic = 0x314e4c50;  // header word 3 of every built plan tile
 
 // Shared-memory arrays of one tile's setup.
 struct TileLds {
@@ -517,7 +518,8 @@ __global__ __launch_bounds__(512) void conv_plan_kernel(ConvArgs a, char* plan) 
     int32_t* hdr = reinterpret_cast<int32_t*>(pt);
     const int U = misc[3];
     const int tid = threadIdx.x;
-    if (tid < 8) hdr[tid] = tid == 0 ? U : tid == 1 ? misc[0] : tid == 2 ? misc[4] : 0;
+    if (tid < 8)
+        hdr[tid] = tid == 0 ? U : tid == 1 ? misc[0] : tid == 2 ? misc[4] : tid == 3 ? kPlanMagic : 0;
     else if (tid < 16) hdr[tid] = (int32_t)tlw[tid - 8];
     for (int i = tid; i < TM; i += 512) reinterpret_cast<int32_t*>(pt + GEO::PLAN_SROW)[i] = srow[i];
     if (misc[4]) {
@@ -596,6 +598,7 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
     uint32_t tile_mask;
     int U;
     bool fast;
+    bool planned = false;
     if (a.plan) {
         // the tile's setup from the plan: one batch of 16-byte copies of the
         // whole plan tile (header, tap words, output rows, union rows, slot
@@ -630,19 +633,20 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
             *dst = pv[k];
         }
         lds_barrier();
+        // a tile of a section the plan's builder skipped has no marker: set it up here
+        planned = misc[3] == kPlanMagic;
         U = misc[0];
         tile_mask = (uint32_t)misc[1];
         fast = misc[2] != 0;
-    } else {
-        if constexpr (kWinWords % NT == 0) {
-            const TileLds L{reinterpret_cast<uint32_t*>(Au), sidx, tlw, urow, srow, wsum, misc};
-            tile_setup<NTAPS, NT, PD, GEO>(a, r0, L);
-            tile_mask = (uint32_t)misc[0];
-            U = misc[3];
-            fast = misc[4] != 0;
-        } else {
-            return;  // wave counts that do not divide the setup are launched with a plan only
-        }
+    }
+    if (!planned) {
+        // tile_setup writes misc[3] only after its first barriers, once every
+        // thread has read the marker above
+        const TileLds L{reinterpret_cast<uint32_t*>(Au), sidx, tlw, urow, srow, wsum, misc};
+        tile_setup<NTAPS, NT, PD, GEO>(a, r0, L);
+        tile_mask = (uint32_t)misc[0];
+        U = misc[3];
+        fast = misc[4] != 0;
     }
     // tile-uniform values: keep them (and the control flow they drive) scalar
     U = __builtin_amdgcn_readfirstlane(U);

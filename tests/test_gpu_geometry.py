@@ -228,3 +228,38 @@ def test_weight_classes_small(spc, orc, dev, geo):
 
     yw, ys = _both(nat, run)
     assert torch.equal(yw, ys)
+
+
+def test_plan_sections(spc, orc, dev, geo):
+    """A plan built for one geometry only (spc_conv_plan_sections): convs of
+    either geometry over it equal the convs over a full plan -- the skipped
+    section's tiles carry no marker, so those convs set their tiles up
+    themselves; spc_conv_tile_geometry names the section a conv reads."""
+    import torch
+
+    nat = geo
+    coords = spc.workloads.ellipsoid_batch(2, seed=12)
+    n = coords.shape[0]
+    _case(f"plan sections N={n} 64->64")
+    _, (x, w, b) = _inputs(spc, orc, n, 64, 64, 27, seed=13)
+    m = nat.map_build(torch.from_numpy(coords).to(dev))
+    pw = nat.pack_weights(w)
+    full = nat.conv_plan(m.token_major, ntaps=27, n_out=n)
+    outs = {}
+    for g in (nat.TILES_WIDE, nat.TILES_SMALL):
+        nat.set_tile_geometry(g)
+        want = nat.PLAN_WIDE if g == nat.TILES_WIDE else nat.PLAN_SMALL
+        assert nat.plan_section(torch.bfloat16, ntaps=27, n_out=n, cin=64, cout=64) == want
+        for sec in (nat.PLAN_WIDE, nat.PLAN_SMALL, nat.PLAN_WIDE | nat.PLAN_SMALL):
+            p = nat.conv_plan(m.token_major, ntaps=27, n_out=n, sections=sec)
+            outs[(g, sec)] = nat.sparse_conv(x, pw, b, m.token_major, ntaps=27, n_out=n, plan=p)
+        outs[(g, 0)] = nat.sparse_conv(x, pw, b, m.token_major, ntaps=27, n_out=n, plan=full)
+    nat.set_tile_geometry(nat.TILES_AUTO)
+    torch.cuda.synchronize()
+    ref = outs[(nat.TILES_WIDE, 0)]
+    for k, v in outs.items():
+        assert torch.equal(v, ref), k
+    # by shape: C=64 bf16 is one or two channel chunks -> small tiles
+    assert nat.plan_section(torch.bfloat16, ntaps=27, n_out=n, cin=64, cout=64) == nat.PLAN_SMALL
+    assert nat.plan_section(torch.bfloat16, ntaps=27, n_out=n, cin=128, cout=128) == nat.PLAN_WIDE
+    assert nat.plan_section(torch.bfloat16, ntaps=8, n_out=n, cin=128, cout=128) == nat.PLAN_SMALL
