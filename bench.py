@@ -59,6 +59,8 @@ def parse():
                     help="only time a 256 MiB device copy (PMC traffic calibration)")
     ap.add_argument("--tiles", choices=["auto", "wide", "small"], default="auto",
                     help="conv tile geometry (auto: each conv picks by shape)")
+    ap.add_argument("--bf16-weights", action="store_true",
+                    help="config 5: the same conv with bf16 weights (no Q8_0 dequantisation)")
     return ap.parse_args()
 
 
@@ -367,6 +369,17 @@ def main():
             w_bytes = wf.nbytes
             es = 4
         elif cfg in (2, 0):
+            x, xb = bf16_dev(orc, xf, dev)
+            w, wb = bf16_dev(orc, wf, dev)
+            b, bb = bf16_dev(orc, bf, dev)
+            call = ConvCall(nat, x, nat.pack_weights(w), b, y, idx, ntaps=27, n_out=n,
+                            layout=layout, perm=perm, plan=plan)
+            dtype = "bf16"
+            peak = PEAK_BF16_TFLOPS
+            cpu_dt = (oracle.BF16, oracle.BF16)
+            w_bytes = wb.nbytes
+            es = 2
+        elif args.bf16_weights:  # config 5's shape with bf16 weights: the dequant's cost
             x, xb = bf16_dev(orc, xf, dev)
             w, wb = bf16_dev(orc, wf, dev)
             b, bb = bf16_dev(orc, bf, dev)
