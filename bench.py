@@ -61,6 +61,9 @@ def parse():
                     help="conv tile geometry (auto: each conv picks by shape)")
     ap.add_argument("--bf16-weights", action="store_true",
                     help="config 5: the same conv with bf16 weights (no Q8_0 dequantisation)")
+    ap.add_argument("--q8-in-registers", action="store_true",
+                    help="config 5: dequantise Q8_0 in the conv's registers (once per row tile) "
+                         "instead of expanding the packed weights once per step")
     return ap.parse_args()
 
 
@@ -76,12 +79,21 @@ class ConvCall:
     overhead per step at a single ctypes call)."""
 
     def __init__(self, nat, x, w, bias, y, idx, *, ntaps, n_out, layout, perm=None,
-                 w_scale=None, wdt=None, plan=None):
+                 w_scale=None, wdt=None, plan=None, expand_q8=False):
         import torch
 
         self.fn = nat.lib().spc_sparse_conv_plan
         self.stream = torch.cuda.current_stream().cuda_stream
         dt = nat.dtype_code(x.dtype)
+        self.expand = None
+        if expand_q8:
+            # each step: packed Q8_0 -> packed bf16 (one HBM pass), then the
+            # bf16 conv on the expansion
+            wx = nat.expand_q8_0(w)
+            self.expand = (nat.lib().spc_conv_expand_q8_0,
+                           (self.stream, w.data.data_ptr(), w.ntaps, w.cin, w.cout,
+                            wx.data.data_ptr()))
+            w = wx
         if isinstance(w, nat.PackedWeights):
             wd, layout_w, wptr, sptr = w.w_dtype, nat.W_PACKED, w.data.data_ptr(), None
         else:
@@ -96,6 +108,10 @@ class ConvCall:
         self.nat = nat
 
     def __call__(self):
+        if self.expand is not None:
+            st = self.expand[0](*self.expand[1])
+            if st != 0:
+                self.nat._check("spc_conv_expand_q8_0", st)
         st = self.fn(*self.args)
         if st != 0:
             self.nat._check("spc_sparse_conv", st)
@@ -396,7 +412,8 @@ def main():
             blocks = orc.q8_0_quantize(wf)
             qs, dsc = nat.q8_0_repack(torch.from_numpy(blocks).to(dev))
             call = ConvCall(nat, x, nat.pack_weights(qs, dsc, cin=cin, cout=cout), b, y, idx,
-                            ntaps=27, n_out=n, layout=layout, perm=perm, plan=plan)
+                            ntaps=27, n_out=n, layout=layout, perm=perm, plan=plan,
+                            expand_q8=not args.q8_in_registers)
             dtype = "bf16 x Q8_0"
             peak = PEAK_BF16_TFLOPS
             wb = orc.q8_0_dequant(blocks, oracle.F16)
@@ -432,6 +449,9 @@ def main():
                          "kernel": "conv_kernel (gather -> MFMA implicit GEMM -> store)",
                          "algorithmic_flops_per_launch": flops},
         }
+        if cfg == 5 and not args.bf16_weights:
+            result["config"]["q8_path"] = ("dequant in registers" if args.q8_in_registers else
+                                           "expand to packed bf16 + bf16 conv, both timed")
         if cfg == 2:
             result["single_shell"] = bench_single_shell(nat, wl, orc, dev, args)
         if dtype == "bf16":

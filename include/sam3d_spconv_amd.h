@@ -318,6 +318,18 @@ int spc_conv_pack_weights(spc_stream_t stream, int w_dtype, int w_layout, const 
                           const void* w_scale, int64_t ntaps, int64_t cin, int64_t cout,
                           void* packed);
 
+/* Packed Q8_0 weights (spc_conv_pack_weights with SPC_Q8_0) -> packed bf16
+ * weights (spc_conv_packed_bytes(SPC_BF16, ...) bytes, 16-byte aligned)
+ * holding bf16(f32(d) * q) per weight: the values the Q8_0 conv feeds its
+ * MFMAs, so spc_sparse_conv with (SPC_BF16, SPC_W_PACKED, packed_bf16) is
+ * bit-identical to (SPC_Q8_0, SPC_W_PACKED, packed_q8).  The dequant cast
+ * the reference runs before each Q8_0 conv GEMM (as_f16,
+ * SRC/slat_flow_graph.cpp:24-27), as one HBM pass: a conv over many row
+ * tiles (the in-register path dequantises every weight once per tile)
+ * runs faster as expand + bf16 conv. */
+int spc_conv_expand_q8_0(spc_stream_t stream, const void* packed_q8, int64_t ntaps, int64_t cin,
+                         int64_t cout, void* packed_bf16);
+
 /* Drop-in for the reference's spconv bridge (same name, arguments and
  * layouts as cpp_ggml/third_party/sam3d-spconv/include/
  * sam3d_spconv_bridge.cuh:10-21, called from PATCH:2033-2038): f16

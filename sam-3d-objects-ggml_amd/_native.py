@@ -85,6 +85,7 @@ def lib() -> ctypes.CDLL:
     L.spc_conv_packed_bytes.restype = _SZ
     L.spc_conv_packed_bytes.argtypes = [_INT, _I64, _I64, _I64]
     L.spc_conv_pack_weights.argtypes = [_P, _INT, _INT, _P, _P, _I64, _I64, _I64, _P]
+    L.spc_conv_expand_q8_0.argtypes = [_P, _P, _I64, _I64, _I64, _P]
     L.sam3d_spconv_f16_forward.argtypes = [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64]
     L.sam3d_spconv_f16_forward.restype = None
     L.spc_q8_0_repack.argtypes = [_P, _P, _I64, _P, _P]
@@ -402,6 +403,27 @@ def pack_weights(weight: torch.Tensor, w_scale: torch.Tensor | None = None, *,
                                  _ptr(w_scale), ntaps, cin, cout, _ptr(out))
     _check("spc_conv_pack_weights", st)
     return PackedWeights(out, wdt, ntaps, cin, cout)
+
+
+def expand_q8_0(packed: PackedWeights, out: torch.Tensor | None = None) -> PackedWeights:
+    """Packed Q8_0 weights -> packed bf16 weights of bf16(f32(d) * q)
+    (spc_conv_expand_q8_0): a bf16 conv on them is bit-identical to the Q8_0
+    conv, and faster over many row tiles (each weight dequantised once
+    instead of once per tile).  `out` (uint8, the packed bf16 size) is
+    reused when given."""
+    if packed.w_dtype != Q8_0:
+        raise ValueError("expand_q8_0 takes packed Q8_0 weights")
+    _need_gpu(packed.data, out)
+    L = lib()
+    nbytes = L.spc_conv_packed_bytes(BF16, packed.ntaps, packed.cin, packed.cout)
+    if out is None:
+        out = torch.empty(nbytes, dtype=torch.uint8, device=packed.data.device)
+    elif out.dtype != torch.uint8 or out.numel() < nbytes or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous uint8 tensor of >= {nbytes} bytes")
+    st = L.spc_conv_expand_q8_0(_stream(out.device), _ptr(packed.data), packed.ntaps,
+                                packed.cin, packed.cout, _ptr(out))
+    _check("spc_conv_expand_q8_0", st)
+    return PackedWeights(out, BF16, packed.ntaps, packed.cin, packed.cout)
 
 
 TILES_AUTO, TILES_WIDE, TILES_SMALL = 0, 1, 2

@@ -91,6 +91,26 @@ __global__ void pack_scales_kernel(const uint16_t* __restrict__ d, float* __rest
     out[id] = f16_bits_to_f32(d[(co * st.co + o * st.o + (int64_t)kc * 32) >> 5]);
 }
 
+// Packed Q8_0 panels -> packed bf16 panels of the same (tap, chunk, c32)
+// order.  A Q8_0 panel holds one 16-byte word per lane (both k-steps of
+// the chunk), a bf16 panel two (one per k-step); the f32 scale of lane l
+// is that of output channel 32 c32 + l % 32.  One thread per panel lane:
+// 16 quant bytes and a scale in, 32 bytes out, all coalesced.
+__global__ void expand_q8_0_kernel(const u32x4* __restrict__ q, const float* __restrict__ sc,
+                                   u32x4* __restrict__ out, int64_t panels, int ncol32,
+                                   int cout) {
+    const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= panels * 64) return;
+    const int lane = (int)(id & 63);
+    const int64_t p = id >> 6;
+    const int64_t tk = p / ncol32;  // tap * chunks + chunk
+    const int c32 = (int)(p - tk * ncol32);
+    const float d = sc[tk * cout + c32 * 32 + (lane & 31)];
+    const u32x4 w = q[id];
+    out[p * 128 + lane] = __builtin_bit_cast(u32x4, q8_dequant8(w.x, w.y, d));
+    out[p * 128 + 64 + lane] = __builtin_bit_cast(u32x4, q8_dequant8(w.z, w.w, d));
+}
+
 __global__ void q8_0_repack_kernel(const uint8_t* __restrict__ blocks, int64_t nblocks,
                                    int8_t* __restrict__ qs, uint16_t* __restrict__ d) {
     const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -298,6 +318,26 @@ int spc_conv_pack_weights(spc_stream_t stream, int w_dtype, int w_layout, const 
             set_last_error("spc_conv_pack_weights: unknown dtype %d", w_dtype);
             return SPC_BAD_ARG;
     }
+    SPC_HIP(hipGetLastError());
+    return SPC_OK;
+}
+
+int spc_conv_expand_q8_0(spc_stream_t stream, const void* packed_q8, int64_t ntaps, int64_t cin,
+                         int64_t cout, void* packed_bf16) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int st = check_shape("spc_conv_expand_q8_0", ntaps, cin, cout, true);
+    if (st != SPC_OK) return st;
+    if (!packed_q8 || !packed_bf16 || !aligned16(packed_q8) || !aligned16(packed_bf16)) {
+        set_last_error("spc_conv_expand_q8_0: null / misaligned pointer");
+        return SPC_BAD_ARG;
+    }
+    const size_t qbytes = packed_quant_bytes<__bf16, true>(ntaps, cin, cout);
+    const int64_t panels = (int64_t)qbytes / 1024;
+    const float* sc =
+        reinterpret_cast<const float*>(static_cast<const char*>(packed_q8) + align_up(qbytes, 256));
+    expand_q8_0_kernel<<<(unsigned)ceil_div(panels * 64, 256), 256, 0, s>>>(
+        static_cast<const u32x4*>(packed_q8), sc, static_cast<u32x4*>(packed_bf16), panels,
+        (int)(cout / 32), (int)cout);
     SPC_HIP(hipGetLastError());
     return SPC_OK;
 }

@@ -156,6 +156,26 @@ struct Panel {
     static_assert(KS % G == 0, "panel geometry");
 };
 
+// Q8_0 dequantisation of one k-step's 8 quants (byte e of lo, hi = quant
+// e, e+4) with block scale d: bf16(d * q), rounded to nearest even.  The
+// bytes are biased to unsigned (u = q + 128, one xor per word) so each
+// converts with a single unsigned-byte convert; fma(d, u, -128 d) is exactly
+// d * q (d is an fp16 value and |q| <= 127, so every intermediate is exact in
+// F32).  The conv's in-register path and the panel expander both use it, so
+// they agree bit for bit.
+__device__ __forceinline__ bf16x8 q8_dequant8(uint32_t lo, uint32_t hi, float d) {
+    lo ^= 0x80808080u;
+    hi ^= 0x80808080u;
+    const float nb = -128.0f * d;
+    bf16x8 f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint32_t word = e < 4 ? lo : hi;
+        f[e] = (__bf16)__builtin_fmaf(d, (float)((word >> (8 * (e & 3))) & 0xffu), nb);
+    }
+    return f;
+}
+
 constexpr int kWinWords = 1024; // dedupe bitmap: 32768 source rows
 constexpr int kHashBits = 11;    // wider spans: LDS hash of the tile's source rows
 constexpr int kHashSlots = 1 << kHashBits;  // 64-bit slots: row | rank << 32
@@ -753,20 +773,9 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
         typename M::frag f;
         const u32x4 wv4 = sl.q[j][ks / P::G];
         if constexpr (Q8) {
-            // 8 int8 quants of this k-step -> bf16(d * q), rounded to nearest
-            // even.  The bytes are biased to unsigned (u = q + 128, one xor
-            // per word) so each converts with a single unsigned-byte convert;
-            // fma(d, u, -128 d) is exactly d * q (d is an fp16 value and
-            // |q| <= 127, so every intermediate is exact in F32).
-            const uint32_t lo32 = ((ks % P::G) == 0 ? wv4.x : wv4.z) ^ 0x80808080u;
-            const uint32_t hi32 = ((ks % P::G) == 0 ? wv4.y : wv4.w) ^ 0x80808080u;
-            const float d = sl.d[j];
-            const float nb = -128.0f * d;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const uint32_t word = e < 4 ? lo32 : hi32;
-                f[e] = (__bf16)__builtin_fmaf(d, (float)((word >> (8 * (e & 3))) & 0xffu), nb);
-            }
+            // 8 int8 quants of this k-step -> bf16(d * q)
+            f = q8_dequant8((ks % P::G) == 0 ? wv4.x : wv4.z, (ks % P::G) == 0 ? wv4.y : wv4.w,
+                            sl.d[j]);
         } else if constexpr (P::G == 1) {
             f = __builtin_bit_cast(typename M::frag, wv4);
         } else {
@@ -1285,7 +1294,8 @@ hipError_t launch_conv(hipStream_t s, ConvArgs a) {
 // workgroups per CU, two at TN = 128): TN = largest of {128, 64, 32} dividing cout, halved
 // while the narrower tiles still fit on the device in one round; waves 2 x 2
 // (64 x 64 / 64 x 32 wave tiles; 32 x 64 / 32 x 32 for 64-row tiles), 4 x 1
-// (32 x 32) at TN = 32, 2 x 1 for 64-row tiles.
+// (32 x 32) at TN = 32, 2 x 1 for 64-row tiles; 1 x 4 (128 x 32) for Q8_0
+// at TN = 128.
 template <typename T, bool Q8, bool PACKED, int NTAPS>
 hipError_t dispatch_small(hipStream_t s, const ConvArgs& a) {
     using G = GeoSmall<NTAPS>;
@@ -1293,7 +1303,12 @@ hipError_t dispatch_small(hipStream_t s, const ConvArgs& a) {
     int tn = a.cout % 128 == 0 ? 128 : a.cout % 64 == 0 ? 64 : 32;
     while (tn > 32 && tiles_m * (a.cout / (tn / 2)) <= a.num_cu) tn /= 2;
     if (a.epi_mode == SPC_EPI_NORM_MOD_SILU) tn = a.cout;  // 32 or 64 here (one tile per row)
-    if (tn == 128) return launch_conv<T, Q8, PACKED, NTAPS, 128, 2, 2, G>(s, a);
+    if (tn == 128) {
+        // Q8_0: 4 waves of 128 x 32, so each in-register dequantised B
+        // fragment feeds four MFMAs and no two waves dequantise the same one
+        if constexpr (Q8 && G::TM == 128) return launch_conv<T, Q8, PACKED, NTAPS, 128, 1, 4, G>(s, a);
+        else return launch_conv<T, Q8, PACKED, NTAPS, 128, 2, 2, G>(s, a);
+    }
     if (tn == 64) return launch_conv<T, Q8, PACKED, NTAPS, 64, 2, 2, G>(s, a);
     if constexpr (G::TM == 128) return launch_conv<T, Q8, PACKED, NTAPS, 32, 4, 1, G>(s, a);
     else return launch_conv<T, Q8, PACKED, NTAPS, 32, 2, 1, G>(s, a);

@@ -460,6 +460,13 @@ class _ConvParams(nn.Module):
             nn.init.uniform_(self.bias, -bound, bound)
 
 
+# Q8_0 convs over at least this many output rows expand the packed quants
+# to packed bf16 once per forward (one HBM pass over the weights) and run
+# the bf16 kernel; smaller ones dequantise in registers, once per row tile.
+# Both give the same bits.
+Q8_EXPAND_MIN_ROWS = 2048
+
+
 class _ConvCore:
     """Weight packing (cached per weight version and dtype), Q8_0 weights
     and the kernel call shared by SparseConv3d and SparseInverseConv3d."""
@@ -566,6 +573,10 @@ class _ConvCore:
             if cin_p != c.in_channels:
                 x = torch.nn.functional.pad(x, (0, cin_p - c.in_channels))
             w = self._weight_operand(x.dtype, x.device)
+            if w.w_dtype == nat.Q8_0 and n_out >= Q8_EXPAND_MIN_ROWS:
+                # the per-forward dequant cast before the GEMM
+                # (SRC/slat_flow_graph.cpp:24-27) as one HBM pass
+                w = nat.expand_q8_0(w)
             b = self._bias_operand(x.dtype, x.device)
             r = None if residual is None else residual.detach().to(x.dtype)
             y = nat.sparse_conv(x, w, b, idx, ntaps=self._ntaps, n_out=n_out, plan=plan,

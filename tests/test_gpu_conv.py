@@ -223,8 +223,17 @@ def test_q8_0_config5_sphere(spc, orc, dev):
     pw = nat.pack_weights(qs, d, cin=c, cout=c)
     yp = nat.sparse_conv(to_dev_bf16(x, dev), pw, to_dev_bf16(b, dev), m.token_major, ntaps=27,
                          n_out=n)
+    # the per-forward expansion to packed bf16, then the bf16 conv: same bits
+    px = nat.expand_q8_0(pw)
+    yx = nat.sparse_conv(to_dev_bf16(x, dev), px, to_dev_bf16(b, dev), m.token_major, ntaps=27,
+                         n_out=n)
     torch.cuda.synchronize()
     assert torch.equal(y, yp)
+    assert torch.equal(y, yx)
+    # the expansion is the bf16 packing of the oracle's bf16(f32(d) * q)
+    wq_b = orc.q8_0_dequant(blocks, oracle.BF16).reshape(c, 27, c)
+    pb = nat.pack_weights(to_dev_bf16(wq_b, dev))
+    assert torch.equal(px.data, pb.data)
     tm = m.token_major.cpu().numpy()
     kw = dict(ntaps=27, n_out=n, idx_layout=1, out_dtype=oracle.F32, x_dtype=oracle.BF16,
               b_dtype=oracle.BF16, nthreads=oracle_threads(), blocked=True)
@@ -237,6 +246,32 @@ def test_q8_0_config5_sphere(spc, orc, dev):
     ref_b = orc.sparse_conv(x, orc.q8_0_dequant(blocks, oracle.BF16), b, tm,
                             w_dtype=oracle.BF16, **kw)
     check_16bit("config5 Q8_0 C=768 vs bf16(d*q) weights", got, ref_b)
+
+
+@pytest.mark.parametrize("ntaps,cin,cout,layout", [(27, 32, 32, "krsc"), (8, 64, 160, "krsc"),
+                                                   (1, 96, 64, "tck"), (27, 64, 96, "tck")])
+def test_q8_0_expand_matches_packing(spc, orc, dev, ntaps, cin, cout, layout):
+    """spc_conv_expand_q8_0 of packed Q8_0 weights == the bf16 packing of
+    the oracle's bf16(f32(d) * q), byte for byte (all-zero blocks
+    included)."""
+    import oracle
+    import torch
+
+    nat = spc._native
+    _case(f"q8_0 expand ntaps={ntaps} cin={cin} cout={cout} {layout}")
+    shape = (cout, ntaps, cin) if layout == "krsc" else (ntaps, cout, cin)
+    wf = spc.workloads.normal(shape, 0.05, seed=ntaps + cin + cout)
+    wf[0] = 0.0
+    blocks = orc.q8_0_quantize(wf)
+    qs, d = nat.q8_0_repack(torch.from_numpy(blocks).to(dev))
+    lay = nat.W_KRSC if layout == "krsc" else nat.W_TCK
+    pw = nat.pack_weights(qs, d, cin=cin, cout=cout, ntaps=ntaps, layout=lay)
+    px = nat.expand_q8_0(pw)
+    wq_b = orc.q8_0_dequant(blocks, oracle.BF16).reshape(shape)
+    pb = nat.pack_weights(to_dev_bf16(wq_b, dev), layout=lay)
+    torch.cuda.synchronize()
+    assert px.data.numel() == pb.data.numel()
+    assert torch.equal(px.data, pb.data)
 
 
 def test_stride2_conv(spc, orc, dev):

@@ -209,6 +209,17 @@ def test_q8_0_module(spc, orc, dev):
                           idx_layout=1, out_dtype=oracle.F32, x_dtype=oracle.BF16,
                           w_dtype=oracle.F16, b_dtype=oracle.BF16)
     assert max_rel(from_dev(y.feats), ref) <= MAXREL
+    # in-register dequant (n below the expansion threshold) and the
+    # per-forward expansion to packed bf16 give the same bits
+    assert n < sp.Q8_EXPAND_MIN_ROWS
+    saved = sp.Q8_EXPAND_MIN_ROWS
+    sp.Q8_EXPAND_MIN_ROWS = 0
+    try:
+        with torch.no_grad():
+            yx = conv(xt.replace(xt.feats))
+    finally:
+        sp.Q8_EXPAND_MIN_ROWS = saved
+    assert torch.equal(yx.feats, y.feats)
     # the mesh GGUF layout of the same quants gives the identical result
     conv_m = sp.SparseConv3d(64, 64, 3).to(dev)
     conv_m.load_state_dict(conv.state_dict())
