@@ -454,6 +454,7 @@ def main():
                                            "expand to packed bf16 + bf16 conv, both timed")
         if cfg == 2:
             result["single_shell"] = bench_single_shell(nat, wl, orc, dev, args)
+            result["bridge"] = bench_bridge(nat, wl, c_dev, dev, args)
         if dtype == "bf16":
             g = library_gemm_tflops(dev, torch.bfloat16)
             g["conv_fraction"] = tflops / g["tflops"]
@@ -551,6 +552,50 @@ def bench_single_shell(nat, wl, orc, dev, args) -> dict:
     return {"workload": "subm3x3x3 bf16 C=128, one sphere shell r=24 in 64^3", "n_voxels": n,
             "pairs": pairs, "ms": ms, "mvoxel_s": n / (ms / 1e3) / 1e6, "tflops": tf,
             "pct_peak": 100.0 * tf / PEAK_BF16_TFLOPS}
+
+
+def bench_bridge(nat, wl, c_dev, dev, args) -> dict:
+    """The drop-in spconv bridge (sam3d_spconv_f16_forward: f16, unpacked
+    KRSC weights packed on every call, offset-major indices, no tile plan)
+    on the headline rows and channels, beside the packed-weight f16 conv of
+    the same data without and with a tile plan.  Outputs are compared bit
+    for bit."""
+    import torch
+
+    n = c_dev.shape[0]
+    m = nat.map_build(c_dev)
+    x = torch.from_numpy(wl.normal((n, 128), 1.0, seed=121)).to(dev).half()
+    w = torch.from_numpy(wl.normal((128, 27, 128), 0.02, seed=122)).to(dev).half()
+    b = torch.from_numpy(wl.normal((128,), 0.01, seed=123)).to(dev).half()
+    y_bridge = torch.empty((n, 128), dtype=torch.float16, device=dev)
+    y_packed = torch.empty_like(y_bridge)
+    y_plan = torch.empty_like(y_bridge)
+    L = nat.lib()
+    s = torch.cuda.current_stream().cuda_stream
+    bargs = (s, x.data_ptr(), w.data_ptr(), b.data_ptr(), y_bridge.data_ptr(),
+             m.offset_major.data_ptr(), m.mask_sorted.data_ptr(), m.argsort.data_ptr(), n, 128,
+             128)
+
+    def bridge():
+        L.sam3d_spconv_f16_forward(*bargs)
+
+    pw = nat.pack_weights(w)
+    packed = ConvCall(nat, x, pw, b, y_packed, m.offset_major, ntaps=27, n_out=n,
+                      layout=nat.IDX_OFFSET_MAJOR)
+    planned = ConvCall(nat, x, pw, b, y_plan, m.token_major, ntaps=27, n_out=n,
+                       layout=nat.IDX_TOKEN_MAJOR, plan=m.plan())
+    ms_bridge, _ = time_gpu(bridge, args.steps, args.warmup)
+    err = L.spc_last_error().decode(errors="replace")
+    if err:
+        raise RuntimeError(f"sam3d_spconv_f16_forward: {err}")
+    ms_packed, _ = time_gpu(packed, args.steps, args.warmup)
+    ms_plan, _ = time_gpu(planned, args.steps, args.warmup)
+    torch.cuda.synchronize()
+    return {"workload": "sam3d_spconv_f16_forward, f16 C=128 -> 128 on the headline rows",
+            "bridge_ms": ms_bridge, "packed_ms": ms_packed, "packed_plan_ms": ms_plan,
+            "bridge_over_packed": ms_bridge / ms_packed,
+            "bit_identical": bool(torch.equal(y_bridge, y_packed) and
+                                  torch.equal(y_bridge, y_plan))}
 
 
 def bench_feature_ops(spc, nat, wl, orc, coords, c_dev, dev, args, workload) -> dict:

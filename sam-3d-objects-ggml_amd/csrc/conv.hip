@@ -2,8 +2,10 @@
 // argument checks, dispatch by dtype, the MFMA-fragment weight packer, the
 // Q8_0 block repacker and the reference-compatible spconv bridge.
 #include <atomic>
+#include <climits>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 
 #include "conv_kernel.h"
 
@@ -35,15 +37,15 @@ WStride weight_strides(int layout, int64_t ntaps, int64_t cin, int64_t cout) {
     return {ntaps * cin, cin, 1};  // SPC_W_KRSC
 }
 
-// One thread per 16-byte panel word: panel (tap, chunk, c32), word g, lane.
+// Panel word `id` (panel (tap, chunk, c32), word g, lane) of the packed
+// weights.
 template <typename T, bool Q8>
-__global__ void pack_weights_kernel(const uint8_t* __restrict__ w, u32x4* __restrict__ out,
-                                    int ntaps, int cin, int cout, WStride st) {
+__device__ __forceinline__ void pack_word(const uint8_t* __restrict__ w, u32x4* __restrict__ out,
+                                          int ntaps, int cin, int cout, WStride st, int64_t id) {
     using P = Panel<T, Q8>;
     const int kch = cin / P::KC;
     const int ncol32 = cout / 32;
     const int64_t words = (int64_t)ntaps * kch * ncol32 * P::NG * 64;
-    const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (id >= words) return;
     const int lane = (int)(id % 64);
     const int64_t rest = id / 64;
@@ -54,6 +56,16 @@ __global__ void pack_weights_kernel(const uint8_t* __restrict__ w, u32x4* __rest
     const int kc = (int)(tk % kch);
     const int o = (int)(tk / kch);
     const int co = c32 * 32 + (lane & 31);
+    if constexpr (!Q8 && sizeof(T) == 2) {
+        if (st.ci == 1 && ((uintptr_t)w & 15u) == 0) {
+            // the word's 8 channels are contiguous: one 16-byte load
+            // (16-byte aligned: cin and the chunk offsets are multiples of 8)
+            const int64_t el = co * st.co + o * st.o + (int64_t)kc * P::KC + g * P::KSUB +
+                               (lane >> 5) * P::EPL;
+            out[id] = *reinterpret_cast<const u32x4*>(w + el * 2);
+            return;
+        }
+    }
     uint8_t bytes[16];
 #pragma unroll
     for (int i = 0; i < P::G; ++i) {
@@ -73,6 +85,13 @@ __global__ void pack_weights_kernel(const uint8_t* __restrict__ w, u32x4* __rest
         v[h] = (uint32_t)bytes[4 * h] | ((uint32_t)bytes[4 * h + 1] << 8) |
                ((uint32_t)bytes[4 * h + 2] << 16) | ((uint32_t)bytes[4 * h + 3] << 24);
     out[id] = u32x4{v[0], v[1], v[2], v[3]};
+}
+
+// One thread per 16-byte panel word.
+template <typename T, bool Q8>
+__global__ void pack_weights_kernel(const uint8_t* __restrict__ w, u32x4* __restrict__ out,
+                                    int ntaps, int cin, int cout, WStride st) {
+    pack_word<T, Q8>(w, out, ntaps, cin, cout, st, (int64_t)blockIdx.x * blockDim.x + threadIdx.x);
 }
 
 // Q8_0 scales as f32 per (tap, chunk, co): a 32-channel chunk is one block
@@ -221,6 +240,113 @@ void* bridge_pack_addr() {
         cache[dev].store(p, std::memory_order_release);
     }
     return p;
+}
+
+// The bridge's self-refreshing tile plan, one per device: a plan buffer
+// for `n` tokens, a copy of the index table its tiles were built from and
+// one flag per (128 rows, tap).  Each call first flags the rows whose entries
+// differ from the copy (bridge_dirty_kernel); the conv runs flagged tiles
+// unplanned and writes their plan tiles and entries back, so repeated
+// calls over one index table (every conv of a coordinate set) skip the
+// tile setup.  Grown with hipMalloc when a call needs more rows, held until
+// the process ends; shared like bridge_pack.
+struct BridgePlan {
+    int32_t* idx = nullptr;
+    int32_t* dirty = nullptr;
+    void* plan = nullptr;
+    size_t idx_cap = 0;
+    size_t plan_cap = 0;
+    int64_t n = -1;
+    int geometry = -1;  // the tile geometry whose plan section the entries describe
+};
+
+__global__ void fill_i32_kernel(int32_t* p, int64_t n, int32_t v) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+// The bridge's per-call preparation in one launch: blocks [0, npack) pack
+// the KRSC f16 weights (one thread per panel word), the rest flag changed
+// index entries: dirty[27 f + o] = whether any offset-major entry (o, r) of
+// [27, n] with r in [128 f, 128 f + 128) differs from the cached copy.  A
+// flag block covers 256 rows, each thread one row across the 27 taps (all
+// 54 loads in flight at once).
+__global__ __launch_bounds__(256) void bridge_prep_kernel(
+    const uint8_t* __restrict__ w, u32x4* __restrict__ packed, int cin, int cout, WStride st,
+    int64_t npack, const int32_t* __restrict__ idx, const int32_t* __restrict__ cache, int64_t n,
+    int32_t* __restrict__ dirty) {
+    const int64_t b = blockIdx.x;
+    const int t = threadIdx.x;
+    if (b < npack) {
+        pack_word<__bf16, false>(w, packed, 27, cin, cout, st, b * 256 + t);
+        return;
+    }
+    if (!cache) return;
+    __shared__ int wd[27][4];
+    const int64_t f2 = b - npack;
+    const int64_t r = f2 * 256 + t;
+    int32_t va[27], vc[27];
+#pragma unroll
+    for (int o = 0; o < 27; ++o) {
+        va[o] = r < n ? idx[(int64_t)o * n + r] : 0;
+        vc[o] = r < n ? cache[(int64_t)o * n + r] : 0;
+    }
+#pragma unroll
+    for (int o = 0; o < 27; ++o) {
+        const uint64_t bal = __ballot(va[o] != vc[o]);
+        if ((t & 63) == 0) wd[o][t >> 6] = bal != 0;
+    }
+    __syncthreads();
+    if (t < 54) {
+        const int o = t % 27, h = t / 27;
+        const int64_t f = 2 * f2 + h;
+        if (f * 128 < n) dirty[f * 27 + o] = wd[o][2 * h] | wd[o][2 * h + 1];
+    }
+}
+
+// The current device's plan cache sized for n tokens (27 taps) and reset
+// when n or the tile geometry changes (the copy then describes no plan
+// tile), or null when it cannot be had (the call then runs without a plan).
+BridgePlan* bridge_plan(hipStream_t s, int64_t n, int geometry) {
+    static std::mutex mu;
+    static BridgePlan cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    BridgePlan& bp = cache[dev];
+    if (bp.n == n && bp.geometry == geometry) return &bp;
+    const size_t need_idx = (size_t)(n + (n + 127) / 128) * 27 * sizeof(int32_t);
+    const size_t need_plan = spc_conv_plan_bytes(n, 27);
+    if (need_plan == 0) return nullptr;
+    if (bp.idx_cap < need_idx || bp.plan_cap < need_plan) {
+        // hipFree waits for the work that may still read the old buffers
+        if (bp.idx) (void)hipFree(bp.idx);
+        if (bp.plan) (void)hipFree(bp.plan);
+        bp = BridgePlan{};
+        void* pi = nullptr;
+        void* pp = nullptr;
+        if (hipMalloc(&pi, need_idx) != hipSuccess || hipMalloc(&pp, need_plan) != hipSuccess) {
+            if (pi) (void)hipFree(pi);
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        bp.idx = static_cast<int32_t*>(pi);
+        bp.plan = pp;
+        bp.dirty = bp.idx + n * 27;
+        bp.idx_cap = need_idx;
+        bp.plan_cap = need_plan;
+    }
+    // entries no index equals: every tile of the first call sets itself up
+    const int64_t ne = n * 27;
+    fill_i32_kernel<<<(unsigned)ceil_div(ne, 256), 256, 0, s>>>(bp.idx, ne, INT_MIN);
+    if (hipGetLastError() != hipSuccess) return nullptr;
+    bp.dirty = bp.idx + n * 27;
+    bp.n = n;
+    bp.geometry = geometry;
+    return &bp;
 }
 
 // Tile-geometry override (spc_conv_set_tile_geometry; initially from
@@ -435,7 +561,8 @@ int conv_entry(spc_stream_t stream, int dtype, const void* x, int w_dtype, int w
                const void* w, const void* w_scale, const void* bias, void* y, const int32_t* idx,
                int idx_layout, const int32_t* row_perm, const void* plan, int64_t ntaps,
                int64_t n_out, int64_t n_in, int64_t cin, int64_t cout, int64_t class_rows,
-               int64_t n_classes, const spc_conv_epilogue* epi) {
+               int64_t n_classes, const spc_conv_epilogue* epi, int32_t* idx_cache = nullptr,
+               const int32_t* plan_dirty = nullptr) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int st = check_shape("spc_sparse_conv", ntaps, cin, cout);
     if (st != SPC_OK) return st;
@@ -488,6 +615,13 @@ int conv_entry(spc_stream_t stream, int dtype, const void* x, int w_dtype, int w
         return SPC_BAD_ARG;
     }
     a.plan = plan;
+    if (idx_cache && (!plan || !plan_dirty || row_perm || !idx)) {
+        set_last_error("spc_sparse_conv: a self-refreshing plan needs a plan, flags, idx and "
+                       "natural row order");
+        return SPC_BAD_ARG;
+    }
+    a.idx_cache = idx_cache;
+    a.plan_dirty = plan_dirty;
     a.num_cu = device_cu_count();
     a.geometry = geometry_override();
     if (epi && epi->mode != SPC_EPI_NONE) {
@@ -638,17 +772,45 @@ void sam3d_spconv_f16_forward(spc_stream_t stream, const void* input, const void
     // packed conv.  Weights beyond the pack buffer run unpacked.
     const size_t wbytes = spc_conv_packed_bytes(SPC_F16, 27, channels, output_channels);
     void* pk = wbytes <= kBridgePackBytes ? bridge_pack_addr() : nullptr;
-    if (pk && spc_conv_pack_weights(stream, SPC_F16, SPC_W_KRSC, weight, nullptr, 27, channels,
-                                    output_channels, pk) == SPC_OK) {
-        spc_sparse_conv(stream, SPC_F16, input, SPC_F16, SPC_W_PACKED, pk, nullptr, bias, output,
-                        indices, SPC_IDX_OFFSET_MAJOR, nullptr, 27, tokens, tokens, channels,
-                        output_channels);
+    // The tile setup (the deduplicated gather of each tile) comes from the
+    // device's self-refreshing plan: built by the first call over an index
+    // table, reused by every later call over the same one.
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int geometry = pk ? spc_conv_tile_geometry(SPC_F16, SPC_F16, 27, tokens, channels,
+                                                     output_channels, 0, SPC_EPI_NONE)
+                            : SPC_TILES_WIDE;
+    BridgePlan* bp = tokens > 0 && tokens <= INT32_MAX && input && indices
+                         ? bridge_plan(s, tokens, geometry)
+                         : nullptr;
+    const void* plan = bp ? bp->plan : nullptr;
+    int32_t* cache = bp ? bp->idx : nullptr;
+    const int32_t* dirty = bp ? bp->dirty : nullptr;
+    // one launch packs the weights and flags the changed index entries
+    const int64_t npack = pk && weight ? (int64_t)(wbytes / 16 + 255) / 256 : 0;
+    const int64_t nflag = bp ? (tokens + 255) / 256 : 0;
+    bool packed = false;
+    if (npack + nflag > 0) {
+        bridge_prep_kernel<<<(unsigned)(npack + nflag), 256, 0, s>>>(
+            static_cast<const uint8_t*>(weight), static_cast<u32x4*>(pk), (int)channels,
+            (int)output_channels, weight_strides(SPC_W_KRSC, 27, channels, output_channels), npack,
+            indices, cache, tokens, bp ? bp->dirty : nullptr);
+        if (hipGetLastError() != hipSuccess) {
+            set_last_error("sam3d_spconv_f16_forward: preparation launch failed");
+            return;
+        }
+        packed = npack > 0;
+    }
+    if (packed) {
+        conv_entry(stream, SPC_F16, input, SPC_F16, SPC_W_PACKED, pk, nullptr, bias, output,
+                   indices, SPC_IDX_OFFSET_MAJOR, nullptr, plan, 27, tokens, tokens, channels,
+                   output_channels, 0, 1, nullptr, cache, dirty);
         return;
     }
-    clear_last_error();
-    spc_sparse_conv(stream, SPC_F16, input, SPC_F16, SPC_W_KRSC, weight, nullptr, bias, output,
-                    indices, SPC_IDX_OFFSET_MAJOR, nullptr, 27, tokens, tokens, channels,
-                    output_channels);
+    // unpacked: weights beyond the pack buffer (wide tiles, the geometry
+    // the cache was set up for)
+    conv_entry(stream, SPC_F16, input, SPC_F16, SPC_W_KRSC, weight, nullptr, bias, output,
+               indices, SPC_IDX_OFFSET_MAJOR, nullptr, plan, 27, tokens, tokens, channels,
+               output_channels, 0, 1, nullptr, cache, dirty);
 }
 
 int spc_q8_0_repack(spc_stream_t stream, const uint8_t* blocks, int64_t nblocks, int8_t* qs,

@@ -74,6 +74,14 @@ struct ConvArgs {
     int32_t n_classes;        //   taps c * ntaps .. (packed weights of n_classes * ntaps taps)
     int64_t tiles_per_xcd;
     const void* plan;         // per-row-tile setup from conv_plan_kernel, or null
+    // Self-refreshing plan (with plan, natural row order): plan_dirty holds
+    // one flag per (128 output rows, tap), set where the index entries
+    // differ from those the plan was built from (idx_cache, same layout as
+    // idx; flag 27 f + o for rows [128 f, 128 f + 128) and tap o).  A tile
+    // over flagged rows sets itself up instead of reading its plan tile, and
+    // its first column tile writes the plan tile and the entries back.
+    const int32_t* plan_dirty;
+    int32_t* idx_cache;
     int32_t num_cu;           // compute units of the device (tile-width choice)
     // fused epilogue (spc_conv_epilogue): SPC_EPI_NONE / _RESIDUAL / _NORM_MOD_SILU
     int32_t epi_mode;
@@ -615,6 +623,14 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
 
     for (int c = tid; c < TN; c += NT) sbias[c] = a.bias ? M::ld(a.bias, co0 + c) : 0.0f;
 
+    // a self-refreshing plan tile over changed rows is not read
+    bool dirty = false;
+    if (a.plan_dirty) {
+        const int64_t f0 = r0 / 128, nf = (a.n_out + 127) / 128;
+        for (int64_t f = f0; f < nf && f * 128 < r0 + TM; ++f)
+            for (int o = 0; o < NTAPS; ++o) dirty |= a.plan_dirty[f * NTAPS + o] != 0;
+    }
+
     uint32_t tile_mask;
     int U;
     bool fast;
@@ -654,7 +670,7 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
         }
         lds_barrier();
         // a tile of a section the plan's builder skipped has no marker: set it up here
-        planned = misc[3] == kPlanMagic;
+        planned = misc[3] == kPlanMagic && !dirty;
         U = misc[0];
         tile_mask = (uint32_t)misc[1];
         fast = misc[2] != 0;
@@ -667,6 +683,32 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
         tile_mask = (uint32_t)misc[0];
         U = misc[3];
         fast = misc[4] != 0;
+        if (a.idx_cache && dirty && tn == 0) {
+            // refresh: this tile's plan tile (as conv_plan_kernel writes it)
+            // and its cached index entries.  No workgroup of this launch reads
+            // them: every tile over these rows is flagged.
+            char* pt = const_cast<char*>(static_cast<const char*>(a.plan)) +
+                       tm * GEO::plan_tile_bytes(NTAPS);
+            int32_t* hdr = reinterpret_cast<int32_t*>(pt);
+            if (tid < 8)
+                hdr[tid] = tid == 0 ? U : tid == 1 ? (int32_t)tile_mask : tid == 2 ? (int32_t)fast
+                         : tid == 3 ? (int32_t)kPlanMagic : 0;
+            else if (tid < 16) hdr[tid] = (int32_t)tlw[tid - 8];
+            for (int i = tid; i < TM; i += NT) reinterpret_cast<int32_t*>(pt + GEO::PLAN_SROW)[i] = srow[i];
+            if (fast) {
+                for (int i = tid; i < U; i += NT) reinterpret_cast<int32_t*>(pt + GEO::PLAN_UROW)[i] = urow[i];
+                for (int i = tid; i < (NTAPS + 1) * TM; i += NT)
+                    reinterpret_cast<uint16_t*>(pt + GEO::PLAN_SIDX)[i] = sidx[i];
+            }
+            for (int q = tid; q < NTAPS * TM; q += NT) {
+                const int o = q / TM;
+                const int64_t rr = r0 + (q - o * TM);
+                if (rr >= a.n_out) continue;
+                const int64_t e = a.idx_layout == SPC_IDX_TOKEN_MAJOR ? rr * NTAPS + o
+                                                                     : (int64_t)o * a.n_out + rr;
+                a.idx_cache[e] = a.idx[e];
+            }
+        }
     }
     // tile-uniform values: keep them (and the control flow they drive) scalar
     U = __builtin_amdgcn_readfirstlane(U);

@@ -198,6 +198,45 @@ def test_f16_spconv_bridge(spc, orc, dev):
                              idx_layout=nat.IDX_OFFSET_MAJOR)
     torch.cuda.synchronize()
     assert torch.equal(y, y_krsc)
+    # the bridge's self-refreshing tile plan: a second call over the same
+    # indices runs planned, a call over other indices of the same token
+    # count refreshes the changed tiles, and the first indices again
+    # refresh them back -- every result equal to the unplanned launch
+    y2, _ = nat.spconv_f16_forward(xd, wd, bd, m.offset_major, m.mask_sorted, m.argsort)
+    cb = coords.copy()
+    cb[:, 1] = 21 - cb[:, 1]  # mirrored in x: same count, other neighbour tables
+    cb = cb[np.lexsort((cb[:, 3], cb[:, 2], cb[:, 1], cb[:, 0]))]
+    mb = nat.map_build(torch.from_numpy(np.ascontiguousarray(cb)).to(dev))
+    assert not torch.equal(mb.offset_major, m.offset_major)
+    yb, _ = nat.spconv_f16_forward(xd, wd, bd, mb.offset_major, mb.mask_sorted, mb.argsort)
+    yb_krsc = nat.sparse_conv(xd, wd, bd, mb.offset_major, ntaps=27, n_out=n,
+                              idx_layout=nat.IDX_OFFSET_MAJOR)
+    # one token's centre tap dropped: only its tiles refresh
+    om = m.offset_major.clone()
+    om[13 * n + 17] = -1
+    yc, _ = nat.spconv_f16_forward(xd, wd, bd, om, m.mask_sorted, m.argsort)
+    yc_krsc = nat.sparse_conv(xd, wd, bd, om, ntaps=27, n_out=n, idx_layout=nat.IDX_OFFSET_MAJOR)
+    y3, _ = nat.spconv_f16_forward(xd, wd, bd, m.offset_major, m.mask_sorted, m.argsort)
+    torch.cuda.synchronize()
+    assert torch.equal(y2, y_krsc)
+    assert torch.equal(yb, yb_krsc)
+    assert torch.equal(yc, yc_krsc) and not torch.equal(yc, y_krsc)
+    assert torch.equal(y3, y_krsc)
+    # two column tiles per row tile (C_out 256), and a change of tile
+    # geometry over the same indices (C_in 128 runs the wide tiles, 64 the
+    # small ones): each call equal to the unplanned launch
+    xw = torch.from_numpy(wl.normal((n, 128), 1.0, seed=45).astype(np.float16)).to(dev)
+    for cin, cout in ((64, 256), (64, 256), (128, 128), (128, 128), (64, 128)):
+        _case(f"f16 bridge plan cache {cin}->{cout}")
+        xi = xd if cin == 64 else xw
+        wi = torch.from_numpy(wl.normal((cout, 27, cin), 0.02, seed=cin + cout)
+                              .astype(np.float16)).to(dev)
+        bi = torch.from_numpy(wl.normal((cout,), 0.01, seed=cout).astype(np.float16)).to(dev)
+        yi, msg = nat.spconv_f16_forward(xi, wi, bi, m.offset_major, m.mask_sorted, m.argsort)
+        yi_krsc = nat.sparse_conv(xi, wi, bi, m.offset_major, ntaps=27, n_out=n,
+                                  idx_layout=nat.IDX_OFFSET_MAJOR)
+        torch.cuda.synchronize()
+        assert msg == "" and torch.equal(yi, yi_krsc)
 
 
 def test_q8_0_config5_sphere(spc, orc, dev):
