@@ -14,9 +14,10 @@
  *   - Every buffer is caller-owned device memory (hipMalloc / torch).  The
  *     library allocates nothing at run time; scratch space comes from a
  *     caller-owned workspace whose size the *_workspace_bytes queries
- *     return.  The exceptions are static device arrays, one per device for
- *     the life of the process: the spconv bridge's 64 MiB weight-pack buffer
- *     (sam3d_spconv_f16_forward) and the 56 MiB map scratch of
+ *     return.  The exceptions, one per device for the life of the process:
+ *     the spconv bridge's 64 MiB weight-pack buffer and its tile-plan cache
+ *     (sam3d_spconv_f16_forward, whose signature has no workspace; the
+ *     cache is the one run-time hipMalloc) and the 56 MiB map scratch of
  *     spc_map_build_noalloc -- documented at their entry points.
  *   - Calls are asynchronous on `stream` (a hipStream_t; 0 = null stream)
  *     unless documented as synchronising.  Calls on one stream are ordered;
@@ -342,10 +343,16 @@ int spc_conv_expand_q8_0(spc_stream_t stream, const void* packed_q8, int64_t nta
  * reference kernel accumulates in f16).  channels and output_channels must
  * be multiples of 32.  The KRSC weights are packed on every call into a
  * library-owned 64 MiB device buffer (one per device, held until the
- * process ends) and the packed conv runs on them: bridge calls on one device
- * share that buffer, so calls on different streams of one device must not
- * overlap (the reference's bridge, too, assumes one stream).  Weights
- * larger than the buffer run unpacked (same results, slower).  Returns
+ * process ends) and the packed conv runs on them.  The tile setup comes
+ * from a library-owned tile plan per device with a copy of the indices it
+ * was built from (device memory of about 160 bytes per token, hipMalloc'd
+ * when a call needs more, held until the process ends): each call checks
+ * its indices against the copy in the same launch as the weight pack, and
+ * tiles whose entries changed set themselves up and refresh their plan, so
+ * repeated calls over one index table skip the setup.  Bridge calls on one
+ * device share these buffers, so calls on different streams of one device
+ * must not overlap (the reference's bridge, too, assumes one stream).
+ * Weights larger than the buffer run unpacked (same results, slower).  Returns
  * nothing, like the reference: spc_last_error() is cleared on entry and
  * is non-empty after the call exactly when it failed (output unwritten). */
 void sam3d_spconv_f16_forward(spc_stream_t stream, const void* input, const void* weight,
