@@ -51,6 +51,9 @@ def parse():
     ap.add_argument("--order", choices=["natural", "mask"], default="natural",
                     help="row processing order of the conv kernel")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="config 2: time the conv only (no single-shell, bridge or library-GEMM "
+                         "lines), for counter runs")
     ap.add_argument("--fused-only", action="store_true",
                     help="configs 6 / 7: time the fused block only (no unfused comparison)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
@@ -452,10 +455,10 @@ def main():
         if cfg == 5 and not args.bf16_weights:
             result["config"]["q8_path"] = ("dequant in registers" if args.q8_in_registers else
                                            "expand to packed bf16 + bf16 conv, both timed")
-        if cfg == 2:
+        if cfg == 2 and not args.headline_only:
             result["single_shell"] = bench_single_shell(nat, wl, orc, dev, args)
             result["bridge"] = bench_bridge(nat, wl, c_dev, dev, args)
-        if dtype == "bf16":
+        if dtype == "bf16" and not args.headline_only:
             g = library_gemm_tflops(dev, torch.bfloat16)
             g["conv_fraction"] = tflops / g["tflops"]
             result["measured_gemm_peak"] = g

@@ -192,27 +192,45 @@ constexpr int kSetupScratchWords = 2 * kWinWords > 2 * kHashSlots + 2 * kSortCap
                                        ? 2 * kWinWords
                                        : 2 * kHashSlots + 2 * kSortCap;
 constexpr int kSegs = 4;        // 16-byte segments per staged 64-byte row chunk
-constexpr int kPitch = 5;       // staged row pitch in 16-byte units (64 bytes + 16 of padding)
 
 // Tile geometry: TM output rows per tile, a deduplicated source-row stage of
-// UMAX rows (+ the zero row), NBUF A buffers.
+// UMAX rows (+ the zero row), NBUF A buffers, and the staged row layout.
 //   GeoWide   256 rows, 895-row stage, double-buffered (the next chunk lands
-//             while the MFMAs run): 159 KB of LDS, one workgroup of 8 waves
-//             per CU -- the wide convs, where every tile is long.
+//             while the MFMAs run), 64-byte rows with swizzled segments:
+//             112 KB of A stage, one workgroup of 8 waves per CU -- the wide
+//             convs, where every tile is long.  The 128-column 16-bit tiles
+//             put the step's weights through a 32 KB LDS ring as well.
 //   GeoSmall  128 rows (64 for the 8-tap stride-2 conv, whose 128 coarse
-//             rows reference ~680 fine rows), 511-row stage, one buffer:
-//             ~51 KB of LDS, three workgroups of 4 waves per CU, which hide
-//             each other's staging and setup latency -- the short tiles of
-//             small channel counts, small row counts and stride-2.
-template <int TM_, int UMAX_, int NBUF_>
+//             rows reference ~680 fine rows), 511-row stage, one buffer,
+//             80-byte padded rows: ~51 KB of LDS, three workgroups of 4 waves
+//             per CU, which hide each other's staging and setup latency --
+//             the short tiles of small channel counts, small row counts and
+//             stride-2.
+// Staged row layouts (one 64-byte chunk of a union row = four 16-byte
+// segments; a wave's A-fragment read takes one segment of 32 slots, which
+// the LDS serves 16 lanes at a time):
+//   SW = false  row r at an 80-byte pitch: segment s at unit 5r + s; 16
+//               consecutive slots reading one segment hit 16 distinct
+//               bank groups (5 is odd).
+//   SW = true   row r at a 64-byte pitch, segment s at unit 4r + (s ^ ((r >> 2)
+//               & 3)): the XOR spreads 16 consecutive slots over the 16 bank
+//               groups as well, without the 16 bytes of padding per row.
+// A slot key is the unit of segment 0's position base: unit(s) = key + s
+// (padded) or key ^ s (swizzled: the key's low two bits carry the swizzle).
+template <int TM_, int UMAX_, int NBUF_, bool SW_>
 struct Geo {
     static constexpr int TM = TM_;
     static constexpr int UMAX = UMAX_;
     static constexpr int NBUF = NBUF_;
+    static constexpr bool SW = SW_;
+    static constexpr int PITCH = SW ? 4 : 5;            // 16-byte units per staged row
     static constexpr int UROWCAP = (UMAX + 3) / 4 * 4;  // union-row table (16-byte multiple)
     // 16-byte units per A buffer: whole 64-unit blocks (one LDS-DMA
     // instruction each) holding the UMAX union rows and the zero row
-    static constexpr int STAGE = ((UMAX + 1) * kPitch + 63) / 64 * 64;
+    static constexpr int STAGE = ((UMAX + 1) * PITCH + 63) / 64 * 64;
+    __host__ __device__ static constexpr int key(int r) { return SW ? 4 * r + ((r >> 2) & 3) : 5 * r; }
+    __host__ __device__ static constexpr int unit(int k, int s) { return SW ? (k ^ s) : k + s; }
+    __host__ __device__ static constexpr int seg_pos(int r, int s) { return unit(key(r), s); }
     // One row tile's plan: header (U, tap mask, fast flag, tap words),
     // output rows, union rows, slot keys.  It depends only on the index
     // table, its layout, the row order and NTAPS -- not on channels or
@@ -224,10 +242,10 @@ struct Geo {
         return (PLAN_SIDX + 2 * (int64_t)(ntaps + 1) * TM + 255) / 256 * 256;
     }
 };
-using GeoWide = Geo<256, 895, 2>;
+using GeoWide = Geo<256, 895, 2, true>;
 template <int NTAPS>
-using GeoSmall = Geo<NTAPS == 8 ? 64 : 128, 511, 1>;
-static_assert(GeoWide::STAGE == 4480 && GeoSmall<27>::STAGE == 2560, "stage geometry");
+using GeoSmall = Geo<NTAPS == 8 ? 64 : 128, 511, 1, false>;
+static_assert(GeoWide::STAGE == 3584 && GeoSmall<27>::STAGE == 2560, "stage geometry");
 
 // Plan buffer: the GeoWide plan of every 256-row tile, then the GeoSmall
 // plan of every small tile (a conv picks its geometry by shape).
@@ -235,18 +253,9 @@ __host__ __device__ constexpr int64_t plan_wide_bytes(int64_t n_out, int ntaps) 
     return (n_out + GeoWide::TM - 1) / GeoWide::TM * GeoWide::plan_tile_bytes(ntaps);
 }
 __host__ __device__ constexpr int64_t plan_small_bytes(int64_t n_out, int ntaps) {
-    return ntaps == 8 ? (n_out + 63) / 64 * Geo<64, 511, 1>::plan_tile_bytes(8)
-                      : (n_out + 127) / 128 * Geo<128, 511, 1>::plan_tile_bytes(ntaps);
+    return ntaps == 8 ? (n_out + 63) / 64 * GeoSmall<8>::plan_tile_bytes(8)
+                      : (n_out + 127) / 128 * GeoSmall<27>::plan_tile_bytes(ntaps);
 }
-
-// LDS position (in 16-byte units) of segment s of staged row r.  The 80-byte
-// pitch puts one segment of 8 (and of 16) consecutive rows on distinct banks,
-// so a wave reading one k-slice of 32 nearly consecutive slots, and the stage
-// writes, run without bank conflicts; the slot table stores slot_key(r), so
-// a fragment address is one multiply-add and the k-steps are immediate
-// offsets.
-__device__ __forceinline__ int slot_key(int r) { return r * kPitch; }
-__device__ __forceinline__ int seg_pos(int r, int s) { return r * kPitch + s; }
 
 constexpr int kTapWords = 8;  // step taps, four per word: up to 28 steps per chunk
 constexpr int32_t kPlanMagic = 0x314e4c50;  // header word 3 of every built plan tile
@@ -440,10 +449,10 @@ __device__ __forceinline__ void tile_setup(const ConvArgs& a, int64_t r0, const 
                         }
                         out = (uint32_t)v == (uint32_t)ent[k] ? (int32_t)(v >> 32) : U;
                     }
-                    L.sidx[o * TM + r] = (uint16_t)slot_key(out);
+                    L.sidx[o * TM + r] = (uint16_t)GEO::key(out);
                 }
             }
-            for (int r = tid; r < TM; r += NT) L.sidx[NTAPS * TM + r] = (uint16_t)slot_key(U);
+            for (int r = tid; r < TM; r += NT) L.sidx[NTAPS * TM + r] = (uint16_t)GEO::key(U);
         }
     } else {
         // ranks: thread tid owns words WPT*tid .. WPT*tid + WPT - 1
@@ -500,10 +509,10 @@ __device__ __forceinline__ void tile_setup(const ConvArgs& a, int64_t r0, const 
                         const int wi = off >> 5;
                         out = wbase[wi] + __popc(bm[wi] & ((1u << (off & 31)) - 1u));
                     }
-                    L.sidx[o * TM + r] = (uint16_t)slot_key(out);
+                    L.sidx[o * TM + r] = (uint16_t)GEO::key(out);
                 }
             }
-            for (int r = tid; r < TM; r += NT) L.sidx[NTAPS * TM + r] = (uint16_t)slot_key(U);
+            for (int r = tid; r < TM; r += NT) L.sidx[NTAPS * TM + r] = (uint16_t)GEO::key(U);
         }
     }
     if (tid == 0) {
@@ -848,8 +857,8 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
         }
     };
     // A fragments of k-slices of 32 rows per FM block.  sl[] holds slot
-    // keys (the row's first 16-byte unit); the byte of each k-step within
-    // the 64-byte row is a lane constant.
+    // keys; the byte of each k-step within the 64-byte row is a lane
+    // constant, its segment placed by the geometry's row layout.
     auto read_frags = [&](int buf, const int* sl, AFrag& f) __attribute__((always_inline)) {
         const char* ab = reinterpret_cast<const char*>(Au + buf * STAGE);
 #pragma unroll
@@ -857,7 +866,8 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
             const int byte = (ks * M::KSUB + (lane >> 5) * M::EPL) * ES;  // within the 64-byte row
 #pragma unroll
             for (int i = 0; i < FM; ++i)
-                f[ks][i] = *reinterpret_cast<const typename M::frag*>(ab + sl[i] * 16 + byte);
+                f[ks][i] = *reinterpret_cast<const typename M::frag*>(
+                    ab + GEO::unit(sl[i], byte >> 4) * 16 + (byte & 15));
         }
     };
     // union slots of the wave's rows for sidx row `row` (a tap, or NTAPS = zeros)
@@ -874,11 +884,11 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
 
     if (dma) {
         // ---- A staging through LDS DMA -----------------------------------
-        // A chunk's stage is U + 1 rows at an 80-byte pitch, in 64-unit
-        // blocks of 16 bytes; one buffer_load_dwordx4 ... lds fills a block
-        // (lane l -> unit 64 * block + l).  Unit 5 r + s holds segment s of
-        // union row r; padding units (s = 4), the zero row U and units past
-        // it read out of range, which writes zeros.  The next chunk's blocks
+        // A chunk's stage is U + 1 rows in the geometry's row layout, in
+        // 64-unit blocks of 16 bytes; one buffer_load_dwordx4 ... lds fills a
+        // block (lane l -> unit 64 * block + l).  A unit holds one segment of
+        // one union row; padding units (the 80-byte layout's fifth unit), the
+        // zero row U and units past it read out of range, which writes zeros.  The next chunk's blocks
         // are issued in NPART parts at the starts of the first step groups;
         // they land in the free buffer while the MFMAs run and are waited
         // for once, before the chunk barrier.
@@ -891,7 +901,7 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
                              (uint32_t)__builtin_amdgcn_readfirstlane(nrec), 0x00020000u};
         const uint32_t au_lds = __builtin_amdgcn_readfirstlane(
             (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) u32x4*)Au));
-        const int nblk = ((U + 1) * kPitch + 63) / 64;
+        const int nblk = ((U + 1) * GEO::PITCH + 63) / 64;
         // Wave w fills blocks w + NW j.  The per-lane source offsets do not
         // depend on the chunk (it enters as the scalar offset), so they are
         // computed once per tile and kept in registers.
@@ -900,8 +910,8 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
             const int v = (wave + NW * j) * 64 + lane;
-            const int r = v / kPitch;
-            const int sg = v - r * kPitch;
+            const int r = v / GEO::PITCH;
+            const int sg = GEO::SW ? (v & 3) ^ ((r >> 2) & 3) : v - r * GEO::PITCH;
             doff[j] = 0x80000000u;  // out of range: zeros
             if (sg < kSegs && r < U)
                 doff[j] = (uint32_t)(urow[r] - row0) * (uint32_t)rowbytes + (uint32_t)(sg * 16);
@@ -1069,9 +1079,9 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
         // together; the round's steps then run from LDS, each step's weights
         // loaded while the previous step's MFMAs run.
         constexpr int UPT = (TM * kSegs + NT - 1) / NT;
-        constexpr int GA = NBUF * STAGE / (TM * kPitch);
+        constexpr int GA = NBUF * STAGE / (TM * GEO::PITCH);
         constexpr int G = GA < 14 / UPT ? GA : 14 / UPT;  // taps per round (<= 56 VGPRs of loads)
-        static_assert(G >= 1 && G * TM * kPitch <= NBUF * STAGE, "fallback rounds fit the A area");
+        static_assert(G >= 1 && G * TM * GEO::PITCH <= NBUF * STAGE, "fallback rounds fit the A area");
         for (int kc = 0; kc < kch; ++kc) {
             const int64_t koff = (int64_t)kc * KC * ES;
             uint32_t m = tile_mask;
@@ -1104,7 +1114,7 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
                     for (int j = 0; j < UPT; ++j) {
                         const int u = j * NT + tid;
                         if (og[g] < 0 || (TM * kSegs % NT != 0 && u >= TM * kSegs)) continue;
-                        Au[seg_pos(g * TM + (u >> 2), u & 3)] = v[g][j];
+                        Au[GEO::seg_pos(g * TM + (u >> 2), u & 3)] = v[g][j];
                     }
                 lds_barrier();
 #pragma unroll
@@ -1115,7 +1125,7 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
                     int sl[FM];
 #pragma unroll
                     for (int i = 0; i < FM; ++i)
-                        sl[i] = slot_key(g * TM + wm * WTM + i * 32 + (lane & 31));
+                        sl[i] = GEO::key(g * TM + wm * WTM + i * 32 + (lane & 31));
                     AFrag af;
                     read_frags(0, sl, af);
                     mma_step(af, bs[g & 1]);
@@ -1126,43 +1136,50 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
 
     // ---- epilogue LayerNorm -> modulation -> SiLU over whole output rows
     // (TN == cout: the tile holds every channel of its rows).  The rounded
-    // conv outputs go to an F32 LDS tile; groups of TN/4 lanes then take one
-    // row each (four channels per lane, four rows in flight per lane group),
-    // with group-local shuffles for the mean and the biased variance.
-    if constexpr (TN <= 128 && TM * (TN + 4) * 4 <= ABYTES) if (a.epi_mode == SPC_EPI_NORM_MOD_SILU) {
+    // conv outputs go to an F32 LDS tile (in NPN passes over row halves when
+    // the whole tile does not fit the A stage); groups of TN/4 lanes then
+    // take one row each (four channels per lane, four rows in flight per
+    // lane group), with group-local shuffles for the mean and the biased
+    // variance.
+    if constexpr (TN <= 128 && TM / 2 * (TN + 4) * 4 <= ABYTES) if (a.epi_mode == SPC_EPI_NORM_MOD_SILU) {
         constexpr int FP = TN + 4;           // f32 row pitch (16-byte multiple)
-        static_assert(TM * FP * 4 <= ABYTES, "f32 output tile fits the A stage");
+        constexpr int NPN = TM * FP * 4 <= ABYTES ? 1 : 2;  // passes
+        constexpr int RPN = TM / NPN;        // tile rows per pass
+        static_assert(RPN * FP * 4 <= ABYTES && RPN % 32 == 0, "f32 output tile fits the A stage");
         constexpr int G = TN / 4;            // lanes per row
         constexpr int RW = 64 / G;           // rows per wave at a time
         constexpr int RB = 4;                // row groups in flight per lane
-        static_assert(TM % (NW * RW * RB) == 0, "norm epilogue geometry");
+        static_assert(RPN % (NW * RW * RB) == 0, "norm epilogue geometry");
         float* of = reinterpret_cast<float*>(Au);
-        lds_barrier();  // every wave is done with the A stage
+        const int gl = lane % G;
+        const int c0 = 4 * gl;
+        char* yb = static_cast<char*>(a.y);
+#pragma unroll
+        for (int p = 0; p < NPN; ++p) {
+        lds_barrier();  // every wave is done with the A stage / the previous pass
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
             const int rl = wm * WTM + i * 32 + (lane & 31);
+            if (wm * WTM + i * 32 < p * RPN || wm * WTM + i * 32 >= (p + 1) * RPN) continue;
 #pragma unroll
             for (int j = 0; j < FN; ++j)
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const int cl = wn * WTN + j * 32 + 8 * g + 4 * (lane >> 5);
-                    *reinterpret_cast<floatx4*>(of + rl * FP + cl) =
+                    *reinterpret_cast<floatx4*>(of + (rl - p * RPN) * FP + cl) =
                         floatx4{M::round(acc[i][j][4 * g]), M::round(acc[i][j][4 * g + 1]),
                                 M::round(acc[i][j][4 * g + 2]), M::round(acc[i][j][4 * g + 3])};
                 }
         }
         lds_barrier();
-        const int gl = lane % G;
-        const int c0 = 4 * gl;
-        char* yb = static_cast<char*>(a.y);
-        for (int it = 0; it < TM / (NW * RW * RB); ++it) {
+        for (int it = 0; it < RPN / (NW * RW * RB); ++it) {
             float v[RB][4];
             int32_t t[RB];
             float s[RB], q[RB];
 #pragma unroll
             for (int k = 0; k < RB; ++k) {
                 const int r = ((it * RB + k) * NW + wave) * RW + lane / G;
-                t[k] = srow[r];
+                t[k] = srow[p * RPN + r];
                 const floatx4 f = *reinterpret_cast<const floatx4*>(of + r * FP + c0);
                 v[k][0] = f.x; v[k][1] = f.y; v[k][2] = f.z; v[k][3] = f.w;
                 s[k] = (v[k][0] + v[k][1]) + (v[k][2] + v[k][3]);
@@ -1209,6 +1226,7 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
                 }
             }
         }
+        }  // passes
         return;
     }
 
