@@ -198,8 +198,7 @@ constexpr int kSegs = 4;        // 16-byte segments per staged 64-byte row chunk
 //   GeoWide   256 rows, 895-row stage, double-buffered (the next chunk lands
 //             while the MFMAs run), 64-byte rows with swizzled segments:
 //             112 KB of A stage, one workgroup of 8 waves per CU -- the wide
-//             convs, where every tile is long.  The 128-column 16-bit tiles
-//             put the step's weights through a 32 KB LDS ring as well.
+//             convs, where every tile is long.
 //   GeoSmall  128 rows (64 for the 8-tap stride-2 conv, whose 128 coarse
 //             rows reference ~680 fine rows), 511-row stage, one buffer,
 //             80-byte padded rows: ~51 KB of LDS, three workgroups of 4 waves
