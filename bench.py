@@ -45,7 +45,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", type=int, default=2, choices=[0, 1, 2, 3, 4, 5, 6, 7, 8, 9],
+    ap.add_argument("--config", type=int, default=2, choices=[0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10],
                     help="2 = the headline workload; others print diagnostic lines (0 = one "
                          "sphere shell, N = 21,766, bf16 C = 128; 9 = feature ops' HBM GB/s)")
     ap.add_argument("--order", choices=["natural", "mask"], default="natural",
@@ -285,6 +285,13 @@ def main():
         cin = cout = 128
         batch = 1
         workload = "subm3x3x3 bf16 C=128, one sphere shell r=24 in 64^3 (N=21,766)"
+    elif cfg == 10:
+        coords = wl.ellipsoid_batch()
+        cin = cout = 128
+        batch = 4
+        workload = ("SLAT IO residual blocks: SparseResBlock3d(128 -> 1024, downsample) on the 4 "
+                    "ellipsoid shells (62,710 -> 11,774 rows) and SparseResBlock3d(2048 -> 128, "
+                    "upsample) back to the fine rows, bf16")
     elif cfg == 9:
         coords = wl.ellipsoid_batch()
         cin = cout = 128
@@ -503,6 +510,8 @@ def main():
                   "pct_peak_subm1024": 100 * f3 / (ms3 / 1e3) / 1e12 / PEAK_BF16_TFLOPS}
     elif cfg == 6:
         result = bench_res_block(spc, nat, wl, orc, coords, c_dev, dev, args, workload)
+    elif cfg == 10:
+        result = bench_io_blocks(spc, nat, wl, orc, coords, c_dev, dev, args, workload)
     elif cfg == 9:
         result = bench_feature_ops(spc, nat, wl, orc, coords, c_dev, dev, args, workload)
     elif cfg in (7, 8):
@@ -712,6 +721,59 @@ def bench_res_block(spc, nat, wl, orc, coords, c_dev, dev, args, workload):
             "ms_per_step": ms_f, "unfused_ms": ms_u, "speedup": ms_u / ms_f if ms_u else None,
             "dtype": "bf16", "max_abs_diff_fused_vs_unfused": diff,
             "config": {"workload": workload, "n_voxels": n, "channels": 128, "batch": 4}}
+
+
+def bench_io_blocks(spc, nat, wl, orc, coords, c_dev, dev, args, workload):
+    """The SLAT flow model's IO residual blocks at their real widths
+    (structured_latent_flow.py:50-74, 140-200): the input block
+    SparseResBlock3d(128, 1024, 1024, downsample=True) -- scatter-mean
+    downsample of the 62,710 fine rows to 11,774 coarse rows, LayerNorm32 +
+    SiLU, conv 128 -> 1024, the norm2 / modulation / SiLU row pass, conv
+    1024 -> 1024 + the 128 -> 1024 skip -- and the output block
+    SparseResBlock3d(2048, 1024, 128, upsample=True) -- the coarse -> fine
+    gather, conv 2048 -> 128 with the fused norm epilogue, conv 128 -> 128 +
+    the 2048 -> 128 skip.  Maps are cached in the tensors' spatial caches
+    (built once, as in a sampling loop); the time is the block forward."""
+    import torch
+
+    sp = spc.sparse
+    n = coords.shape[0]
+    out = {}
+    for mode, cin, cout in (("down", 128, 1024), ("up", 2048, 128)):
+        torch.manual_seed(7 + cin)
+        blk = spc.blocks.SparseResBlock3d(cin, 1024, cout, downsample=mode == "down",
+                                          upsample=mode == "up").to(dev)
+        with torch.no_grad():
+            for prm in blk.conv2.parameters():
+                prm.normal_(0, 0.02)
+        blk = blk.to(torch.bfloat16)
+        blk.norm1.float()
+        if mode == "down":
+            x, _ = bf16_dev(orc, wl.normal((n, cin), 1.0, seed=1001), dev)
+            xt = sp.SparseTensor(x, c_dev)
+        else:
+            ft = sp.SparseTensor(torch.zeros((n, 32), dtype=torch.bfloat16, device=dev), c_dev)
+            ct = sp.SparseDownsample(2)(ft)
+            x, _ = bf16_dev(orc, wl.normal((ct.coords.shape[0], cin), 1.0, seed=1002), dev)
+            xt = ct.replace(x)
+        emb = torch.randn(4, 1024, device=dev).bfloat16()
+
+        def fwd():
+            with torch.no_grad():
+                return blk(xt, emb)
+
+        y = fwd()  # builds and caches the maps and plans
+        ms, _ = time_gpu(fwd, args.steps, args.warmup)
+        n_in, n_out = xt.feats.shape[0], y.feats.shape[0]
+        flops = 0.0
+        for conv, rows, ci, co in ((blk.conv1, n_out, cin, cout), (blk.conv2, n_out, cout, cout)):
+            flops += 2.0 * ci * co * rows * 27  # dense-equivalent (tap padding included)
+        out[mode] = {"block": f"SparseResBlock3d({cin} -> {cout}, {mode}sample)", "rows_in": n_in,
+                     "rows_out": n_out, "ms": ms, "mvoxel_s": n_out / (ms / 1e3) / 1e6,
+                     "dense_equiv_tflops": flops / (ms / 1e3) / 1e12}
+    return {"metric": f"config 10: {workload}", "dtype": "bf16", "blocks": out,
+            "config": {"workload": workload, "n_fine": n,
+                       "n_coarse": out["down"]["rows_out"]}}
 
 
 def bench_subdivide_block(spc, nat, wl, orc, coords, c_dev, dev, args, workload, cin, cout, res):

@@ -844,36 +844,42 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
     // holds output row l%32 and output channels 8*(k/4) + 4*(l/32) + k%4 for
     // element k -- four runs of four consecutive channels per lane, stored
     // straight to global memory.
-    auto mma_step = [&](const AFrag& af, const Slot& bs) __attribute__((always_inline)) {
+    // fa_const: the wave's live 32-row blocks (FM, or fewer in a partial
+    // last row tile, whose dead blocks are skipped)
+    auto mma_step = [&](const AFrag& af, const Slot& bs, auto fa_const) __attribute__((always_inline)) {
+        constexpr int FA = decltype(fa_const)::value;
 #pragma unroll
         for (int ks = 0; ks < P::KS; ++ks) {
 #pragma unroll
             for (int j = 0; j < FN; ++j) {
                 const typename M::frag bf = b_frag(bs, j, ks);
 #pragma unroll
-                for (int i = 0; i < FM; ++i) acc[i][j] = M::mma(bf, af[ks][i], acc[i][j]);
+                for (int i = 0; i < FA; ++i) acc[i][j] = M::mma(bf, af[ks][i], acc[i][j]);
             }
         }
     };
     // A fragments of k-slices of 32 rows per FM block.  sl[] holds slot
     // keys; the byte of each k-step within the 64-byte row is a lane
     // constant, its segment placed by the geometry's row layout.
-    auto read_frags = [&](int buf, const int* sl, AFrag& f) __attribute__((always_inline)) {
+    auto read_frags = [&](int buf, const int* sl, AFrag& f, auto fa_const) __attribute__((always_inline)) {
+        constexpr int FA = decltype(fa_const)::value;
         const char* ab = reinterpret_cast<const char*>(Au + buf * STAGE);
 #pragma unroll
         for (int ks = 0; ks < P::KS; ++ks) {
             const int byte = (ks * M::KSUB + (lane >> 5) * M::EPL) * ES;  // within the 64-byte row
 #pragma unroll
-            for (int i = 0; i < FM; ++i)
+            for (int i = 0; i < FA; ++i)
                 f[ks][i] = *reinterpret_cast<const typename M::frag*>(
                     ab + GEO::unit(sl[i], byte >> 4) * 16 + (byte & 15));
         }
     };
     // union slots of the wave's rows for sidx row `row` (a tap, or NTAPS = zeros)
-    auto read_slots = [&](int row, int* sl) __attribute__((always_inline)) {
+    auto read_slots = [&](int row, int* sl, auto fa_const) __attribute__((always_inline)) {
+        constexpr int FA = decltype(fa_const)::value;
 #pragma unroll
-        for (int i = 0; i < FM; ++i) sl[i] = sidx[row * TM + wm * WTM + i * 32 + (lane & 31)];
+        for (int i = 0; i < FA; ++i) sl[i] = sidx[row * TM + wm * WTM + i * 32 + (lane & 31)];
     };
+    const auto fm_all = std::integral_constant<int, FM>{};
 
     // The fast path stages through LDS DMA with 32-bit offsets from the
     // tile's lowest source row.
@@ -969,6 +975,8 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
                 dma_barrier<0>();
             }
         } else {
+          auto run_tile = [&](auto fa_const) __attribute__((always_inline)) {
+            constexpr int FA = decltype(fa_const)::value;
             Slot ring[PD];
             AFrag afr[2];
             int sreg[2][FM];
@@ -983,11 +991,11 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
                 const uint32_t w0 = tw_first[0];
 #pragma unroll
                 for (int p = 0; p < PD; ++p) load_b(b_tap(w0, p), 0, ring[p]);
-                read_slots(s_row(w0, 0), sreg[0]);
-                read_slots(s_row(w0, 1), sreg[1]);
+                read_slots(s_row(w0, 0), sreg[0], fa_const);
+                read_slots(s_row(w0, 1), sreg[1], fa_const);
                 for (int h = 0; h < NPART; ++h) stage_part_rt(0, 0, h);
                 dma_barrier<0>();
-                read_frags(0, sreg[0], afr[0]);
+                read_frags(0, sreg[0], afr[0], fa_const);
             }
 
             for (int kc = 0; kc < kch; ++kc) {
@@ -1009,7 +1017,7 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
                         if (ngr >= NPART && LPS > 0) dma_barrier<PD * LPS>();
                         else dma_barrier<0>();
                     }
-                    read_frags(buf, sreg[0], afr[0]);
+                    read_frags(buf, sreg[0], afr[0], fa_const);
                 }
 #pragma unroll
                 for (int w = 0; w < kTapWords; ++w) tw[w] = tw_first[w];
@@ -1028,23 +1036,23 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
                     auto step = [&](auto u_const) __attribute__((always_inline)) {
                         constexpr int u = decltype(u_const)::value;
                         // slots of the step after next (they do not depend on the chunk)
-                        read_slots(u + 2 < PD ? s_row(w0, u + 2) : s_row(w1, u + 2 - PD), sreg[u & 1]);
+                        read_slots(u + 2 < PD ? s_row(w0, u + 2) : s_row(w1, u + 2 - PD), sreg[u & 1], fa_const);
                         // A fragments of the next step; after a chunk's last step they
                         // are re-read behind the barrier, so this read is unused
-                        read_frags(buf, sreg[(u + 1) & 1], afr[(u + 1) & 1]);
+                        read_frags(buf, sreg[(u + 1) & 1], afr[(u + 1) & 1], fa_const);
                         if constexpr (last_g && u > 0) {
-                            if (u < nreal) mma_step(afr[u & 1], ring[u]);
+                            if (u < nreal) mma_step(afr[u & 1], ring[u], fa_const);
                         } else {
-                            mma_step(afr[u & 1], ring[u]);
+                            mma_step(afr[u & 1], ring[u], fa_const);
                         }
                         // weights of the step PD ahead
                         load_b(b_tap(w1, u), kc_b, ring[u]);
                         // issue order: slot reads, then MFMAs interleaved with the
                         // fragment reads and their address arithmetic, then the
                         // weight loads
-                        constexpr int NMF = P::KS * FM * FN;
-                        constexpr int NFR = P::KS * FM;
-                        __builtin_amdgcn_sched_group_barrier(0x100, FM, 0);
+                        constexpr int NMF = P::KS * FA * FN;
+                        constexpr int NFR = P::KS * FA;
+                        __builtin_amdgcn_sched_group_barrier(0x100, FA, 0);
 #pragma unroll
                         for (int q = 0; q < NMF; ++q) {
                             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -1069,6 +1077,21 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
                 run_group(ngr - 1, std::true_type{});
                 if (more)  // short chunks: the parts the group loop did not reach
                     for (int h = ngr; h < NPART; ++h) stage_part_rt(kc + 1, buf ^ 1, h);
+            }
+          };
+            // A wave of the partial last row tile whose rows end inside its
+            // first 32-row block runs that block's MFMAs only (the same
+            // loads and barriers): a 6-row tile no longer costs a full one.
+            uint32_t live_blocks = 0;  // bit i: block i has a row
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+                live_blocks |= (__builtin_amdgcn_ballot_w64(srow[wm * WTM + i * 32 + (lane & 31)] >= 0) != 0)
+                                << i;
+            if constexpr (FM >= 2) {
+                if (live_blocks == 1u) run_tile(std::integral_constant<int, 1>{});
+                else run_tile(fm_all);
+            } else {
+                run_tile(fm_all);
             }
         }
     } else if (nt > 0) {
@@ -1126,8 +1149,8 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
                     for (int i = 0; i < FM; ++i)
                         sl[i] = GEO::key(g * TM + wm * WTM + i * 32 + (lane & 31));
                     AFrag af;
-                    read_frags(0, sl, af);
-                    mma_step(af, bs[g & 1]);
+                    read_frags(0, sl, af, fm_all);
+                    mma_step(af, bs[g & 1], fm_all);
                 }
             }
         }

@@ -263,3 +263,46 @@ def test_plan_sections(spc, orc, dev, geo):
     assert nat.plan_section(torch.bfloat16, ntaps=27, n_out=n, cin=64, cout=64) == nat.PLAN_SMALL
     assert nat.plan_section(torch.bfloat16, ntaps=27, n_out=n, cin=128, cout=128) == nat.PLAN_WIDE
     assert nat.plan_section(torch.bfloat16, ntaps=8, n_out=n, cin=128, cout=128) == nat.PLAN_SMALL
+
+
+@pytest.mark.parametrize("r", [1, 6, 31, 32, 33, 64, 65, 129, 255])
+def test_partial_tile_live_blocks(spc, orc, dev, geo, r):
+    """A partial last row tile of 2 * 256 + r rows: its waves whose rows end
+    inside their first 32-row block run that block's MFMAs only.  bf16
+    128 -> 128 on the wide tiles (64-row waves), the small tiles (64-row
+    waves over 128-row tiles) and Q8_0 128 -> 128 (128-row waves), every
+    row against the oracle."""
+    import oracle
+    import torch
+
+    nat = geo
+    n = 512 + r
+    coords = spc.workloads.random_voxels(n + 400, 14, batches=1, seed=r)[:n]
+    coords = np.ascontiguousarray(coords)
+    _case(f"partial tile N={n} (r={r}): bf16 wide / small, Q8_0")
+    (xh, wh, bh), (x, w, b) = _inputs(spc, orc, n, 128, 128, 27, seed=r + 5)
+    m = nat.map_build(torch.from_numpy(coords).to(dev))
+    tm = m.token_major.cpu().numpy()
+    pw = nat.pack_weights(w)
+    yw, ys = _both(nat, lambda: nat.sparse_conv(x, pw, b, m.token_major, ntaps=27, n_out=n,
+                                                plan=nat.conv_plan(m.token_major, ntaps=27,
+                                                                   n_out=n)))
+    ref = orc.sparse_conv(xh, wh, bh, tm, ntaps=27, n_out=n, idx_layout=1, out_dtype=oracle.F32,
+                          x_dtype=oracle.BF16, w_dtype=oracle.BF16, b_dtype=oracle.BF16,
+                          nthreads=oracle_threads(), blocked=True)
+    check_16bit(f"partial tile wide N={n}", from_dev(yw), ref)
+    check_16bit(f"partial tile small N={n}", from_dev(ys), ref)
+    # Q8_0 weights (in-register dequantisation: 4 waves of 128 x 64 rows)
+    blocks = orc.q8_0_quantize(spc.workloads.normal((128, 27, 128), 0.05, seed=r + 9))
+    qs, dsc = nat.q8_0_repack(torch.from_numpy(blocks).to(dev))
+    pq = nat.pack_weights(qs, dsc, cin=128, cout=128)
+    nat.set_tile_geometry(nat.TILES_WIDE)
+    yq = nat.sparse_conv(x, pq, b, m.token_major, ntaps=27, n_out=n)
+    torch.cuda.synchronize()
+    nat.set_tile_geometry(nat.TILES_AUTO)
+    # the kernel's operands bf16(f32(d) * q): one bf16 rounding per element
+    wq = orc.q8_0_dequant(blocks, oracle.BF16)
+    refq = orc.sparse_conv(xh, wq, bh, tm, ntaps=27, n_out=n, idx_layout=1, out_dtype=oracle.F32,
+                           x_dtype=oracle.BF16, w_dtype=oracle.BF16, b_dtype=oracle.BF16,
+                           nthreads=oracle_threads(), blocked=True)
+    check_16bit(f"partial tile Q8_0 wide N={n}", from_dev(yq), refq)
