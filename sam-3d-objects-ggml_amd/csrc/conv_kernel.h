@@ -200,11 +200,13 @@ constexpr int kSegs = 4;        // 16-byte segments per staged 64-byte row chunk
 //             112 KB of A stage, one workgroup of 8 waves per CU -- the wide
 //             convs, where every tile is long.
 //   GeoSmall  128 rows (64 for the 8-tap stride-2 conv, whose 128 coarse
-//             rows reference ~680 fine rows), 511-row stage, one buffer,
-//             80-byte padded rows: ~51 KB of LDS, three workgroups of 4 waves
-//             per CU, which hide each other's staging and setup latency --
-//             the short tiles of small channel counts, small row counts and
-//             stride-2.
+//             rows reference ~680 fine rows), 511-row stage, swizzled rows,
+//             one buffer: ~42 KB of LDS, three workgroups of 4 waves per CU,
+//             which hide each other's staging and setup latency -- the short
+//             tiles of small channel counts, small row counts and stride-2.
+//             (A double-buffered variant measured no faster: stride-2
+//             128 -> 128 11.6 -> 11.5 us, subdivided 128^3 C=64 24.7 -> 27.4
+//             us with two workgroups per CU instead of three.)
 // Staged row layouts (one 64-byte chunk of a union row = four 16-byte
 // segments; a wave's A-fragment read takes one segment of 32 slots, which
 // the LDS serves 16 lanes at a time):
@@ -243,8 +245,8 @@ struct Geo {
 };
 using GeoWide = Geo<256, 895, 2, true>;
 template <int NTAPS>
-using GeoSmall = Geo<NTAPS == 8 ? 64 : 128, 511, 1, false>;
-static_assert(GeoWide::STAGE == 3584 && GeoSmall<27>::STAGE == 2560, "stage geometry");
+using GeoSmall = Geo<NTAPS == 8 ? 64 : 128, 511, 1, true>;
+static_assert(GeoWide::STAGE == 3584 && GeoSmall<27>::STAGE == 2048, "stage geometry");
 
 // Plan buffer: the GeoWide plan of every 256-row tile, then the GeoSmall
 // plan of every small tile (a conv picks its geometry by shape).
@@ -567,7 +569,7 @@ __global__ __launch_bounds__(512) void conv_plan_kernel(ConvArgs a, char* plan) 
 }
 
 // Workgroups per CU a geometry is built for: GeoWide fills the CU's LDS
-// with one; GeoSmall's ~51 KB admit three (register budget 168 per wave),
+// with one; GeoSmall's ~42 KB admit three (register budget 168 per wave),
 // two for 128-column tiles, whose 64 x 64 wave tiles need ~226 registers.
 template <typename GEO, int TN>
 constexpr int geo_blocks_per_cu() { return GEO::NBUF == 1 ? (TN >= 128 ? 2 : 3) : 1; }
@@ -1257,7 +1259,7 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
     // tile (8-byte writes, 16 in f32), then whole rows leave with coalesced
     // 16-byte stores.
     constexpr int OPITCH = TN * ES + 8;  // bytes per output-tile row in LDS
-    constexpr int NPASS = TM * OPITCH <= ABYTES ? 1 : 2;  // f32 tiles go in two halves
+    constexpr int NPASS = TM * OPITCH <= ABYTES ? 1 : TM / 2 * OPITCH <= ABYTES ? 2 : 4;  // wide f32 tiles go in parts
     constexpr int RPP = TM / NPASS;      // tile rows per pass
     static_assert(RPP * OPITCH <= ABYTES && RPP % 32 == 0, "output tile fits the A stage");
     constexpr int UPR = TN * ES / 16;    // 16-byte units per output row
