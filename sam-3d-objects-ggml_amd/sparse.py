@@ -105,33 +105,38 @@ class SparseTensor:
     SparseTensor(data, shape=None, layout=None, **kwargs); kwargs `scale`
     and `spatial_cache` as in SP/basic.py:55-137."""
 
+    # the two constructor forms: a leading tensor selects the first, a
+    # leading SparseTensorData (or, with no positional argument, a `data`
+    # keyword) the second
+    _FORMS = (("feats", "coords", "shape", "layout"), ("data", "shape", "layout"))
+
     def __init__(self, *args, **kwargs):
-        if len(args) != 0:
-            method = 0 if isinstance(args[0], torch.Tensor) else 1
+        if args:
+            names = self._FORMS[0 if isinstance(args[0], torch.Tensor) else 1]
         else:
-            method = 1 if "data" in kwargs else 0
-        if method == 0:
-            feats, coords, shape, layout = args + (None,) * (4 - len(args))
-            feats = kwargs.pop("feats", feats)
-            coords = kwargs.pop("coords", coords)
-            shape = kwargs.pop("shape", shape)
-            layout = kwargs.pop("layout", layout)
-            if shape is None:
-                shape = self._cal_shape(feats, coords)
-            if layout is None:
-                layout = self._cal_layout(coords, shape[0])
-            spatial = (coords.max(0)[0] + 1).tolist()[1:] if coords.shape[0] else [0, 0, 0]
-            self.data = SparseTensorData(feats, coords, spatial, shape[0])
+            names = self._FORMS[1 if "data" in kwargs else 0]
+        if len(args) > len(names):
+            raise TypeError(f"SparseTensor takes at most {len(names)} positional arguments")
+        given = dict(zip(names, args))
+        for name in names:
+            if name in kwargs:
+                given[name] = kwargs[name]  # a keyword wins over the positional slot
+        if "data" in names:
+            self.data = given.get("data")
         else:
-            data, shape, layout = args + (None,) * (3 - len(args))
-            data = kwargs.pop("data", data)
-            shape = kwargs.pop("shape", shape)
-            layout = kwargs.pop("layout", layout)
-            self.data = data
-            if shape is None:
-                shape = self._cal_shape(self.feats, self.coords)
-            if layout is None:
-                layout = self._cal_layout(self.coords, shape[0])
+            coords = given.get("coords")
+            shape0 = given.get("shape")
+            n_b = shape0[0] if shape0 is not None else self._batch_count(coords)
+            extent = [0, 0, 0]
+            if coords.shape[0]:
+                extent = [int(v) + 1 for v in coords[:, 1:].amax(0).tolist()]
+            self.data = SparseTensorData(given.get("feats"), coords, extent, n_b)
+        shape = given.get("shape")
+        if shape is None:
+            shape = torch.Size([self._batch_count(self.coords), *self.feats.shape[1:]])
+        layout = given.get("layout")
+        if layout is None:
+            layout = self._batch_slices(self.coords, shape[0])
         self._shape = torch.Size(shape)
         self._layout = layout
         self._scale = kwargs.get("scale", (1, 1, 1))
@@ -143,17 +148,16 @@ class SparseTensor:
                     f"the rows of batch {i} are not contiguous"
 
     @staticmethod
-    def _cal_shape(feats, coords):
-        return torch.Size([int(coords[:, 0].max().item()) + 1, *feats.shape[1:]])
+    def _batch_count(coords) -> int:
+        """Batch items: one past the largest batch index."""
+        return int(coords[:, 0].max().item()) + 1
 
     @staticmethod
-    def _cal_layout(coords, batch_size):
-        seq = torch.bincount(coords[:, 0], minlength=batch_size).tolist()
-        out, start = [], 0
-        for n in seq[:batch_size]:
-            out.append(slice(start, start + n))
-            start += n
-        return out
+    def _batch_slices(coords, batch_size) -> List[slice]:
+        """Row range of each batch item (rows of an item are contiguous)."""
+        sizes = torch.bincount(coords[:, 0], minlength=batch_size)[:batch_size]
+        ends = torch.cumsum(sizes, 0).tolist()
+        return [slice(e - int(c), e) for e, c in zip(ends, sizes.tolist())]
 
     # -- accessors ----------------------------------------------------------
     @property
@@ -193,22 +197,18 @@ class SparseTensor:
 
     # -- conversions --------------------------------------------------------
     def to(self, *args, **kwargs) -> "SparseTensor":
-        device = dtype = None
+        """to(device), to(dtype), to(device, dtype) or the keywords; the
+        coordinates follow the device only."""
+        target = {"device": None, "dtype": None}
         if len(args) == 2:
-            device, dtype = args
+            target["device"], target["dtype"] = args
         elif len(args) == 1:
-            if isinstance(args[0], torch.dtype):
-                dtype = args[0]
-            else:
-                device = args[0]
-        if "dtype" in kwargs:
-            assert dtype is None, "to() received multiple values for argument 'dtype'"
-            dtype = kwargs["dtype"]
-        if "device" in kwargs:
-            assert device is None, "to() received multiple values for argument 'device'"
-            device = kwargs["device"]
-        return self.replace(self.feats.to(device=device, dtype=dtype),
-                            self.coords.to(device=device))
+            target["dtype" if isinstance(args[0], torch.dtype) else "device"] = args[0]
+        for k in ("device", "dtype"):
+            if k in kwargs:
+                assert target[k] is None, f"to() received multiple values for argument '{k}'"
+                target[k] = kwargs[k]
+        return self.replace(self.feats.to(**target), self.coords.to(device=target["device"]))
 
     def type(self, dtype) -> "SparseTensor":
         return self.replace(self.feats.type(dtype))
@@ -250,11 +250,18 @@ class SparseTensor:
 
     @staticmethod
     def full(aabb, dim, value, dtype=torch.float32, device=None) -> "SparseTensor":
-        n, c = dim
-        axes = [torch.arange(aabb[i], aabb[i + 3] + 1) for i in range(3)]
-        grid = torch.stack(torch.meshgrid(*axes, indexing="ij"), dim=-1).reshape(-1, 3)
-        b = torch.arange(n).view(-1, 1).repeat(1, grid.shape[0]).view(-1, 1)
-        coords = torch.cat([b, grid.repeat(n, 1)], dim=1).to(dtype=torch.int32, device=device)
+        """Every voxel of the inclusive box aabb = (x0, y0, z0, x1, y1, z1)
+        in each of dim[0] batch items, dim[1] channels of `value`; rows in
+        (b, x, y, z) lexicographic order."""
+        n_b, c = dim
+        lo = torch.tensor(aabb[:3], dtype=torch.int64)
+        ext = torch.tensor(aabb[3:], dtype=torch.int64) - lo + 1
+        cells = int(ext.prod())
+        r = torch.arange(n_b * cells, dtype=torch.int64)
+        local = r % cells
+        coords = torch.stack([r // cells, lo[0] + local // (ext[1] * ext[2]),
+                              lo[1] + (local // ext[2]) % ext[1], lo[2] + local % ext[2]], 1)
+        coords = coords.to(dtype=torch.int32, device=device)
         feats = torch.full((coords.shape[0], c), value, dtype=dtype, device=device)
         return SparseTensor(feats=feats, coords=coords)
 
@@ -297,30 +304,32 @@ class SparseTensor:
     def __rtruediv__(self, other):
         return self._elemwise(other, lambda x, y: torch.div(y, x))
 
-    def __getitem__(self, idx) -> "SparseTensor":
+    def _batch_ids(self, idx) -> List[int]:
+        """Batch items an index selects: an int, a slice, a bool mask over
+        the items or an int32 / int64 vector of item indices."""
         if isinstance(idx, int):
-            idx = [idx]
-        elif isinstance(idx, slice):
-            idx = range(*idx.indices(self.shape[0]))
-        elif isinstance(idx, torch.Tensor):
-            if idx.dtype == torch.bool:
-                assert idx.shape == (self.shape[0],), f"Invalid index shape: {idx.shape}"
-                idx = idx.nonzero().squeeze(1)
-            elif idx.dtype in (torch.int32, torch.int64):
-                assert idx.dim() == 1, f"Invalid index shape: {idx.shape}"
-            else:
-                raise ValueError(f"Unknown index type: {idx.dtype}")
-            idx = idx.tolist()
-        else:
+            return [idx]
+        if isinstance(idx, slice):
+            return list(range(self.shape[0]))[idx]
+        if not isinstance(idx, torch.Tensor):
             raise ValueError(f"Unknown index type: {type(idx)}")
-        coords, feats = [], []
-        for new_b, old_b in enumerate(idx):
-            c = self.coords[self.layout[old_b]].clone()
-            c[:, 0] = new_b
-            coords.append(c)
-            feats.append(self.feats[self.layout[old_b]])
-        return SparseTensor(feats=torch.cat(feats, 0).contiguous(),
-                            coords=torch.cat(coords, 0).contiguous())
+        if idx.dtype == torch.bool:
+            assert idx.shape == (self.shape[0],), f"Invalid index shape: {idx.shape}"
+            return torch.nonzero(idx).flatten().tolist()
+        if idx.dtype not in (torch.int32, torch.int64):
+            raise ValueError(f"Unknown index type: {idx.dtype}")
+        assert idx.dim() == 1, f"Invalid index shape: {idx.shape}"
+        return idx.tolist()
+
+    def __getitem__(self, idx) -> "SparseTensor":
+        """The selected batch items, renumbered 0.. in selection order."""
+        rows = [self.layout[b] for b in self._batch_ids(idx)]
+        coords = torch.cat([self.coords[r] for r in rows], 0)
+        coords[:, 0] = torch.repeat_interleave(
+            torch.arange(len(rows), dtype=coords.dtype, device=coords.device),
+            torch.tensor([r.stop - r.start for r in rows], device=coords.device))
+        feats = torch.cat([self.feats[r] for r in rows], 0)
+        return SparseTensor(feats=feats.contiguous(), coords=coords.contiguous())
 
     # -- spatial cache (keyed by the current scale) -------------------------
     def register_spatial_cache(self, key, value) -> None:

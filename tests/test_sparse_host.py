@@ -100,6 +100,10 @@ def test_getitem_cat_unbind(sp):
     assert [p.feats.shape[0] for p in parts] == [3, 2]
     cols = x.unbind(1)
     assert len(cols) == 3 and torch.equal(cols[1].feats, x.feats[:, 1])
+    rev = x[torch.tensor([1, 0])]  # items renumbered in selection order
+    assert rev.coords[:, 0].tolist() == [0, 0, 1, 1, 1]
+    assert torch.equal(rev.feats, torch.cat([x.feats[3:5], x.feats[:3]]))
+    assert torch.equal(x[::-1].feats, rev.feats)
     with pytest.raises(ValueError):
         x[torch.tensor([0.5])]
 
