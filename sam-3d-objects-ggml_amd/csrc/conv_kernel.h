@@ -607,6 +607,17 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
     __shared__ int32_t wsum[NW];
     __shared__ __attribute__((aligned(16))) int32_t misc[8];
     __shared__ __attribute__((aligned(16))) float sbias[TN];
+    // Per-wave epilogue (16-bit outputs of the wide 8-wave tiles): once a wave
+    // is done with the last chunk it writes its own block through a private
+    // LDS region and stores it, while the other waves still compute.  The
+    // regions are the stage buffer the last chunk does not read, and PWX
+    // more here for the waves it cannot hold.
+    constexpr int PW_PITCH = WTN * ES + 16;      // bytes per row of a wave's block
+    constexpr int PW_BYTES = WTM * PW_PITCH;
+    constexpr bool PWE = ES == 2 && NBUF == 2 && NW == 8 && WTM * WTN <= 4096;
+    constexpr int PW_IN_STAGE = PWE ? STAGE * 16 / PW_BYTES : 0;  // regions in the free buffer
+    constexpr int PWX = PWE && PW_IN_STAGE < NW ? NW - PW_IN_STAGE : 0;
+    __shared__ __attribute__((aligned(16))) char pw_extra[PWX > 0 ? PWX * PW_BYTES : 16];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1251,6 +1262,79 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
             }
         }
         }  // passes
+        return;
+    }
+
+    // ---- per-wave epilogue (staged fast path, 16-bit output, no norm): the
+    // wave's rounded block goes to its private LDS region (the last chunk
+    // reads only its own buffer, so the other one is free) and back as
+    // whole 16-byte pieces of its rows, which leave with coalesced
+    // non-temporal stores -- no barrier, so early waves store while the
+    // late ones finish their MFMAs.  Same values as the tile epilogue below.
+    if constexpr (PWE) if (dma) {
+        const int freebuf = ((kch - 1) & 1) ^ 1;
+        char* reg = wave < PW_IN_STAGE
+                        ? reinterpret_cast<char*>(Au + freebuf * STAGE) + wave * PW_BYTES
+                        : pw_extra + (wave - PW_IN_STAGE) * PW_BYTES;
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            const int rl = i * 32 + (lane & 31);
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int cl = j * 32 + 8 * g + 4 * (lane >> 5);
+                    *reinterpret_cast<u32x2*>(reg + rl * PW_PITCH + cl * ES) =
+                        u32x2{(uint32_t)M::cvt(acc[i][j][4 * g]) | ((uint32_t)M::cvt(acc[i][j][4 * g + 1]) << 16),
+                              (uint32_t)M::cvt(acc[i][j][4 * g + 2]) | ((uint32_t)M::cvt(acc[i][j][4 * g + 3]) << 16)};
+                }
+        }
+        // the reads below take other lanes' writes: keep the compiler from
+        // moving them up, and let the writes land
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0)
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        constexpr int UPW = WTN * ES / 16;     // 16-byte pieces per row of the block
+        constexpr int NUW = WTM * UPW / 64;    // per lane
+        static_assert(WTM * UPW % 64 == 0, "per-wave store geometry");
+        char* yb = static_cast<char*>(a.y);
+        const int64_t col = co0 + wn * WTN;
+        int32_t tt[NUW];
+        u32x4 vv[NUW];
+#pragma unroll
+        for (int k = 0; k < NUW; ++k) {
+            const int c = k * 64 + lane;
+            const int r = c / UPW;
+            tt[k] = srow[wm * WTM + r];
+            vv[k] = *reinterpret_cast<const u32x4*>(reg + r * PW_PITCH + (c % UPW) * 16);
+        }
+        if (a.epi_mode == SPC_EPI_RESIDUAL) {
+            // y = dt(dt(conv + bias) + residual), as in the tile epilogue
+#pragma unroll
+            for (int k = 0; k < NUW; ++k) {
+                int32_t rr = tt[k];
+                if (a.residual_rows && rr >= 0) {
+                    const int32_t v = a.residual_rows[rr];
+                    rr = (v >= 0 && v < a.n_residual) ? v : -1;
+                }
+                const u32x4 rv = rr >= 0 ? *reinterpret_cast<const u32x4*>(
+                                               static_cast<const char*>(a.residual) +
+                                               ((int64_t)rr * a.cout + col) * ES + ((k * 64 + lane) % UPW) * 16)
+                                         : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float lo = M::unpack(vv[k][e], 0) + M::unpack(rv[e], 0);
+                    const float hi = M::unpack(vv[k][e], 1) + M::unpack(rv[e], 1);
+                    vv[k][e] = (uint32_t)M::cvt(lo) | ((uint32_t)M::cvt(hi) << 16);
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < NUW; ++k)
+            if (tt[k] >= 0)
+                __builtin_nontemporal_store(
+                    vv[k], reinterpret_cast<u32x4*>(yb + ((int64_t)tt[k] * a.cout + col) * ES +
+                                                    ((k * 64 + lane) % UPW) * 16));
         return;
     }
 
