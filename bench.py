@@ -60,7 +60,7 @@ def parse():
                     help="target duration of the all-core CPU baseline sample (5 runs)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only time a 256 MiB device copy (PMC traffic calibration)")
-    ap.add_argument("--tiles", choices=["auto", "wide", "small"], default="auto",
+    ap.add_argument("--tiles", choices=["auto", "wide", "small", "tall"], default="auto",
                     help="conv tile geometry (auto: each conv picks by shape)")
     ap.add_argument("--bf16-weights", action="store_true",
                     help="config 5: the same conv with bf16 weights (no Q8_0 dequantisation)")
@@ -273,7 +273,7 @@ def main():
     torch.cuda.set_device(dev)
 
     nat.set_tile_geometry({"auto": nat.TILES_AUTO, "wide": nat.TILES_WIDE,
-                           "small": nat.TILES_SMALL}[args.tiles])
+                           "small": nat.TILES_SMALL, "tall": nat.TILES_TALL}[args.tiles])
     cfg = args.config
     if cfg == 2:
         coords = wl.ellipsoid_batch()

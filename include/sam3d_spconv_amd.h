@@ -284,25 +284,33 @@ int spc_sparse_conv_plan(spc_stream_t stream, int dtype, const void* x, int w_dt
                          const void* plan, int64_t ntaps, int64_t n_out, int64_t n_in,
                          int64_t cin, int64_t cout);
 
-/* Tile geometry of the conv kernel.  Every conv runs on one of two:
+/* Tile geometry of the conv kernel.  Every conv runs on one of three:
  *   SPC_TILES_WIDE   256-row tiles over an 895-row double-buffered stage,
  *                    one 8-wave workgroup per CU (long tiles: wide channels);
  *   SPC_TILES_SMALL  128-row tiles (64 for 8 taps) over a 511-row stage,
  *                    two or three 4-wave workgroups per CU (short tiles: small
- *                    channel counts, few rows, the stride-2 conv).
- * Both give the same results.  By default (SPC_TILES_AUTO) each conv picks
+ *                    channel counts, few rows, the stride-2 conv);
+ *   SPC_TILES_TALL   256-row tiles over a 559-row stage, three 4-wave
+ *                    workgroups per CU (one-chunk rows: 16-bit C_in = 32 with
+ *                    C_out 32 or 64); reads the wide tiles' plan section.
+ * All give the same results.  By default (SPC_TILES_AUTO) each conv picks
  * by shape; spc_conv_set_tile_geometry forces one for every later conv of
  * the process (measurements, tests; initially from the environment
- * variable SPC_CONV_GEOMETRY = "wide" / "small").  The small tiles apply to
- * packed weights with 27 or 8 taps.  Plans (spc_conv_plan) hold both.  No
- * reference counterpart. */
+ * variable SPC_CONV_GEOMETRY = "wide" / "small" / "tall").  The small tiles
+ * apply to packed weights with 27 or 8 taps, the tall ones to packed
+ * weights with 27 taps and C_out a multiple of 32, without the norm
+ * epilogue or weight classes (elsewhere a forced geometry that does not
+ * apply leaves the choice by shape).  Plans (spc_conv_plan) hold the wide
+ * and the small sections.  No reference counterpart. */
 #define SPC_TILES_AUTO 0
 #define SPC_TILES_WIDE 1
 #define SPC_TILES_SMALL 2
+#define SPC_TILES_TALL 3
 int spc_conv_set_tile_geometry(int geometry);
-/* The geometry (SPC_TILES_WIDE / SPC_TILES_SMALL) a conv with packed weights
+/* The geometry (SPC_TILES_WIDE / SMALL / TALL) a conv with packed weights
  * and these arguments runs now (epi_mode a spc_epilogue_mode, class_rows 0
- * without weight classes): which plan section it reads. */
+ * without weight classes); SPC_TILES_SMALL reads the small plan section,
+ * the others the wide one. */
 int spc_conv_tile_geometry(int dtype, int w_dtype, int64_t ntaps, int64_t n_out, int64_t cin,
                            int64_t cout, int64_t class_rows, int epi_mode);
 

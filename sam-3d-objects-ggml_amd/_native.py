@@ -426,24 +426,34 @@ def expand_q8_0(packed: PackedWeights, out: torch.Tensor | None = None) -> Packe
     return PackedWeights(out, BF16, packed.ntaps, packed.cin, packed.cout)
 
 
-TILES_AUTO, TILES_WIDE, TILES_SMALL = 0, 1, 2
+TILES_AUTO, TILES_WIDE, TILES_SMALL, TILES_TALL = 0, 1, 2, 3
 PLAN_WIDE, PLAN_SMALL = 1, 2
+
+
+def tile_geometry(dtype: torch.dtype, *, ntaps: int, n_out: int, cin: int, cout: int,
+                  q8: bool = False, class_rows: int = 0, epi_mode: int = 0) -> int:
+    """spc_conv_tile_geometry: the geometry (TILES_WIDE / TILES_SMALL /
+    TILES_TALL) a packed-weight conv with these arguments runs now."""
+    dt = dtype_code(dtype)
+    return lib().spc_conv_tile_geometry(dt, Q8_0 if q8 else dt, ntaps, n_out, cin, cout,
+                                        class_rows, epi_mode)
 
 
 def plan_section(dtype: torch.dtype, *, ntaps: int, n_out: int, cin: int, cout: int,
                  q8: bool = False, class_rows: int = 0, epi_mode: int = 0) -> int:
     """The plan section (PLAN_WIDE / PLAN_SMALL) a packed-weight conv with
-    these arguments reads (spc_conv_tile_geometry)."""
-    dt = dtype_code(dtype)
-    g = lib().spc_conv_tile_geometry(dt, Q8_0 if q8 else dt, ntaps, n_out, cin, cout,
-                                     class_rows, epi_mode)
+    these arguments reads: the small tiles read the small section, the wide
+    and the tall tiles the wide one."""
+    g = tile_geometry(dtype, ntaps=ntaps, n_out=n_out, cin=cin, cout=cout, q8=q8,
+                      class_rows=class_rows, epi_mode=epi_mode)
     return PLAN_SMALL if g == TILES_SMALL else PLAN_WIDE
 
 
 def set_tile_geometry(geometry: int) -> None:
-    """spc_conv_set_tile_geometry: TILES_WIDE / TILES_SMALL force the conv
-    kernel's tile geometry for every later conv of the process; TILES_AUTO
-    (the default) lets each conv pick by shape.  Results are the same."""
+    """spc_conv_set_tile_geometry: TILES_WIDE / TILES_SMALL / TILES_TALL
+    force the conv kernel's tile geometry for every later conv of the
+    process (where it applies); TILES_AUTO (the default) lets each conv pick
+    by shape.  Results are the same."""
     _check("spc_conv_set_tile_geometry", lib().spc_conv_set_tile_geometry(int(geometry)))
 
 

@@ -350,11 +350,12 @@ BridgePlan* bridge_plan(hipStream_t s, int64_t n, int geometry) {
 }
 
 // Tile-geometry override (spc_conv_set_tile_geometry; initially from
-// SPC_CONV_GEOMETRY=wide / small): 0 = each conv picks by shape.
+// SPC_CONV_GEOMETRY=wide / small / tall): 0 = each conv picks by shape.
 std::atomic<int> g_geometry{[] {
     const char* e = getenv("SPC_CONV_GEOMETRY");
     if (e && strcmp(e, "wide") == 0) return SPC_TILES_WIDE;
     if (e && strcmp(e, "small") == 0) return SPC_TILES_SMALL;
+    if (e && strcmp(e, "tall") == 0) return SPC_TILES_TALL;
     return SPC_TILES_AUTO;
 }()};
 int geometry_override() { return g_geometry.load(std::memory_order_relaxed); }
@@ -732,21 +733,23 @@ int spc_conv_tile_geometry(int dtype, int w_dtype, int64_t ntaps, int64_t n_out,
     a.epi_mode = epi_mode;
     a.num_cu = device_cu_count();
     a.geometry = geometry_override();
-    bool small = false;
+    int g = SPC_TILES_WIDE;
     auto pick = [&](auto t_c, auto q8_c) {
         using T = decltype(t_c);
         constexpr bool Q8 = decltype(q8_c)::value;
-        if (ntaps == 27) small = use_small_tiles<T, Q8, true, 27>(a);
-        else if (ntaps == 8) small = use_small_tiles<T, Q8, true, 8>(a);
+        if (ntaps == 27 && use_tall_tiles<T, Q8, true, 27>(a)) g = SPC_TILES_TALL;
+        else if (ntaps == 27 && use_small_tiles<T, Q8, true, 27>(a)) g = SPC_TILES_SMALL;
+        else if (ntaps == 8 && use_small_tiles<T, Q8, true, 8>(a)) g = SPC_TILES_SMALL;
     };
     if (w_dtype == SPC_Q8_0) pick(__bf16{}, std::true_type{});
     else if (dtype == SPC_F32) pick(float{}, std::false_type{});
     else pick(__bf16{}, std::false_type{});  // bf16 and f16: 2-byte rows
-    return small ? SPC_TILES_SMALL : SPC_TILES_WIDE;
+    return g;
 }
 
 int spc_conv_set_tile_geometry(int geometry) {
-    if (geometry != SPC_TILES_AUTO && geometry != SPC_TILES_WIDE && geometry != SPC_TILES_SMALL) {
+    if (geometry != SPC_TILES_AUTO && geometry != SPC_TILES_WIDE && geometry != SPC_TILES_SMALL &&
+        geometry != SPC_TILES_TALL) {
         set_last_error("spc_conv_set_tile_geometry: unknown geometry %d", geometry);
         return SPC_BAD_ARG;
     }

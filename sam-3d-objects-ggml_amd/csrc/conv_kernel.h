@@ -207,6 +207,15 @@ constexpr int kSegs = 4;        // 16-byte segments per staged 64-byte row chunk
 //             (A double-buffered variant measured no faster: stride-2
 //             128 -> 128 11.6 -> 11.5 us, subdivided 128^3 C=64 24.7 -> 27.4
 //             us with two workgroups per CU instead of three.)
+//   GeoTall   256 rows over one 559-row stage (the most that keeps three
+//             workgroups of 4 waves per CU: ~53 KB of LDS each), twice the
+//             rows in flight per CU of GeoSmall -- rows of one 64-byte chunk,
+//             whose tiles are mostly setup and staging latency and whose
+//             256-row union fits on surface-like sets (the subdivided 256^3
+//             shell: 429 rows on average, 523 at most).  It reads the wide
+//             tiles' plans (same row tiles, slot keys and plan layout); a tile
+//             whose union exceeds its stage takes the per-tap fallback, two
+//             taps per round, about four times the staged tile's time.
 // Staged row layouts (one 64-byte chunk of a union row = four 16-byte
 // segments; a wave's A-fragment read takes one segment of 32 slots, which
 // the LDS serves 16 lanes at a time):
@@ -218,7 +227,7 @@ constexpr int kSegs = 4;        // 16-byte segments per staged 64-byte row chunk
 //               groups as well, without the 16 bytes of padding per row.
 // A slot key is the unit of segment 0's position base: unit(s) = key + s
 // (padded) or key ^ s (swizzled: the key's low two bits carry the swizzle).
-template <int TM_, int UMAX_, int NBUF_, bool SW_>
+template <int TM_, int UMAX_, int NBUF_, bool SW_, int PUMAX_ = UMAX_>
 struct Geo {
     static constexpr int TM = TM_;
     static constexpr int UMAX = UMAX_;
@@ -226,6 +235,10 @@ struct Geo {
     static constexpr bool SW = SW_;
     static constexpr int PITCH = SW ? 4 : 5;            // 16-byte units per staged row
     static constexpr int UROWCAP = (UMAX + 3) / 4 * 4;  // union-row table (16-byte multiple)
+    static constexpr int PUROWCAP = (PUMAX_ + 3) / 4 * 4;  // the plan's union-row table
+    // the plan section the geometry reads: the 256-row tiles' (up to 895
+    // union rows) or the small tiles'
+    static constexpr bool WIDE_PLAN = TM_ == 256 && PUMAX_ == 895;
     // 16-byte units per A buffer: whole 64-unit blocks (one LDS-DMA
     // instruction each) holding the UMAX union rows and the zero row
     static constexpr int STAGE = ((UMAX + 1) * PITCH + 63) / 64 * 64;
@@ -238,7 +251,7 @@ struct Geo {
     // weights.
     static constexpr int PLAN_SROW = 64;
     static constexpr int PLAN_UROW = PLAN_SROW + 4 * TM;
-    static constexpr int PLAN_SIDX = PLAN_UROW + 4 * UROWCAP;
+    static constexpr int PLAN_SIDX = PLAN_UROW + 4 * PUROWCAP;
     __host__ __device__ static constexpr int64_t plan_tile_bytes(int ntaps) {
         return (PLAN_SIDX + 2 * (int64_t)(ntaps + 1) * TM + 255) / 256 * 256;
     }
@@ -246,7 +259,12 @@ struct Geo {
 using GeoWide = Geo<256, 895, 2, true>;
 template <int NTAPS>
 using GeoSmall = Geo<NTAPS == 8 ? 64 : 128, 511, 1, true>;
-static_assert(GeoWide::STAGE == 3584 && GeoSmall<27>::STAGE == 2048, "stage geometry");
+using GeoTall = Geo<256, 559, 1, true, 895>;
+static_assert(GeoWide::STAGE == 3584 && GeoSmall<27>::STAGE == 2048 && GeoTall::STAGE == 2240,
+              "stage geometry");
+static_assert(GeoTall::WIDE_PLAN && GeoTall::plan_tile_bytes(27) == GeoWide::plan_tile_bytes(27) &&
+                  GeoTall::PLAN_SIDX == GeoWide::PLAN_SIDX && !GeoSmall<27>::WIDE_PLAN,
+              "the tall tiles read the wide plan");
 
 // Plan buffer: the GeoWide plan of every 256-row tile, then the GeoSmall
 // plan of every small tile (a conv picks its geometry by shape).
@@ -569,8 +587,9 @@ __global__ __launch_bounds__(512) void conv_plan_kernel(ConvArgs a, char* plan) 
 }
 
 // Workgroups per CU a geometry is built for: GeoWide fills the CU's LDS
-// with one; GeoSmall's ~42 KB admit three (register budget 168 per wave),
-// two for 128-column tiles, whose 64 x 64 wave tiles need ~226 registers.
+// with one; GeoSmall's ~42 KB and GeoTall's ~53 KB admit three (register
+// budget 168 per wave), two for 128-column tiles, whose 64 x 64 wave tiles
+// need ~226 registers.
 template <typename GEO, int TN>
 constexpr int geo_blocks_per_cu() { return GEO::NBUF == 1 ? (TN >= 128 ? 2 : 3) : 1; }
 
@@ -664,18 +683,21 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
                                                          tm * GEO::plan_tile_bytes(NTAPS));
         constexpr int NHD = 2, NTW = 2;              // header and tap-word units
         constexpr int NSR = TM / 4;                  // srow units
-        constexpr int NUR = GEO::UROWCAP / 4;        // urow units
+        constexpr int NUR = GEO::UROWCAP / 4;        // urow units (the stage's union capacity)
+        constexpr int NURP = GEO::PUROWCAP / 4;      // urow units in the plan
         constexpr int NSI = (NTAPS + 1) * TM / 8;    // sidx units
         constexpr int TOTAL = NHD + NTW + NSR + NUR + NSI;
         constexpr int IT = (TOTAL + NT - 1) / NT;
         static_assert(GEO::PLAN_SROW == 16 * (NHD + NTW) && GEO::PLAN_UROW == GEO::PLAN_SROW + 16 * NSR &&
-                          GEO::PLAN_SIDX == GEO::PLAN_UROW + 16 * NUR,
+                          GEO::PLAN_SIDX == GEO::PLAN_UROW + 16 * NURP && NURP >= NUR,
                       "plan sections are contiguous");
         u32x4 pv[IT];
 #pragma unroll
         for (int k = 0; k < IT; ++k) {
             const int u = tid + k * NT;
-            if (u < TOTAL) pv[k] = pt[u];
+            // union rows past the stage's capacity are not copied: such a
+            // tile takes the fallback, which does not read them
+            if (u < TOTAL) pv[k] = pt[u < NHD + NTW + NSR + NUR ? u : u + (NURP - NUR)];
         }
 #pragma unroll
         for (int k = 0; k < IT; ++k) {
@@ -1452,7 +1474,7 @@ hipError_t launch_conv(hipStream_t s, ConvArgs a) {
     const int64_t grid = a.tiles_per_xcd * 8 + (a.total_tiles - a.heavy_tiles);
     if (grid == 0) return hipSuccess;
     // the plan buffer holds the wide plans, then the small ones
-    if (a.plan && !std::is_same<GEO, GeoWide>::value)
+    if (a.plan && !GEO::WIDE_PLAN)
         a.plan = static_cast<const char*>(a.plan) + plan_wide_bytes(a.n_out, NTAPS);
     conv_kernel<T, Q8, PACKED, NTAPS, TN, WM, WN, 4, GEO><<<(unsigned)grid, WM * WN * 64, 0, s>>>(a);
     return hipGetLastError();
@@ -1508,7 +1530,7 @@ bool use_small_tiles(const ConvArgs& a) {
         return false;
     } else {
         if (a.epi_mode == SPC_EPI_NORM_MOD_SILU && a.cout > 64) return false;
-        if (a.geometry != 0) return a.geometry == 2;
+        if (a.geometry == SPC_TILES_WIDE || a.geometry == SPC_TILES_SMALL) return a.geometry == SPC_TILES_SMALL;
         if (a.class_rows > 0) return false;
         if (NTAPS == 8) return true;
         const int64_t kch = (int64_t)a.cin * (int64_t)sizeof(T) / 64;
@@ -1516,6 +1538,30 @@ bool use_small_tiles(const ConvArgs& a) {
         const int64_t tiles_m = ceil_div(a.n_out, GeoWide::TM);
         return a.cout % 128 == 0 && tiles_m * (a.cout / 128) > a.num_cu;
     }
+}
+
+// Tall tiles (GeoTall: 256 rows over one 559-row stage, three 4-wave
+// workgroups per CU): the SubM convs whose rows are one 64-byte chunk
+// (C_in = 32 in 16-bit, 16 in f32) and whose C_out is 32 or 64 -- where a
+// 128-row small tile is mostly setup and staging latency and only three of
+// them fit a CU.  Forced (SPC_TILES_TALL), any packed 27-tap conv with
+// 32-column multiples except the norm epilogue and weight classes.  Waves
+// 4 x 1 of 64 x 32 (64 x 64 wave tiles would spill at the 168-register
+// budget of three workgroups per CU; C_out = 64 runs two column tiles).
+template <typename T, bool Q8, bool PACKED, int NTAPS>
+bool use_tall_tiles(const ConvArgs& a) {
+    if constexpr (!PACKED || NTAPS != 27) {
+        return false;
+    } else {
+        if (a.epi_mode == SPC_EPI_NORM_MOD_SILU || a.class_rows > 0 || a.cout % 32 != 0) return false;
+        if (a.geometry != SPC_TILES_AUTO) return a.geometry == SPC_TILES_TALL;
+        return (int64_t)a.cin * (int64_t)sizeof(T) == 64 && a.cout <= 64;
+    }
+}
+
+template <typename T, bool Q8, bool PACKED, int NTAPS>
+hipError_t dispatch_tall(hipStream_t s, const ConvArgs& a) {
+    return launch_conv<T, Q8, PACKED, NTAPS, 32, 4, 1, GeoTall>(s, a);
 }
 
 // Wide tiles: TN = largest of {128, 64, 32} dividing cout, halved while the
@@ -1528,6 +1574,8 @@ hipError_t dispatch_tn(hipStream_t s, const ConvArgs& a) {
     if (a.epi_mode == SPC_EPI_NORM_MOD_SILU && a.cout != 32 && a.cout != 64 && a.cout != 128)
         return hipErrorInvalidValue;  // the epilogue's lane groups need one 32/64/128-column tile
     if constexpr (PACKED && NTAPS != 1) {
+        if constexpr (NTAPS == 27)
+            if (use_tall_tiles<T, Q8, PACKED, NTAPS>(a)) return dispatch_tall<T, Q8, PACKED, NTAPS>(s, a);
         if (use_small_tiles<T, Q8, PACKED, NTAPS>(a)) return dispatch_small<T, Q8, PACKED, NTAPS>(s, a);
     }
     const int64_t tiles_m = ceil_div(a.n_out, GeoWide::TM);

@@ -1,10 +1,12 @@
-"""The conv kernel's two tile geometries (SPC_TILES_WIDE: 256-row tiles over a
-double-buffered 895-row stage; SPC_TILES_SMALL: 128-row tiles, 64 for 8
-taps, over a single 511-row stage, several workgroups per CU) compute every
-output row with the same sequence of MFMA steps -- chunks outer, active taps
-ascending, absent taps adding exact zeros -- so their outputs are equal
-value for value, with and without a tile plan, for every dtype, epilogue and
-staging path.  The small tiles are also checked against the oracle."""
+"""The conv kernel's three tile geometries (SPC_TILES_WIDE: 256-row tiles over
+a double-buffered 895-row stage; SPC_TILES_SMALL: 128-row tiles, 64 for 8
+taps, over a single 511-row stage, several workgroups per CU;
+SPC_TILES_TALL: 256-row tiles over a single 559-row stage, reading the wide
+plan) compute every output row with the same sequence of MFMA steps --
+chunks outer, active taps ascending, absent taps adding exact zeros -- so
+their outputs are equal value for value, with and without a tile plan, for
+every dtype, epilogue and staging path.  The small and the tall tiles are
+also checked against the oracle."""
 import numpy as np
 import pytest
 
@@ -30,6 +32,20 @@ def _both(nat, fn):
 
     out = []
     for g in (nat.TILES_WIDE, nat.TILES_SMALL):
+        nat.set_tile_geometry(g)
+        out.append(fn())
+    torch.cuda.synchronize()
+    nat.set_tile_geometry(nat.TILES_AUTO)
+    return out
+
+
+def _all(nat, fn):
+    """fn() under the wide, the small and the tall tiles (the tall ones
+    apply to 27 taps; elsewhere the conv keeps its choice by shape)."""
+    import torch
+
+    out = []
+    for g in (nat.TILES_WIDE, nat.TILES_SMALL, nat.TILES_TALL):
         nat.set_tile_geometry(g)
         out.append(fn())
     torch.cuda.synchronize()
@@ -63,7 +79,7 @@ def test_subm_wide_equals_small(spc, orc, dev, geo, dt, cin, cout, nvox, grid):
     nat = geo
     coords = spc.workloads.random_voxels(nvox, grid, batches=2, seed=cin + cout)
     n = coords.shape[0]
-    _case(f"subm {dt} N={n} {cin}->{cout}: wide vs small tiles")
+    _case(f"subm {dt} N={n} {cin}->{cout}: wide vs small vs tall tiles")
     (xh, wh, bh), (x, w, b) = _inputs(spc, orc, n, cin, cout, 27, seed=cin * 7 + cout, dt=dt)
     m = nat.map_build(torch.from_numpy(coords).to(dev))
     pw = nat.pack_weights(w)
@@ -73,9 +89,9 @@ def test_subm_wide_equals_small(spc, orc, dev, geo, dt, cin, cout, nvox, grid):
         return (nat.sparse_conv(x, pw, b, m.token_major, ntaps=27, n_out=n, plan=plan),
                 nat.sparse_conv(x, pw, b, m.token_major, ntaps=27, n_out=n))
 
-    (wp, wn), (sp_, sn) = _both(nat, run)
-    assert torch.equal(wp, wn) and torch.equal(sp_, sn)
-    assert torch.equal(wp, sp_)
+    (wp, wn), (sp_, sn), (tp, tn_) = _all(nat, run)
+    assert torch.equal(wp, wn) and torch.equal(sp_, sn) and torch.equal(tp, tn_)
+    assert torch.equal(wp, sp_) and torch.equal(wp, tp)
     tm = m.token_major.cpu().numpy()
     code = {"bf16": oracle.BF16, "f16": oracle.F16, "f32": oracle.F32}[dt]
     ref = orc.sparse_conv(xh, wh, bh, tm, ntaps=27, n_out=n, idx_layout=1, out_dtype=oracle.F32,
@@ -124,14 +140,14 @@ def test_ragged_and_tiny(spc, orc, dev, geo, n):
     nat = geo
     coords = spc.workloads.random_voxels(n, 5 if n < 100 else 9, batches=1, seed=n)[:n]
     n = coords.shape[0]
-    _case(f"ragged N={n}: wide vs small tiles")
+    _case(f"ragged N={n}: wide vs small vs tall tiles")
     _, (x, w, b) = _inputs(spc, orc, n, 64, 64, 27, seed=n + 11)
     m = nat.map_build(torch.from_numpy(np.ascontiguousarray(coords)).to(dev))
     pw = nat.pack_weights(w)
-    yw, ys = _both(nat, lambda: nat.sparse_conv(x, pw, b, m.token_major, ntaps=27, n_out=n,
-                                                plan=nat.conv_plan(m.token_major, ntaps=27,
-                                                                   n_out=n)))
-    assert torch.equal(yw, ys)
+    yw, ys, yt = _all(nat, lambda: nat.sparse_conv(x, pw, b, m.token_major, ntaps=27, n_out=n,
+                                                   plan=nat.conv_plan(m.token_major, ntaps=27,
+                                                                      n_out=n)))
+    assert torch.equal(yw, ys) and torch.equal(yw, yt)
 
 
 def test_q8_0_wide_equals_small(spc, orc, dev, geo):
@@ -140,23 +156,24 @@ def test_q8_0_wide_equals_small(spc, orc, dev, geo):
     nat = geo
     coords = spc.workloads.random_voxels(15000, 32, batches=2, seed=5)
     n = coords.shape[0]
-    _case(f"Q8_0 N={n} 64->128: wide vs small tiles")
+    _case(f"Q8_0 N={n} 64->128: wide vs small vs tall tiles")
     g = torch.Generator(device="cpu").manual_seed(3)
     x = torch.randn((n, 64), generator=g).to(dev, torch.bfloat16)
     blocks = nat.q8_0_quantize((torch.randn((128, 27, 64), generator=g) * 0.02).to(dev))
     qs, dsc = nat.q8_0_repack(blocks)
     pw = nat.pack_weights(qs, dsc, cin=64, cout=128)
     m = nat.map_build(torch.from_numpy(coords).to(dev))
-    yw, ys = _both(nat, lambda: nat.sparse_conv(x, pw, None, m.token_major, ntaps=27, n_out=n,
-                                                plan=nat.conv_plan(m.token_major, ntaps=27,
-                                                                   n_out=n)))
-    assert torch.equal(yw, ys)
+    yw, ys, yt = _all(nat, lambda: nat.sparse_conv(x, pw, None, m.token_major, ntaps=27,
+                                                   n_out=n, plan=nat.conv_plan(
+                                                       m.token_major, ntaps=27, n_out=n)))
+    assert torch.equal(yw, ys) and torch.equal(yw, yt)
 
 
 def test_wide_span_and_fallback_small(spc, orc, dev, geo):
     """Small tiles whose sources span beyond the bitmap window (the LDS hash
     dedupe) and tiles in random row order (union beyond the 511-row stage:
-    the per-tap fallback) equal the wide tiles."""
+    the per-tap fallback) equal the wide tiles; so do the tall tiles (the
+    shuffled shell's 256-row unions exceed their 511-row stage too)."""
     import torch
 
     nat = geo
@@ -166,25 +183,27 @@ def test_wide_span_and_fallback_small(spc, orc, dev, geo):
     shuffled = np.ascontiguousarray(shell[np.random.default_rng(6).permutation(len(shell))])
     for name, coords in (("two slabs", slabs), ("shuffled shell", shuffled)):
         n = coords.shape[0]
-        _case(f"{name} N={n}: wide vs small tiles")
+        _case(f"{name} N={n}: wide vs small vs tall tiles")
         _, (x, w, b) = _inputs(spc, orc, n, 32, 64, 27, seed=n % 1000)
         m = nat.map_build(torch.from_numpy(coords).to(dev))
         pw = nat.pack_weights(w)
-        yw, ys = _both(nat, lambda: nat.sparse_conv(
+        yw, ys, yt = _all(nat, lambda: nat.sparse_conv(
             x, pw, b, m.token_major, ntaps=27, n_out=n,
             plan=nat.conv_plan(m.token_major, ntaps=27, n_out=n)))
-        assert torch.equal(yw, ys)
+        assert torch.equal(yw, ys) and torch.equal(yw, yt)
 
 
 @pytest.mark.parametrize("cout", [32, 64])
 def test_epilogues_wide_equal_small(spc, orc, dev, geo, cout):
-    """Residual and norm / modulation / SiLU epilogues on the small tiles."""
+    """Residual and norm / modulation / SiLU epilogues on the small tiles,
+    the residual one on the tall tiles (the norm epilogue keeps its choice
+    by shape there)."""
     import torch
 
     nat = geo
     coords = spc.workloads.random_voxels(20000, 36, batches=3, seed=cout)
     n = coords.shape[0]
-    _case(f"epilogues N={n} 64->{cout}: wide vs small tiles")
+    _case(f"epilogues N={n} 64->{cout}: wide vs small vs tall tiles")
     _, (x, w, b) = _inputs(spc, orc, n, 64, cout, 27, seed=cout + 1)
     cd = torch.from_numpy(coords).to(dev)
     m = nat.map_build(cd)
@@ -200,8 +219,9 @@ def test_epilogues_wide_equal_small(spc, orc, dev, geo, cout):
                 nat.sparse_conv(x, pw, b, m.token_major, ntaps=27, n_out=n, plan=plan,
                                 norm_mod=(sc, sh, cd, 1e-6)))
 
-    (rw, nw), (rs, ns) = _both(nat, run)
+    (rw, nw), (rs, ns), (rt, nt_) = _all(nat, run)
     assert torch.equal(rw, rs) and torch.equal(nw, ns)
+    assert torch.equal(rw, rt) and torch.equal(nw, nt_)
 
 
 def test_weight_classes_small(spc, orc, dev, geo):
@@ -246,9 +266,9 @@ def test_plan_sections(spc, orc, dev, geo):
     pw = nat.pack_weights(w)
     full = nat.conv_plan(m.token_major, ntaps=27, n_out=n)
     outs = {}
-    for g in (nat.TILES_WIDE, nat.TILES_SMALL):
+    for g in (nat.TILES_WIDE, nat.TILES_SMALL, nat.TILES_TALL):
         nat.set_tile_geometry(g)
-        want = nat.PLAN_WIDE if g == nat.TILES_WIDE else nat.PLAN_SMALL
+        want = nat.PLAN_SMALL if g == nat.TILES_SMALL else nat.PLAN_WIDE
         assert nat.plan_section(torch.bfloat16, ntaps=27, n_out=n, cin=64, cout=64) == want
         for sec in (nat.PLAN_WIDE, nat.PLAN_SMALL, nat.PLAN_WIDE | nat.PLAN_SMALL):
             p = nat.conv_plan(m.token_major, ntaps=27, n_out=n, sections=sec)
@@ -263,6 +283,12 @@ def test_plan_sections(spc, orc, dev, geo):
     assert nat.plan_section(torch.bfloat16, ntaps=27, n_out=n, cin=64, cout=64) == nat.PLAN_SMALL
     assert nat.plan_section(torch.bfloat16, ntaps=27, n_out=n, cin=128, cout=128) == nat.PLAN_WIDE
     assert nat.plan_section(torch.bfloat16, ntaps=8, n_out=n, cin=128, cout=128) == nat.PLAN_SMALL
+    # one-chunk rows with C_out <= 64 -> tall tiles, which read the wide section
+    tg = nat.tile_geometry(torch.bfloat16, ntaps=27, n_out=n, cin=32, cout=32)
+    assert tg == nat.TILES_TALL
+    assert nat.plan_section(torch.bfloat16, ntaps=27, n_out=n, cin=32, cout=64) == nat.PLAN_WIDE
+    assert nat.tile_geometry(torch.bfloat16, ntaps=27, n_out=n, cin=32, cout=128) == nat.TILES_SMALL
+    assert nat.tile_geometry(torch.bfloat16, ntaps=27, n_out=n, cin=64, cout=64) == nat.TILES_SMALL
 
 
 @pytest.mark.parametrize("r", [1, 6, 31, 32, 33, 64, 65, 129, 255])
@@ -270,8 +296,9 @@ def test_partial_tile_live_blocks(spc, orc, dev, geo, r):
     """A partial last row tile of 2 * 256 + r rows: its waves whose rows end
     inside their first 32-row block run that block's MFMAs only.  bf16
     128 -> 128 on the wide tiles (64-row waves), the small tiles (64-row
-    waves over 128-row tiles) and Q8_0 128 -> 128 (128-row waves), every
-    row against the oracle."""
+    waves over 128-row tiles), the tall tiles (64-row waves over 256-row
+    tiles) and Q8_0 128 -> 128 (128-row waves), every row against the
+    oracle."""
     import oracle
     import torch
 
@@ -279,19 +306,20 @@ def test_partial_tile_live_blocks(spc, orc, dev, geo, r):
     n = 512 + r
     coords = spc.workloads.random_voxels(n + 400, 14, batches=1, seed=r)[:n]
     coords = np.ascontiguousarray(coords)
-    _case(f"partial tile N={n} (r={r}): bf16 wide / small, Q8_0")
+    _case(f"partial tile N={n} (r={r}): bf16 wide / small / tall, Q8_0")
     (xh, wh, bh), (x, w, b) = _inputs(spc, orc, n, 128, 128, 27, seed=r + 5)
     m = nat.map_build(torch.from_numpy(coords).to(dev))
     tm = m.token_major.cpu().numpy()
     pw = nat.pack_weights(w)
-    yw, ys = _both(nat, lambda: nat.sparse_conv(x, pw, b, m.token_major, ntaps=27, n_out=n,
-                                                plan=nat.conv_plan(m.token_major, ntaps=27,
-                                                                   n_out=n)))
+    yw, ys, yt = _all(nat, lambda: nat.sparse_conv(x, pw, b, m.token_major, ntaps=27, n_out=n,
+                                                   plan=nat.conv_plan(m.token_major, ntaps=27,
+                                                                      n_out=n)))
     ref = orc.sparse_conv(xh, wh, bh, tm, ntaps=27, n_out=n, idx_layout=1, out_dtype=oracle.F32,
                           x_dtype=oracle.BF16, w_dtype=oracle.BF16, b_dtype=oracle.BF16,
                           nthreads=oracle_threads(), blocked=True)
     check_16bit(f"partial tile wide N={n}", from_dev(yw), ref)
     check_16bit(f"partial tile small N={n}", from_dev(ys), ref)
+    check_16bit(f"partial tile tall N={n}", from_dev(yt), ref)
     # Q8_0 weights (in-register dequantisation: 4 waves of 128 x 64 rows)
     blocks = orc.q8_0_quantize(spc.workloads.normal((128, 27, 128), 0.05, seed=r + 9))
     qs, dsc = nat.q8_0_repack(torch.from_numpy(blocks).to(dev))
