@@ -216,6 +216,11 @@ constexpr int kSegs = 4;        // 16-byte segments per staged 64-byte row chunk
 //             tiles' plans (same row tiles, slot keys and plan layout); a tile
 //             whose union exceeds its stage takes the per-tap fallback, two
 //             taps per round, about four times the staged tile's time.
+//   GeoQuad   GeoSmall<8>'s 64-row tiles and plan over four 511-row buffers
+//             (128 KB, one workgroup per CU): a tile stages four channel
+//             chunks at once, so a stride-2 conv over 16-bit rows of up to
+//             128 channels waits for one staging instead of one per chunk --
+//             for the stride-2 convs whose tiles fit the device in one round.
 // Staged row layouts (one 64-byte chunk of a union row = four 16-byte
 // segments; a wave's A-fragment read takes one segment of 32 slots, which
 // the LDS serves 16 lanes at a time):
@@ -260,8 +265,11 @@ using GeoWide = Geo<256, 895, 2, true>;
 template <int NTAPS>
 using GeoSmall = Geo<NTAPS == 8 ? 64 : 128, 511, 1, true>;
 using GeoTall = Geo<256, 559, 1, true, 895>;
+using GeoQuad = Geo<64, 511, 4, true>;
 static_assert(GeoWide::STAGE == 3584 && GeoSmall<27>::STAGE == 2048 && GeoTall::STAGE == 2240,
               "stage geometry");
+static_assert(GeoQuad::plan_tile_bytes(8) == GeoSmall<8>::plan_tile_bytes(8) && !GeoQuad::WIDE_PLAN,
+              "the four-buffer tiles read the small plan");
 static_assert(GeoTall::WIDE_PLAN && GeoTall::plan_tile_bytes(27) == GeoWide::plan_tile_bytes(27) &&
                   GeoTall::PLAN_SIDX == GeoWide::PLAN_SIDX && !GeoSmall<27>::WIDE_PLAN,
               "the tall tiles read the wide plan");
@@ -586,8 +594,8 @@ __global__ __launch_bounds__(512) void conv_plan_kernel(ConvArgs a, char* plan) 
     }
 }
 
-// Workgroups per CU a geometry is built for: GeoWide fills the CU's LDS
-// with one; GeoSmall's ~42 KB and GeoTall's ~53 KB admit three (register
+// Workgroups per CU a geometry is built for: GeoWide and GeoQuad fill the
+// CU's LDS with one; GeoSmall's ~42 KB and GeoTall's ~53 KB admit three (register
 // budget 168 per wave), two for 128-column tiles, whose 64 x 64 wave tiles
 // need ~226 registers.
 template <typename GEO, int TN>
@@ -616,7 +624,7 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
     static_assert(NTAPS <= 32, "tap mask is 32-bit");
     static_assert(kSetupScratchWords * 4 <= ABYTES, "setup scratch aliases the A stage");
     static_assert(PD == 4, "the step groups pack four taps per word");
-    static_assert(NBUF == 1 || NBUF == 2, "one or two A buffers");
+    static_assert(NBUF == 1 || NBUF == 2 || NBUF == 4, "one, two or four A buffers");
 
     __shared__ u32x4 Au[NBUF * STAGE];  // A buffers: (U + 1) rows x 64 bytes each
     __shared__ __attribute__((aligned(16))) uint16_t sidx[NQ + TM];  // slot keys; row NTAPS = zeros
@@ -626,15 +634,16 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
     __shared__ int32_t wsum[NW];
     __shared__ __attribute__((aligned(16))) int32_t misc[8];
     __shared__ __attribute__((aligned(16))) float sbias[TN];
-    // Per-wave epilogue (16-bit outputs of the wide 8-wave tiles): once a wave
-    // is done with the last chunk it writes its own block through a private
-    // LDS region and stores it, while the other waves still compute.  The
-    // regions are the stage buffer the last chunk does not read, and PWX
-    // more here for the waves it cannot hold.
+    // Per-wave epilogue (16-bit outputs of 8-wave tiles): once a wave is done
+    // with the last chunk it writes its own block through a private LDS
+    // region and stores it, while the other waves still compute.  The
+    // regions are the stage buffer the last chunk does not read (two
+    // buffers), and PWX more here for the waves it cannot hold (all of them
+    // with four buffers, whose waves run a group's chunks without barriers).
     constexpr int PW_PITCH = WTN * ES + 16;      // bytes per row of a wave's block
     constexpr int PW_BYTES = WTM * PW_PITCH;
-    constexpr bool PWE = ES == 2 && NBUF == 2 && NW == 8 && WTM * WTN <= 4096;
-    constexpr int PW_IN_STAGE = PWE ? STAGE * 16 / PW_BYTES : 0;  // regions in the free buffer
+    constexpr bool PWE = ES == 2 && (NBUF == 2 || NBUF == 4) && NW == 8 && WTM * WTN <= 4096;
+    constexpr int PW_IN_STAGE = PWE && NBUF == 2 ? STAGE * 16 / PW_BYTES : 0;  // regions in the free buffer
     constexpr int PWX = PWE && PW_IN_STAGE < NW ? NW - PW_IN_STAGE : 0;
     __shared__ __attribute__((aligned(16))) char pw_extra[PWX > 0 ? PWX * PW_BYTES : 16];
 
@@ -974,6 +983,12 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
             else if (h == 2) stage_part(kc, buf, std::integral_constant<int, 2>{});
             else stage_part(kc, buf, std::integral_constant<int, 3>{});
         };
+        // four buffers: the chunks g0 .. g0 + 3 at once, chunk c in buffer c % 4
+        // (one staging latency per four chunks instead of one per chunk)
+        auto stage_group = [&](int g0) __attribute__((always_inline)) {
+            for (int c = g0; c < kch && c < g0 + NBUF; ++c)
+                for (int h = 0; h < NPART; ++h) stage_part_rt(c, c % NBUF, h);
+        };
         // vector-memory loads per step (weight words, plus Q8_0 scales)
         constexpr int LPS = PACKED ? FN * P::NG + (Q8 ? FN : 0) : 0;
 
@@ -1002,12 +1017,20 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
         for (int k = lane; k < WTM; k += 64) has_row |= srow[wm * WTM + k] >= 0;
         if (__builtin_amdgcn_ballot_w64(has_row != 0) == 0) {
             // the same barriers as the working waves, in the same order
-            for (int h = 0; h < NPART; ++h) stage_part_rt(0, 0, h);
-            dma_barrier<0>();
-            for (int kc = 0; kc + 1 < kch; ++kc) {
-                if constexpr (NBUF == 1) lds_barrier();  // the buffer is free
-                for (int h = 0; h < NPART; ++h) stage_part_rt(kc + 1, NBUF == 1 ? 0 : (kc & 1) ^ 1, h);
+            if constexpr (NBUF == 4) {
+                for (int g0 = 0; g0 < kch; g0 += NBUF) {
+                    if (g0 > 0) lds_barrier();
+                    stage_group(g0);
+                    dma_barrier<0>();
+                }
+            } else {
+                for (int h = 0; h < NPART; ++h) stage_part_rt(0, 0, h);
                 dma_barrier<0>();
+                for (int kc = 0; kc + 1 < kch; ++kc) {
+                    if constexpr (NBUF == 1) lds_barrier();  // the buffer is free
+                    for (int h = 0; h < NPART; ++h) stage_part_rt(kc + 1, NBUF == 1 ? 0 : (kc & 1) ^ 1, h);
+                    dma_barrier<0>();
+                }
             }
         } else {
           auto run_tile = [&](auto fa_const) __attribute__((always_inline)) {
@@ -1028,17 +1051,26 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
                 for (int p = 0; p < PD; ++p) load_b(b_tap(w0, p), 0, ring[p]);
                 read_slots(s_row(w0, 0), sreg[0], fa_const);
                 read_slots(s_row(w0, 1), sreg[1], fa_const);
-                for (int h = 0; h < NPART; ++h) stage_part_rt(0, 0, h);
+                if constexpr (NBUF == 4) stage_group(0);
+                else for (int h = 0; h < NPART; ++h) stage_part_rt(0, 0, h);
                 dma_barrier<0>();
                 read_frags(0, sreg[0], afr[0], fa_const);
             }
 
             for (int kc = 0; kc < kch; ++kc) {
-                const int buf = NBUF == 1 ? 0 : kc & 1;
+                const int buf = NBUF == 1 ? 0 : NBUF == 2 ? kc & 1 : kc % NBUF;
                 // two buffers: the next chunk is staged while this one runs
                 const bool more = NBUF == 2 && kc + 1 < kch;
                 if (kc > 0) {
-                    if constexpr (NBUF == 1) {
+                    if constexpr (NBUF == 4) {
+                        // a group's first chunk: once every wave is done with
+                        // the last group, stage this one and wait for it
+                        if (kc % NBUF == 0) {
+                            lds_barrier();
+                            stage_group(kc);
+                            dma_barrier<0>();
+                        }
+                    } else if constexpr (NBUF == 1) {
                         // one buffer: once every wave is done reading the last
                         // chunk (the barrier's fence waits for this wave's LDS
                         // reads), stage this one and wait for it; the weight
@@ -1137,7 +1169,10 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
         // loaded while the previous step's MFMAs run.
         constexpr int UPT = (TM * kSegs + NT - 1) / NT;
         constexpr int GA = NBUF * STAGE / (TM * GEO::PITCH);
-        constexpr int G = GA < 14 / UPT ? GA : 14 / UPT;  // taps per round (<= 56 VGPRs of loads)
+        // taps per round: <= 56 VGPRs of loads, and at most 8 (a longer round
+        // is not unrolled, and its register arrays would go to memory)
+        constexpr int G0 = GA < 14 / UPT ? GA : 14 / UPT;
+        constexpr int G = G0 < 8 ? G0 : 8;
         static_assert(G >= 1 && G * TM * GEO::PITCH <= NBUF * STAGE, "fallback rounds fit the A area");
         for (int kc = 0; kc < kch; ++kc) {
             const int64_t koff = (int64_t)kc * KC * ES;
@@ -1288,13 +1323,13 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
     }
 
     // ---- per-wave epilogue (staged fast path, 16-bit output, no norm): the
-    // wave's rounded block goes to its private LDS region (the last chunk
-    // reads only its own buffer, so the other one is free) and back as
+    // wave's rounded block goes to its private LDS region (with two buffers
+    // the last chunk reads only its own, so the other one is free) and back as
     // whole 16-byte pieces of its rows, which leave with coalesced
     // non-temporal stores -- no barrier, so early waves store while the
     // late ones finish their MFMAs.  Same values as the tile epilogue below.
     if constexpr (PWE) if (dma) {
-        const int freebuf = ((kch - 1) & 1) ^ 1;
+        const int freebuf = ((kch - 1) & 1) ^ 1;  // (two buffers)
         char* reg = wave < PW_IN_STAGE
                         ? reinterpret_cast<char*>(Au + freebuf * STAGE) + wave * PW_BYTES
                         : pw_extra + (wave - PW_IN_STAGE) * PW_BYTES;
@@ -1480,6 +1515,23 @@ hipError_t launch_conv(hipStream_t s, ConvArgs a) {
     return hipGetLastError();
 }
 
+// The stride-2 conv's 64-row tiles over four buffers (GeoQuad), picked by
+// shape: up to four 64-byte channel chunks (C_in <= 128 in 16-bit, 64 in
+// f32) and every tile on its own CU in one round (config 2's 11,774 coarse
+// rows at C_out 128: 184 tiles).  Same wave layouts as the small tiles.
+template <typename T, bool Q8, bool PACKED, int NTAPS>
+bool use_quad_tiles(const ConvArgs& a, int tn) {
+    if constexpr (NTAPS != 8) {
+        return false;
+    } else {
+        const int64_t kch = (int64_t)a.cin * (int64_t)sizeof(T) / 64;
+        // by shape, also under a forced geometry that does not apply here
+        return a.geometry != SPC_TILES_WIDE && a.geometry != SPC_TILES_SMALL &&
+               a.epi_mode != SPC_EPI_NORM_MOD_SILU && kch <= 4 &&
+               ceil_div(a.n_out, GeoQuad::TM) * (a.cout / tn) <= a.num_cu;
+    }
+}
+
 // Small tiles (GeoSmall: 128 rows, 64 for stride-2; three 4-wave
 // workgroups per CU, two at TN = 128): TN = largest of {128, 64, 32} dividing cout, halved
 // while the narrower tiles still fit on the device in one round; waves 2 x 2
@@ -1493,6 +1545,13 @@ hipError_t dispatch_small(hipStream_t s, const ConvArgs& a) {
     int tn = a.cout % 128 == 0 ? 128 : a.cout % 64 == 0 ? 64 : 32;
     while (tn > 32 && tiles_m * (a.cout / (tn / 2)) <= a.num_cu) tn /= 2;
     if (a.epi_mode == SPC_EPI_NORM_MOD_SILU) tn = a.cout;  // 32 or 64 here (one tile per row)
+    if constexpr (NTAPS == 8) {
+        if (use_quad_tiles<T, Q8, PACKED, NTAPS>(a, tn)) {
+            if (tn == 128) return launch_conv<T, Q8, PACKED, NTAPS, 128, 2, 4, GeoQuad>(s, a);
+            if (tn == 64) return launch_conv<T, Q8, PACKED, NTAPS, 64, 2, 2, GeoQuad>(s, a);
+            return launch_conv<T, Q8, PACKED, NTAPS, 32, 2, 1, GeoQuad>(s, a);
+        }
+    }
     if (tn == 128) {
         // Q8_0: 4 waves of 128 x 32, so each in-register dequantised B
         // fragment feeds four MFMAs and no two waves dequantise the same one
@@ -1503,6 +1562,7 @@ hipError_t dispatch_small(hipStream_t s, const ConvArgs& a) {
     if constexpr (G::TM == 128) return launch_conv<T, Q8, PACKED, NTAPS, 32, 4, 1, G>(s, a);
     else return launch_conv<T, Q8, PACKED, NTAPS, 32, 2, 1, G>(s, a);
 }
+
 
 // Which geometry a conv runs.  a.geometry forces one (1 wide, 2 small);
 // otherwise the small tiles take the shapes where their single stage buffer

@@ -107,7 +107,9 @@ def test_subm_wide_equals_small(spc, orc, dev, geo, dt, cin, cout, nvox, grid):
 def test_stride2_wide_equals_small(spc, orc, dev, geo, cin, cout):
     """The 2x2x2 stride-2 conv on the config-2 coords: the wide tiles' 256
     coarse rows overflow their stage (per-tap fallback), the small tiles'
-    64 coarse rows (about 340 fine rows) take the staged path."""
+    64 coarse rows (about 340 fine rows) take the staged path, and so do the
+    four-buffer tiles the shape picks where its tiles fit one round (every
+    case here but 128 -> 1024)."""
     import oracle
     import torch
 
@@ -115,7 +117,7 @@ def test_stride2_wide_equals_small(spc, orc, dev, geo, cin, cout):
     coords = spc.workloads.ellipsoid_batch()
     nf = coords.shape[0]
     d = nat.downsample_map(torch.from_numpy(coords).to(dev), 4, 64)
-    _case(f"stride-2 nf={nf} nc={d.nc} {cin}->{cout}: wide vs small tiles")
+    _case(f"stride-2 nf={nf} nc={d.nc} {cin}->{cout}: wide vs small vs by-shape tiles")
     (xh, wh, bh), (x, w, b) = _inputs(spc, orc, nf, cin, cout, 8, seed=cin + 3 * cout)
     pw = nat.pack_weights(w)
 
@@ -123,8 +125,8 @@ def test_stride2_wide_equals_small(spc, orc, dev, geo, cin, cout):
         plan = nat.conv_plan(d.stride2_taps, ntaps=8, n_out=d.nc, n_in=nf)
         return nat.sparse_conv(x, pw, b, d.stride2_taps, ntaps=8, n_out=d.nc, plan=plan)
 
-    yw, ys = _both(nat, run)
-    assert torch.equal(yw, ys)
+    yw, ys, yq = _all(nat, run)
+    assert torch.equal(yw, ys) and torch.equal(yw, yq)
     ref = orc.sparse_conv(xh, wh, bh, d.stride2_taps.cpu().numpy(), ntaps=8, n_out=d.nc,
                           idx_layout=1, out_dtype=oracle.F32, x_dtype=oracle.BF16,
                           w_dtype=oracle.BF16, b_dtype=oracle.BF16, nthreads=oracle_threads(),
