@@ -237,6 +237,20 @@ def test_f16_spconv_bridge(spc, orc, dev):
                                   idx_layout=nat.IDX_OFFSET_MAJOR)
         torch.cuda.synchronize()
         assert msg == "" and torch.equal(yi, yi_krsc)
+    # the tall tiles (C_in 32, C_out <= 64) keep their plan in the wide
+    # layout: planned, refreshed over other indices and over one changed
+    # entry, and back -- each call equal to the unplanned launch
+    x32 = torch.from_numpy(wl.normal((n, 32), 1.0, seed=46).astype(np.float16)).to(dev)
+    w32 = torch.from_numpy(wl.normal((64, 27, 32), 0.02, seed=47).astype(np.float16)).to(dev)
+    b32 = torch.from_numpy(wl.normal((64,), 0.01, seed=48).astype(np.float16)).to(dev)
+    assert nat.tile_geometry(torch.float16, ntaps=27, n_out=n, cin=32, cout=64) == nat.TILES_TALL
+    for k, om_i in enumerate((m.offset_major, m.offset_major, mb.offset_major, om, m.offset_major)):
+        _case(f"f16 bridge tall tiles 32->64 call {k}")
+        yt, msg = nat.spconv_f16_forward(x32, w32, b32, om_i, m.mask_sorted, m.argsort)
+        yt_krsc = nat.sparse_conv(x32, w32, b32, om_i, ntaps=27, n_out=n,
+                                  idx_layout=nat.IDX_OFFSET_MAJOR)
+        torch.cuda.synchronize()
+        assert msg == "" and torch.equal(yt, yt_krsc)
 
 
 def test_q8_0_config5_sphere(spc, orc, dev):
