@@ -782,9 +782,16 @@ class SparseDownsample(nn.Module):
             raise NotImplementedError("SparseDownsample supports factor 2")
         d = _downsample_map(input)
         feats = nat.scatter_mean(input.feats, d.fine_to_coarse, d.counts, d.nc)
+        # The coarse level's maps are kept with the fine coordinates (a
+        # block's downsample yields the same coarse coordinates every call,
+        # so its convs' maps and plans are built once), and the coarse maps
+        # keep the fine level's for the paired upsample.  Maps depend on the
+        # coordinates only, so reusing them changes no result.
         data = SparseTensorData(feats, d.coarse_coords,
                                 [(s + 1) // 2 for s in input.data.spatial_shape],
-                                input.data.batch_size)
+                                input.data.batch_size, input.data.cached("down2_maps", lambda c: {}))
+        fine_maps = input.data.indice_dict
+        data.cached("up2_maps", lambda c: fine_maps)
         out = SparseTensor(data, shape=input.shape)
         out._scale = tuple(s // f for s, f in zip(input._scale, factor))
         out._spatial_cache = input._spatial_cache
@@ -811,6 +818,12 @@ class SparseUpsample(nn.Module):
             raise ValueError("Upsample cache not found. SparseUpsample must be paired with "
                              "SparseDownsample.")
         out = SparseTensor(nat.gather_rows(input.feats, idx), coords, input.shape, layout)
+        # the fine level's maps, kept by the paired downsample (their entries
+        # check that they were built from these coordinates)
+        ent = input.data.indice_dict.get("up2_maps")
+        c = input.data.indices
+        if ent is not None and ent[0] is c and ent[1] == c._version:
+            out.data.indice_dict = ent[2]
         out._scale = tuple(s * f for s, f in zip(input._scale, factor))
         out._spatial_cache = input._spatial_cache
         return out

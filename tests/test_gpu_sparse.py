@@ -307,6 +307,47 @@ def test_downsample_upsample(spc, orc, dev, dt):
     assert up._scale == tuple(s * 2 for s in down._scale)
 
 
+def test_down_up_reuse_maps(spc, orc, dev):
+    """A block's downsample yields the same coarse coordinates on every
+    call: the coarse convs' maps and plans are built once (kept with the
+    fine coordinates), and the paired upsample hands the fine level's maps
+    back -- the same results as tensors without any cached map."""
+    import torch
+
+    coords = spc.workloads.ellipsoid_batch(2, seed=31)
+    n = coords.shape[0]
+    _case(f"down / conv / up / conv map reuse N={n} C=64")
+    sp = _sp(spc)
+    g = torch.Generator().manual_seed(3)
+    xt = sp.SparseTensor(torch.randn((n, 64), generator=g).to(dev, torch.bfloat16),
+                         torch.from_numpy(coords).to(dev))
+    conv_c = sp.SparseConv3d(64, 64, 3).to(dev, torch.bfloat16)
+    conv_f = sp.SparseConv3d(64, 64, 3).to(dev, torch.bfloat16)
+    outs = []
+    with torch.no_grad():
+        for _ in range(2):
+            down = sp.SparseDownsample(2)(xt)
+            hc = conv_c(down)
+            up = sp.SparseUpsample(2)(hc)
+            hf = conv_f(up)
+            outs.append((hc.feats.clone(), hf.feats.clone(), down.data.indice_dict,
+                         up.data.indice_dict))
+    torch.cuda.synchronize()
+    # one coarse map cache across the calls, the fine level's handed back
+    assert outs[0][2] is outs[1][2] and "subm3" in outs[0][2]
+    assert outs[0][3] is xt.data.indice_dict and outs[1][3] is xt.data.indice_dict
+    assert "subm3" in xt.data.indice_dict
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    # tensors with fresh caches (new coordinate tensors): the same values
+    xt2 = sp.SparseTensor(xt.feats.clone(), xt.coords.clone())
+    with torch.no_grad():
+        hc2 = conv_c(sp.SparseDownsample(2)(xt2))
+        hf2 = conv_f(sp.SparseUpsample(2)(hc2))
+    torch.cuda.synchronize()
+    assert hf2.data.indice_dict is xt2.data.indice_dict
+    assert torch.equal(hc2.feats, outs[0][0]) and torch.equal(hf2.feats, outs[0][1])
+
+
 def test_subdivide_module(spc, orc, dev):
     import torch
 
