@@ -790,9 +790,12 @@ class SparseDownsample(nn.Module):
         data = SparseTensorData(feats, d.coarse_coords,
                                 [(s + 1) // 2 for s in input.data.spatial_shape],
                                 input.data.batch_size, input.data.cached("down2_maps", lambda c: {}))
-        fine_maps = input.data.indice_dict
-        data.cached("up2_maps", lambda c: fine_maps)
-        out = SparseTensor(data, shape=input.shape)
+        fine = input.data
+        data.cached("up2_maps", lambda c: (fine.indice_dict, fine.spatial_shape, fine.batch_size))
+        # the coarse rows' batch slices, cached like the maps (computing them
+        # reads the coordinates back to the host)
+        layout = data.cached("layout", lambda c: SparseTensor._batch_slices(c, input.shape[0]))
+        out = SparseTensor(data, shape=input.shape, layout=layout)
         out._scale = tuple(s // f for s, f in zip(input._scale, factor))
         out._spatial_cache = input._spatial_cache
         out.register_spatial_cache(f"upsample_{factor}_coords", input.coords)
@@ -817,13 +820,18 @@ class SparseUpsample(nn.Module):
         if any(v is None for v in (coords, layout, idx)):
             raise ValueError("Upsample cache not found. SparseUpsample must be paired with "
                              "SparseDownsample.")
-        out = SparseTensor(nat.gather_rows(input.feats, idx), coords, input.shape, layout)
-        # the fine level's maps, kept by the paired downsample (their entries
-        # check that they were built from these coordinates)
+        feats = nat.gather_rows(input.feats, idx)
+        # the fine level's maps and extent, kept by the paired downsample
+        # (the maps' entries check that they were built from these
+        # coordinates); without them the extent is read from the coordinates
         ent = input.data.indice_dict.get("up2_maps")
         c = input.data.indices
         if ent is not None and ent[0] is c and ent[1] == c._version:
-            out.data.indice_dict = ent[2]
+            maps, extent, n_b = ent[2]
+            out = SparseTensor(SparseTensorData(feats, coords, extent, n_b, maps),
+                               shape=input.shape, layout=layout)
+        else:
+            out = SparseTensor(feats, coords, input.shape, layout)
         out._scale = tuple(s * f for s, f in zip(input._scale, factor))
         out._spatial_cache = input._spatial_cache
         return out
