@@ -400,6 +400,18 @@ int spc_scatter_mean(spc_stream_t stream, int dtype, const void* features, const
                      const float* counts, void* out, int64_t channels, int64_t nf, int64_t nc,
                      void* workspace, size_t workspace_bytes);
 
+/* The scatter-mean above from spc_downsample_map's children lists instead
+ * of fine_to_coarse: out[r] = (children of r, ascending fine rows, summed
+ * with the same per-add rounding) / counts[r] -- the same values as
+ * spc_scatter_mean on the same map, without its sort or workspace.
+ * children is int32 [8 * nc], each list ended by a value outside [0, nf)
+ * (the map pads with nf).  No reference counterpart: SparseDownsample's
+ * fast path once the map is built (the reference module re-runs its
+ * scatter_reduce every call, SP/spatial.py:59-62). */
+int spc_children_mean(spc_stream_t stream, int dtype, const void* features,
+                      const int32_t* children, const float* counts, void* out, int64_t channels,
+                      int64_t nf, int64_t nc);
+
 /* Row gather dst[i] = src[idx[i]] (zero row when idx[i] is outside
  * [0, n_src)).  SparseUpsample's feats[idx] (SP/spatial.py:92; SRC/
  * slat_flow_graph.cpp:244-247) and SparseSubdivide's parent broadcast

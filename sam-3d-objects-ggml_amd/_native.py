@@ -94,6 +94,7 @@ def lib() -> ctypes.CDLL:
     L.spc_scatter_mean_workspace_bytes.restype = _SZ
     L.spc_scatter_mean_workspace_bytes.argtypes = [_I64, _I64]
     L.spc_scatter_mean.argtypes = [_P, _INT, _P, _P, _P, _P, _I64, _I64, _I64, _P, _SZ]
+    L.spc_children_mean.argtypes = [_P, _INT, _P, _P, _P, _P, _I64, _I64, _I64]
     L.spc_gather_rows.argtypes = [_P, _INT, _P, _P, _P, _I64, _I64, _I64]
     L.spc_layernorm_silu.argtypes = [_P, _INT, _P, _I64, _I64, _P, _P, ctypes.c_float, _INT, _P]
     L.spc_conv_set_tile_geometry.argtypes = [_INT]
@@ -684,6 +685,25 @@ def scatter_mean(features: torch.Tensor, rows: torch.Tensor, counts: torch.Tenso
     st = L.spc_scatter_mean(_stream(dev), dtype_code(features.dtype), _ptr(features), _ptr(rows),
                             _ptr(counts), _ptr(out), c, nf, nc, _ptr(ws), ws.numel())
     _check("spc_scatter_mean", st)
+    return out
+
+
+def children_mean(features: torch.Tensor, children: torch.Tensor, counts: torch.Tensor,
+                  nc: int) -> torch.Tensor:
+    """spc_children_mean: scatter_mean's values from a downsample map's
+    children lists (no sort)."""
+    _need_gpu(features, children, counts)
+    features = features.contiguous()
+    children = children.to(torch.int32).contiguous()
+    counts = counts.to(torch.float32).contiguous()
+    nf, c = features.shape
+    if children.numel() < 8 * nc or counts.numel() < nc:
+        raise ValueError("children must hold 8 * nc entries and counts nc")
+    out = torch.empty((nc, c), dtype=features.dtype, device=features.device)
+    st = lib().spc_children_mean(_stream(features.device), dtype_code(features.dtype),
+                                 _ptr(features), _ptr(children), _ptr(counts), _ptr(out), c, nf,
+                                 nc)
+    _check("spc_children_mean", st)
     return out
 
 

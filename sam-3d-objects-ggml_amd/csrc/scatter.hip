@@ -7,6 +7,9 @@
 //                      (coarse row, channel) adds in that order, rounding the
 //                      partial sum to the storage dtype after every add, and
 //                      divides by the count in F32.
+//   spc_children_mean: the same values from the downsample map's children
+//                      lists (ascending fine rows, at most 8 per coarse row):
+//                      no sort, one pass.
 //   spc_gather_rows  : dst[i] = src[idx[i]] with 16-byte vector copies.
 #include "common.h"
 
@@ -71,6 +74,29 @@ __global__ __launch_bounds__(256) void scatter_mean_kernel(
     const int32_t b = seg[r];
     const int32_t end = seg[r + 1];
     for (int32_t p = b; p < end; ++p) acc = S::st(S::ld(acc) + S::ld(feats[(int64_t)sv[p] * channels + c]));
+    out[e] = S::st(S::ld(acc) / counts[r]);
+}
+
+// The scatter-mean of one (coarse row, channel) from its children list
+// (ascending fine rows, padded with values outside [0, nf)): the same adds
+// in the same order as scatter_mean_kernel over the sorted rows.
+template <int DT>
+__global__ __launch_bounds__(256) void children_mean_kernel(
+    const typename Store<DT>::t* __restrict__ feats, const int32_t* __restrict__ children,
+    const float* __restrict__ counts, int64_t channels, int64_t nf, int64_t nc,
+    typename Store<DT>::t* __restrict__ out) {
+    using S = Store<DT>;
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= nc * channels) return;
+    const int64_t r = e / channels;
+    const int64_t c = e - r * channels;
+    typename S::t acc = S::st(0.0f);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int32_t f = children[r * 8 + k];
+        if (f < 0 || f >= nf) break;  // compacted lists: the padding ends them
+        acc = S::st(S::ld(acc) + S::ld(feats[(int64_t)f * channels + c]));
+    }
     out[e] = S::st(S::ld(acc) / counts[r]);
 }
 
@@ -168,6 +194,44 @@ int spc_scatter_mean(spc_stream_t stream, int dtype, const void* features, const
             break;
         default:
             set_last_error("spc_scatter_mean: unknown dtype %d", dtype);
+            return SPC_BAD_ARG;
+    }
+    SPC_HIP(hipGetLastError());
+    return SPC_OK;
+}
+
+int spc_children_mean(spc_stream_t stream, int dtype, const void* features,
+                      const int32_t* children, const float* counts, void* out, int64_t channels,
+                      int64_t nf, int64_t nc) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (channels <= 0 || nf < 0 || nc < 0 || nf > INT32_MAX || nc >= INT32_MAX) {
+        set_last_error("spc_children_mean: bad shape");
+        return SPC_BAD_SHAPE;
+    }
+    if (nc == 0) return SPC_OK;
+    if (!out || !counts || !children || (nf > 0 && !features)) {
+        set_last_error("spc_children_mean: null argument");
+        return SPC_BAD_ARG;
+    }
+    const unsigned g = grid_for(nc * channels, 256);
+    switch (dtype) {
+        case SPC_F16:
+            children_mean_kernel<SPC_F16><<<g, 256, 0, s>>>(
+                static_cast<const uint16_t*>(features), children, counts, channels, nf, nc,
+                static_cast<uint16_t*>(out));
+            break;
+        case SPC_BF16:
+            children_mean_kernel<SPC_BF16><<<g, 256, 0, s>>>(
+                static_cast<const uint16_t*>(features), children, counts, channels, nf, nc,
+                static_cast<uint16_t*>(out));
+            break;
+        case SPC_F32:
+            children_mean_kernel<SPC_F32><<<g, 256, 0, s>>>(static_cast<const float*>(features),
+                                                            children, counts, channels, nf, nc,
+                                                            static_cast<float*>(out));
+            break;
+        default:
+            set_last_error("spc_children_mean: unknown dtype %d", dtype);
             return SPC_BAD_ARG;
     }
     SPC_HIP(hipGetLastError());

@@ -781,7 +781,8 @@ class SparseDownsample(nn.Module):
         if factor != (2, 2, 2):
             raise NotImplementedError("SparseDownsample supports factor 2")
         d = _downsample_map(input)
-        feats = nat.scatter_mean(input.feats, d.fine_to_coarse, d.counts, d.nc)
+        # the map's children lists give scatter_mean's values without its sort
+        feats = nat.children_mean(input.feats, d.children, d.counts, d.nc)
         # The coarse level's maps are kept with the fine coordinates (a
         # block's downsample yields the same coarse coordinates every call,
         # so its convs' maps and plans are built once), and the coarse maps

@@ -54,6 +54,40 @@ def test_scatter_mean_downsample_map(spc, orc, dev, dt):
     assert np.array_equal(got, ref)
 
 
+@pytest.mark.parametrize("dt,channels", [("bf16", 128), ("f16", 13), ("f32", 64)])
+def test_children_mean_equals_scatter_mean(spc, orc, dev, dt, channels):
+    """spc_children_mean over the downsample map's children lists gives
+    spc_scatter_mean's values (and the oracle's) bit for bit."""
+    import oracle
+    import torch
+
+    coords = spc.workloads.ellipsoid_batch(3, seed=17)
+    n = coords.shape[0]
+    _case(f"children_mean {dt} C={channels} N={n}")
+    nat = spc._native
+    d = nat.downsample_map(torch.from_numpy(coords).to(dev), 3, 64)
+    x = spc.workloads.normal((n, channels), 1.0, seed=channels)
+    if dt == "bf16":
+        x_np, code = orc.f32_to_bf16(x), oracle.BF16
+        feats = torch.from_numpy(x_np.view(np.int16)).view(torch.bfloat16)
+    elif dt == "f16":
+        x_np, code = x.astype(np.float16), oracle.F16
+        feats = torch.from_numpy(x_np)
+    else:
+        x_np, code, feats = x, oracle.F32, torch.from_numpy(x)
+    feats = feats.to(dev)
+    a = nat.children_mean(feats, d.children, d.counts, d.nc)
+    b = nat.scatter_mean(feats, d.fine_to_coarse, d.counts, d.nc)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16) if dt != "f32" else a,
+                       b.view(torch.int16) if dt != "f32" else b)
+    ref = orc.scatter_mean(x_np, d.fine_to_coarse.cpu().numpy(), d.counts.cpu().numpy(), d.nc,
+                           dtype=code)
+    got = a.cpu()
+    got = got.numpy() if dt == "f32" else got.view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, ref.view(np.uint16) if dt == "f16" else ref)
+
+
 @pytest.mark.parametrize("dt,channels", [("f32", 64), ("bf16", 128), ("f16", 96), ("bf16", 3),
                                          ("f32", 1)])
 def test_gather_rows(spc, dev, dt, channels):
