@@ -612,7 +612,8 @@ def bench_bridge(nat, wl, c_dev, dev, args) -> dict:
 
 def bench_feature_ops(spc, nat, wl, orc, coords, c_dev, dev, args, workload) -> dict:
     """HBM rates of the non-GEMM kernels of the SLAT IO blocks on the config-2
-    rows (bf16): the scatter-mean downsample (fine -> coarse), the upsample
+    rows (bf16): the scatter-mean downsample (fine -> coarse; from the rows'
+    coarse index with a sort, and from the map's children lists), the upsample
     gather (coarse -> fine), LayerNorm + SiLU, LayerNorm + modulation + SiLU
     and the GroupNorm pair.  Algorithmic bytes per launch: every input row
     read once and every output row written once (plus 4-byte row indices
@@ -640,7 +641,7 @@ def bench_feature_ops(spc, nat, wl, orc, coords, c_dev, dev, args, workload) -> 
                     "pct_hbm": 100.0 * nbytes / (ms / 1e3) / 1e9 / PEAK_HBM_GBS, **kw})
 
     ws = torch.empty(L.spc_scatter_mean_workspace_bytes(n, nc), dtype=torch.uint8, device=dev)
-    f2c, cnt = d.fine_to_coarse.contiguous(), d.counts.contiguous()
+    f2c, cnt, ch = d.fine_to_coarse.contiguous(), d.counts.contiguous(), d.children.contiguous()
     keep = []
     for c in (128, 1024):
         xf, _ = bf16_dev(orc, wl.normal((n, c), 1.0, seed=900 + c), dev)
@@ -652,6 +653,9 @@ def bench_feature_ops(spc, nat, wl, orc, coords, c_dev, dev, args, workload) -> 
         rec(f"scatter_mean {n}->{nc} C={c}", L.spc_scatter_mean,
             (s, BF, p(xf), p(f2c), p(cnt), p(yc), c, n, nc, p(ws), ws.numel()),
             n * c * 2 + nc * c * 2 + 4 * n + 4 * nc, rows_in=n, rows_out=nc, channels=c)
+        rec(f"children_mean {n}->{nc} C={c}", L.spc_children_mean,
+            (s, BF, p(xf), p(ch), p(cnt), p(yc), c, n, nc),
+            n * c * 2 + nc * c * 2 + 4 * 8 * nc + 4 * nc, rows_in=n, rows_out=nc, channels=c)
         rec(f"gather (upsample) {nc}->{n} C={c}", L.spc_gather_rows,
             (s, BF, p(xc), p(f2c), p(yf), n, nc, c), nc * c * 2 + n * c * 2 + 4 * n,
             rows_in=nc, rows_out=n, channels=c)

@@ -6,7 +6,8 @@
 //                      fine row inside a group), then one thread per
 //                      (coarse row, channel) adds in that order, rounding the
 //                      partial sum to the storage dtype after every add, and
-//                      divides by the count in F32.
+//                      divides by the count in F32 (16-byte groups of
+//                      channels per thread where the rows allow).
 //   spc_children_mean: the same values from the downsample map's children
 //                      lists (ascending fine rows, at most 8 per coarse row):
 //                      no sort, one pass.
@@ -77,6 +78,41 @@ __global__ __launch_bounds__(256) void scatter_mean_kernel(
     out[e] = S::st(S::ld(acc) / counts[r]);
 }
 
+// scatter_mean_kernel over 16-byte groups of channels (channels a multiple
+// of the group): one thread per (coarse row, group), the adds per element
+// in the same order.
+template <int DT>
+__global__ __launch_bounds__(256) void scatter_mean_vec_kernel(
+    const u32x4* __restrict__ feats, const int32_t* __restrict__ sv,
+    const int32_t* __restrict__ seg, const float* __restrict__ counts, int64_t groups,
+    int64_t nc, u32x4* __restrict__ out) {
+    using S = Store<DT>;
+    using T = typename S::t;
+    constexpr int VEC = 16 / sizeof(T);
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= nc * groups) return;
+    const int64_t r = e / groups;
+    const int64_t q = e - r * groups;
+    T acc[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) acc[v] = S::st(0.0f);
+    const int32_t b = seg[r];
+    const int32_t end = seg[r + 1];
+    for (int32_t p = b; p < end; ++p) {
+        const u32x4 w = feats[(int64_t)sv[p] * groups + q];
+        T x[VEC];
+        __builtin_memcpy(x, &w, 16);
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) acc[v] = S::st(S::ld(acc[v]) + S::ld(x[v]));
+    }
+    const float cnt = counts[r];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) acc[v] = S::st(S::ld(acc[v]) / cnt);
+    u32x4 o;
+    __builtin_memcpy(&o, acc, 16);
+    out[e] = o;
+}
+
 // The scatter-mean of one (coarse row, channel) from its children list
 // (ascending fine rows, padded with values outside [0, nf)): the same adds
 // in the same order as scatter_mean_kernel over the sorted rows.
@@ -98,6 +134,42 @@ __global__ __launch_bounds__(256) void children_mean_kernel(
         acc = S::st(S::ld(acc) + S::ld(feats[(int64_t)f * channels + c]));
     }
     out[e] = S::st(S::ld(acc) / counts[r]);
+}
+
+// The same over 16-byte groups of channels (channels a multiple of the
+// group): one thread per (coarse row, group), 16-byte loads and stores, the
+// adds per element as above.
+template <int DT>
+__global__ __launch_bounds__(256) void children_mean_vec_kernel(
+    const u32x4* __restrict__ feats, const int32_t* __restrict__ children,
+    const float* __restrict__ counts, int64_t groups, int64_t nf, int64_t nc,
+    u32x4* __restrict__ out) {
+    using S = Store<DT>;
+    using T = typename S::t;
+    constexpr int VEC = 16 / sizeof(T);
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= nc * groups) return;
+    const int64_t r = e / groups;
+    const int64_t q = e - r * groups;
+    T acc[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) acc[v] = S::st(0.0f);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int32_t f = children[r * 8 + k];
+        if (f < 0 || f >= nf) break;
+        const u32x4 w = feats[(int64_t)f * groups + q];
+        T x[VEC];
+        __builtin_memcpy(x, &w, 16);
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) acc[v] = S::st(S::ld(acc[v]) + S::ld(x[v]));
+    }
+    const float cnt = counts[r];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) acc[v] = S::st(S::ld(acc[v]) / cnt);
+    u32x4 o;
+    __builtin_memcpy(&o, acc, 16);
+    out[e] = o;
 }
 
 template <typename V>
@@ -175,6 +247,22 @@ int spc_scatter_mean(spc_stream_t stream, int dtype, const void* features, const
                                sort_bytes));
     }
     segment_bounds_kernel<<<grid_for(nc + 1, 256), 256, 0, s>>>(sk, nf, nc, seg);
+    const int es = dtype == SPC_F32 ? 4 : 2;
+    if ((dtype == SPC_F16 || dtype == SPC_BF16 || dtype == SPC_F32) && channels * es % 16 == 0 &&
+        ((uintptr_t)features & 15u) == 0 && ((uintptr_t)out & 15u) == 0) {
+        const int64_t groups = channels * es / 16;
+        const unsigned gv = grid_for(nc * groups, 256);
+        const u32x4* fv = static_cast<const u32x4*>(features);
+        u32x4* ov = static_cast<u32x4*>(out);
+        if (dtype == SPC_F16)
+            scatter_mean_vec_kernel<SPC_F16><<<gv, 256, 0, s>>>(fv, sv, seg, counts, groups, nc, ov);
+        else if (dtype == SPC_BF16)
+            scatter_mean_vec_kernel<SPC_BF16><<<gv, 256, 0, s>>>(fv, sv, seg, counts, groups, nc, ov);
+        else
+            scatter_mean_vec_kernel<SPC_F32><<<gv, 256, 0, s>>>(fv, sv, seg, counts, groups, nc, ov);
+        SPC_HIP(hipGetLastError());
+        return SPC_OK;
+    }
     const unsigned g = grid_for(nc * channels, 256);
     switch (dtype) {
         case SPC_F16:
@@ -212,6 +300,23 @@ int spc_children_mean(spc_stream_t stream, int dtype, const void* features,
     if (!out || !counts || !children || (nf > 0 && !features)) {
         set_last_error("spc_children_mean: null argument");
         return SPC_BAD_ARG;
+    }
+    const int es = dtype == SPC_F32 ? 4 : 2;
+    const bool vec = channels * es % 16 == 0 && ((uintptr_t)features & 15u) == 0 &&
+                     ((uintptr_t)out & 15u) == 0;
+    if (vec && (dtype == SPC_F16 || dtype == SPC_BF16 || dtype == SPC_F32)) {
+        const int64_t groups = channels * es / 16;
+        const unsigned gv = grid_for(nc * groups, 256);
+        const u32x4* fv = static_cast<const u32x4*>(features);
+        u32x4* ov = static_cast<u32x4*>(out);
+        if (dtype == SPC_F16)
+            children_mean_vec_kernel<SPC_F16><<<gv, 256, 0, s>>>(fv, children, counts, groups, nf, nc, ov);
+        else if (dtype == SPC_BF16)
+            children_mean_vec_kernel<SPC_BF16><<<gv, 256, 0, s>>>(fv, children, counts, groups, nf, nc, ov);
+        else
+            children_mean_vec_kernel<SPC_F32><<<gv, 256, 0, s>>>(fv, children, counts, groups, nf, nc, ov);
+        SPC_HIP(hipGetLastError());
+        return SPC_OK;
     }
     const unsigned g = grid_for(nc * channels, 256);
     switch (dtype) {
