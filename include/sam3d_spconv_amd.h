@@ -289,7 +289,10 @@ int spc_sparse_conv_plan(spc_stream_t stream, int dtype, const void* x, int w_dt
  *                    one 8-wave workgroup per CU (long tiles: wide channels);
  *   SPC_TILES_SMALL  128-row tiles (64 for 8 taps) over a 511-row stage,
  *                    two or three 4-wave workgroups per CU (short tiles: small
- *                    channel counts, few rows, the stride-2 conv);
+ *                    channel counts, few rows, the stride-2 conv; a stride-2
+ *                    conv of up to four 64-byte channel chunks whose tiles
+ *                    fit the CUs in one round stages all its chunks at once
+ *                    in four buffers, one 8-wave workgroup per CU);
  *   SPC_TILES_TALL   256-row tiles over a 559-row stage, three 4-wave
  *                    workgroups per CU (one-chunk rows: 16-bit C_in = 32 with
  *                    C_out 32 or 64); reads the wide tiles' plan section.
