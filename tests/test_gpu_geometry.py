@@ -152,6 +152,33 @@ def test_ragged_and_tiny(spc, orc, dev, geo, n):
     assert torch.equal(yw, ys) and torch.equal(yw, yt)
 
 
+@pytest.mark.parametrize("n", [1, 9, 70, 700])
+def test_stride2_ragged_and_tiny(spc, orc, dev, geo, n):
+    """Stride-2 convs over a few fine rows (one partial 64-row tile, dead
+    waves, coarse rows with one child): the wide, small and four-buffer
+    tiles agree with each other and with the oracle."""
+    import oracle
+    import torch
+
+    nat = geo
+    coords = spc.workloads.random_voxels(n, 6 if n < 100 else 14, batches=1, seed=n + 3)[:n]
+    coords = np.ascontiguousarray(coords)
+    nf = coords.shape[0]
+    d = nat.downsample_map(torch.from_numpy(coords).to(dev), 1, 16)
+    _case(f"stride-2 ragged nf={nf} nc={d.nc} 128->128")
+    (xh, wh, bh), (x, w, b) = _inputs(spc, orc, nf, 128, 128, 8, seed=n + 21)
+    pw = nat.pack_weights(w)
+    yw, ys, yq = _all(nat, lambda: nat.sparse_conv(
+        x, pw, b, d.stride2_taps, ntaps=8, n_out=d.nc,
+        plan=nat.conv_plan(d.stride2_taps, ntaps=8, n_out=d.nc, n_in=nf)))
+    assert torch.equal(yw, ys) and torch.equal(yw, yq)
+    ref = orc.sparse_conv(xh, wh, bh, d.stride2_taps.cpu().numpy(), ntaps=8, n_out=d.nc,
+                          idx_layout=1, out_dtype=oracle.F32, x_dtype=oracle.BF16,
+                          w_dtype=oracle.BF16, b_dtype=oracle.BF16, nthreads=oracle_threads(),
+                          blocked=True)
+    check_16bit(f"stride-2 ragged nf={nf}", from_dev(yq), ref)
+
+
 def test_q8_0_wide_equals_small(spc, orc, dev, geo):
     import torch
 
