@@ -36,7 +36,15 @@
 //   store   + bias in F32, one rounding; the MFMAs produce the transposed
 //           tile, so each lane holds runs of consecutive output channels of
 //           one row: they pass through an LDS output tile and every output
-//           row is written once with coalesced 16-byte stores.
+//           row is written once with coalesced 16-byte stores (8-wave
+//           16-bit tiles: per wave, through a private LDS region, with no
+//           workgroup barrier).
+//   shapes  the tile geometry (Geo below) sets rows per tile, stage rows
+//           and buffers: 256-row double-buffered tiles for long convs,
+//           128-row single-buffered ones several to a CU for short tiles,
+//           256-row single-buffered ones for one-chunk rows, and 64-row
+//           four-buffer ones for the stride-2 conv; every geometry runs the
+//           same MFMA steps in the same order, so all give the same bits.
 //   tiles   XCD-major: workgroup b runs on XCD b % 8 and each XCD gets a
 //           contiguous range of row tiles, so a neighbourhood's feature rows
 //           stay in that XCD's L2.
