@@ -103,8 +103,9 @@ def test_subm_wide_equals_small(spc, orc, dev, geo, dt, cin, cout, nvox, grid):
         check_16bit(f"small tiles {dt} {cin}->{cout}", from_dev(sp_), ref)
 
 
-@pytest.mark.parametrize("cin,cout", [(128, 128), (64, 64), (64, 32), (128, 1024)])
-def test_stride2_wide_equals_small(spc, orc, dev, geo, cin, cout):
+@pytest.mark.parametrize("dt,cin,cout", [("bf16", 128, 128), ("bf16", 64, 64), ("bf16", 64, 32),
+                                         ("bf16", 128, 1024), ("f16", 128, 128), ("f32", 64, 64)])
+def test_stride2_wide_equals_small(spc, orc, dev, geo, dt, cin, cout):
     """The 2x2x2 stride-2 conv on the config-2 coords: the wide tiles' 256
     coarse rows overflow their stage (per-tap fallback), the small tiles'
     64 coarse rows (about 340 fine rows) take the staged path, and so do the
@@ -117,8 +118,8 @@ def test_stride2_wide_equals_small(spc, orc, dev, geo, cin, cout):
     coords = spc.workloads.ellipsoid_batch()
     nf = coords.shape[0]
     d = nat.downsample_map(torch.from_numpy(coords).to(dev), 4, 64)
-    _case(f"stride-2 nf={nf} nc={d.nc} {cin}->{cout}: wide vs small vs by-shape tiles")
-    (xh, wh, bh), (x, w, b) = _inputs(spc, orc, nf, cin, cout, 8, seed=cin + 3 * cout)
+    _case(f"stride-2 {dt} nf={nf} nc={d.nc} {cin}->{cout}: wide vs small vs by-shape tiles")
+    (xh, wh, bh), (x, w, b) = _inputs(spc, orc, nf, cin, cout, 8, seed=cin + 3 * cout, dt=dt)
     pw = nat.pack_weights(w)
 
     def run():
@@ -127,11 +128,15 @@ def test_stride2_wide_equals_small(spc, orc, dev, geo, cin, cout):
 
     yw, ys, yq = _all(nat, run)
     assert torch.equal(yw, ys) and torch.equal(yw, yq)
+    code = {"bf16": oracle.BF16, "f16": oracle.F16, "f32": oracle.F32}[dt]
     ref = orc.sparse_conv(xh, wh, bh, d.stride2_taps.cpu().numpy(), ntaps=8, n_out=d.nc,
-                          idx_layout=1, out_dtype=oracle.F32, x_dtype=oracle.BF16,
-                          w_dtype=oracle.BF16, b_dtype=oracle.BF16, nthreads=oracle_threads(),
-                          blocked=True)
-    check_16bit(f"small tiles stride-2 {cin}->{cout}", from_dev(ys), ref)
+                          idx_layout=1, out_dtype=oracle.F32, x_dtype=code, w_dtype=code,
+                          b_dtype=code, nthreads=oracle_threads(), blocked=True)
+    if dt == "f32":
+        got = yq.cpu().numpy()
+        assert np.all(np.abs(got - ref) <= 1e-5 + 1e-4 * np.abs(ref))
+    else:
+        check_16bit(f"by-shape tiles stride-2 {dt} {cin}->{cout}", from_dev(yq), ref)
 
 
 @pytest.mark.parametrize("n", [1, 5, 127, 130, 300])
