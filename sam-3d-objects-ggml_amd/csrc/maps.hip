@@ -89,32 +89,46 @@ __global__ __launch_bounds__(256) void dense_insert_kernel(const int4* __restric
     atomicMin(&grid[(((int64_t)c.x * res + c.y) * res + c.z) * res + c.w], (int32_t)i);
 }
 
-__device__ inline int32_t hash_find(const unsigned long long* __restrict__ hkeys,
-                                    const int32_t* __restrict__ hvals, uint32_t cap_mask,
-                                    unsigned long long key) {
-    uint32_t h = hash_key(key) & cap_mask;
-    for (uint32_t it = 0; it <= cap_mask; ++it) {
-        const unsigned long long k = hkeys[h];
-        if (k == key) return hvals[h];
-        if (k == kEmptyKey) return -1;
-        h = (h + 1) & cap_mask;
-    }
-    return -1;
-}
-
 constexpr int kNbrTokens = 64;
 
 // Row lookups of the 27-offset query: the hash table, or a dense grid
 // [n_batch][R][R][R] of row ids when the caller bounds the coordinates.
+// A lookup runs in three steps so that a thread's lookups can have their
+// memory loads in flight together: start (the key and its first slot, or
+// dead), first (the one load most lookups need) and finish (the value;
+// the hash table's rare continued probe).
 struct HashLookup {
     const unsigned long long* hkeys;
     const int32_t* hvals;
     uint32_t cap_mask;
-    __device__ int32_t operator()(int b, int x, int y, int z) const {
+    struct Probe {
+        unsigned long long key;
+        uint32_t h;
+        bool live;
+    };
+    __device__ Probe start(int b, int x, int y, int z) const {
+        Probe p{0ull, 0u, false};
         if (b < 0 || b >= kBatchLimit || x < 0 || x >= kCoordLimit || y < 0 || y >= kCoordLimit ||
             z < 0 || z >= kCoordLimit)
-            return -1;
-        return hash_find(hkeys, hvals, cap_mask, pack_key(b, x, y, z));
+            return p;
+        p.key = pack_key(b, x, y, z);
+        p.h = hash_key(p.key) & cap_mask;
+        p.live = true;
+        return p;
+    }
+    __device__ unsigned long long first(const Probe& p) const { return p.live ? hkeys[p.h] : kEmptyKey; }
+    __device__ int32_t finish(const Probe& p, unsigned long long k) const {
+        if (!p.live || k == kEmptyKey) return -1;
+        if (k == p.key) return hvals[p.h];
+        // collision at the first slot: probe on from the next one
+        uint32_t h = (p.h + 1) & cap_mask;
+        for (uint32_t it = 0; it < cap_mask; ++it) {
+            const unsigned long long kk = hkeys[h];
+            if (kk == p.key) return hvals[h];
+            if (kk == kEmptyKey) return -1;
+            h = (h + 1) & cap_mask;
+        }
+        return -1;
     }
 };
 
@@ -122,12 +136,16 @@ struct DenseLookup {
     const int32_t* grid;
     int32_t n_batch;
     int32_t res;
-    __device__ int32_t operator()(int b, int x, int y, int z) const {
+    struct Probe {
+        int64_t cell;  // -1: outside the grid
+    };
+    __device__ Probe start(int b, int x, int y, int z) const {
         if (b < 0 || b >= n_batch || x < 0 || x >= res || y < 0 || y >= res || z < 0 || z >= res)
-            return -1;
-        const int32_t v = grid[(((int64_t)b * res + x) * res + y) * res + z];
-        return v == INT_MAX ? -1 : v;
+            return Probe{-1};
+        return Probe{(((int64_t)b * res + x) * res + y) * res + z};
     }
+    __device__ int32_t first(const Probe& p) const { return p.cell >= 0 ? grid[p.cell] : INT_MAX; }
+    __device__ int32_t finish(const Probe&, int32_t v) const { return v == INT_MAX ? -1 : v; }
 };
 
 // MESH: duplicates are an error (build_mesh_conv_table); otherwise the
@@ -140,16 +158,30 @@ __global__ __launch_bounds__(256) void neighbor_kernel(
     __shared__ int32_t owner[kNbrTokens];
     const int tid = threadIdx.x;
     const int64_t t0 = (int64_t)blockIdx.x * kNbrTokens;
-    for (int e = tid; e < 27 * kNbrTokens; e += 256) {
+    // the thread's (offset, token) pairs e = tid + 256 i: every lookup's
+    // first load issued before any result is needed
+    constexpr int PER = (27 * kNbrTokens + 255) / 256;
+    typename Lookup::Probe pr[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int e = tid + 256 * i;
         const int o = e / kNbrTokens;
         const int tl = e % kNbrTokens;
         const int64_t t = t0 + tl;
-        int32_t res = -1;
-        if (t < n) {
+        if (e < 27 * kNbrTokens && t < n) {
             const int4 c = coords[t];
-            res = find(c.x, c.y + (o / 9 - 1), c.z + ((o / 3) % 3 - 1), c.w + (o % 3 - 1));
+            pr[i] = find.start(c.x, c.y + (o / 9 - 1), c.z + ((o / 3) % 3 - 1), c.w + (o % 3 - 1));
+        } else {
+            pr[i] = find.start(-1, 0, 0, 0);  // dead
         }
-        nb[o][tl] = res;
+    }
+    decltype(find.first(pr[0])) fk[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) fk[i] = find.first(pr[i]);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int e = tid + 256 * i;
+        if (e < 27 * kNbrTokens) nb[e / kNbrTokens][e % kNbrTokens] = find.finish(pr[i], fk[i]);
     }
     __syncthreads();
     if (tid < kNbrTokens) {
