@@ -1147,6 +1147,15 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
                     step(std::integral_constant<int, 3>{});
 #pragma unroll
                     for (int w = 0; w + 1 < kTapWords; ++w) tw[w] = tw[w + 1];
+                    // 8 waves: waves w and w + 4 share a SIMD, and the older
+                    // one wins issue, so waves 4-7 fell ~3.4 us behind in
+                    // every chunk and ended it alone; taking turns at the
+                    // higher priority every step group keeps the pair
+                    // together (config 2: 55.3 -> 54.2 us)
+                    if constexpr (NW == 8) {
+                        if (((g + (wave >> 2)) & 1) != 0) __builtin_amdgcn_s_setprio(1);
+                        else __builtin_amdgcn_s_setprio(0);
+                    }
                 };
                 for (int g = 0; g + 1 < ngr; ++g) run_group(g, std::false_type{});
                 run_group(ngr - 1, std::true_type{});
@@ -1168,6 +1177,7 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
             } else {
                 run_tile(fm_all);
             }
+            if constexpr (NW == 8) __builtin_amdgcn_s_setprio(0);
         }
     } else if (nt > 0) {
         // Fallback (the union does not fit the stage): the 256 source rows of
