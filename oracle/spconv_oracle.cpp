@@ -419,7 +419,7 @@ int64_t orc_downsample_map(const int32_t* coords, int64_t nf, int32_t* fine_to_c
 }
 
 // ---------------------------------------------------------------------------
-// Stride-2, kernel-2 tap table (the reference runs the
+// Stride-2, kernel-2 tap table (the 64^3 -> 32^3 downsampling conv; the reference runs the
 // strided SparseConv3d through spconv, SP/conv/conv_spconv.py:39-50, where
 // an input p lands in output p//2 at kernel tap k = p%2 per axis).
 // taps[c*8 + k] = fine row at tap k = (x&1)*4 + (y&1)*2 + (z&1) of coarse

@@ -1151,7 +1151,8 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
                     // one wins issue, so waves 4-7 fell ~3.4 us behind in
                     // every chunk and ended it alone; taking turns at the
                     // higher priority every step group keeps the pair
-                    // together (config 2: 55.3 -> 54.2 us)
+                    // together (C=128 over 4 ellipsoid shells, 62,710 rows:
+                    // 55.3 -> 54.2 us)
                     if constexpr (NW == 8) {
                         if (((g + (wave >> 2)) & 1) != 0) __builtin_amdgcn_s_setprio(1);
                         else __builtin_amdgcn_s_setprio(0);
@@ -1535,7 +1536,7 @@ hipError_t launch_conv(hipStream_t s, ConvArgs a) {
 
 // The stride-2 conv's 64-row tiles over four buffers (GeoQuad), picked by
 // shape: up to four 64-byte channel chunks (C_in <= 128 in 16-bit, 64 in
-// f32) and every tile on its own CU in one round (config 2's 11,774 coarse
+// f32) and every tile on its own CU in one round (4 ellipsoid shells' 11,774 coarse
 // rows at C_out 128: 184 tiles).  Same wave layouts as the small tiles.
 template <typename T, bool Q8, bool PACKED, int NTAPS>
 bool use_quad_tiles(const ConvArgs& a, int tn) {

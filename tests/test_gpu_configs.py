@@ -1,4 +1,4 @@
-"""GPU parity at BASELINE's full shapes for the stages not covered by
+"""GPU parity at the workloads' full shapes for the stages not covered by
 test_gpu_conv.py, every output row against the oracle:
 
   config 3  the coarse-map submanifold convs of the SLAT IO block at 32^3

@@ -91,7 +91,7 @@ def test_bf16_wide_tiles(spc, orc, dev, ntaps, cout):
 
 
 def test_bf16_config2_ellipsoids(spc, orc, dev):
-    """BASELINE config 2: 4 ellipsoid shells, C=128, bf16, fp32 accumulate;
+    """4 ellipsoid shells in 64^3 (N=62,710), C=128, bf16, fp32 accumulate;
     every output row against the oracle, in natural and in mask-argsort
     processing order."""
     import torch
@@ -134,7 +134,7 @@ def test_bf16_single_shell_c128(spc, orc, dev):
 
 
 def test_f32_config1_sphere(spc, orc, dev):
-    """BASELINE config 1 on the GPU: sphere shell, C=64, fp32, zero bias;
+    """One sphere shell in 64^3 (N=21,766) on the GPU: C=64, fp32, zero bias;
     every row within |a-b| <= 1e-5 + 1e-4 |b|."""
     import oracle
     import torch
@@ -254,7 +254,7 @@ def test_f16_spconv_bridge(spc, orc, dev):
 
 
 def test_q8_0_config5_sphere(spc, orc, dev):
-    """Q8_0 weights (C=768) dequantised inside the GEMM,
+    """Sphere shell, Q8_0 weights (C=768) dequantised inside the GEMM,
     against the reference's f16(f32(d)*q) GEMM input."""
     import oracle
     import torch
@@ -328,7 +328,7 @@ def test_q8_0_expand_matches_packing(spc, orc, dev, ntaps, cin, cout, layout):
 
 
 def test_stride2_conv(spc, orc, dev):
-    """BASELINE config 3 first stage: 2x2x2 stride-2 conv 64^3 -> 32^3."""
+    """The SLAT IO block's first stage: 2x2x2 stride-2 conv 64^3 -> 32^3."""
     import torch
 
     nat = spc._native
