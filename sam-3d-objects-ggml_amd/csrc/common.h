@@ -93,6 +93,28 @@ __device__ __forceinline__ void dma_barrier() {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
+// s_waitcnt vmcnt(n) for a wave-uniform run-time n in [0, MAX]: the
+// immediate comes from a chain of scalar compares.
+template <int N, int MAX>
+__device__ __forceinline__ void wait_vmcnt_le(int n) {
+    if constexpr (N >= MAX) {
+        wait_vmcnt<MAX>();
+    } else {
+        if (n <= N) wait_vmcnt<N>();
+        else wait_vmcnt_le<N + 1, MAX>(n);
+    }
+}
+
+// dma_barrier for a run-time count n <= MAX of younger loads.
+template <int MAX>
+__device__ __forceinline__ void dma_barrier_le(int n) {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    wait_vmcnt_le<0, MAX>(n);
+    __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // Round-to-nearest-even float -> bf16 / f16 bits (device): the gfx950
 // hardware converts (v_cvt_pk_bf16_f32, v_cvt_f16_f32); NaNs stay NaNs.
 __device__ inline uint16_t f32_to_bf16_bits(float f) {

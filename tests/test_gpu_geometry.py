@@ -104,7 +104,8 @@ def test_subm_wide_equals_small(spc, orc, dev, geo, dt, cin, cout, nvox, grid):
 
 
 @pytest.mark.parametrize("dt,cin,cout", [("bf16", 128, 128), ("bf16", 64, 64), ("bf16", 64, 32),
-                                         ("bf16", 128, 1024), ("f16", 128, 128), ("f32", 64, 64)])
+                                         ("bf16", 32, 64), ("bf16", 96, 32), ("bf16", 128, 1024),
+                                         ("f16", 128, 128), ("f32", 64, 64)])
 def test_stride2_wide_equals_small(spc, orc, dev, geo, dt, cin, cout):
     """The 2x2x2 stride-2 conv on the config-2 coords: the wide tiles' 256
     coarse rows overflow their stage (per-tap fallback), the small tiles'
@@ -182,6 +183,35 @@ def test_stride2_ragged_and_tiny(spc, orc, dev, geo, n):
                           w_dtype=oracle.BF16, b_dtype=oracle.BF16, nthreads=oracle_threads(),
                           blocked=True)
     check_16bit(f"stride-2 ragged nf={nf}", from_dev(yq), ref)
+
+
+def test_stride2_q8_0(spc, orc, dev, geo):
+    """Stride-2 128 -> 128 with Q8_0 weights on the config-2 coords: the
+    four-buffer tiles the shape picks (their weight ring holds the block
+    scales too) equal the wide and small tiles and the oracle on the
+    kernel's operands bf16(f32(d) * q)."""
+    import oracle
+    import torch
+
+    nat = geo
+    coords = spc.workloads.ellipsoid_batch()
+    nf = coords.shape[0]
+    d = nat.downsample_map(torch.from_numpy(coords).to(dev), 4, 64)
+    _case(f"stride-2 Q8_0 nf={nf} nc={d.nc} 128->128: wide vs small vs by-shape tiles")
+    (xh, _, bh), (x, _, b) = _inputs(spc, orc, nf, 128, 128, 8, seed=77)
+    blocks = orc.q8_0_quantize(spc.workloads.normal((128, 8, 128), 0.05, seed=78))
+    qs, dsc = nat.q8_0_repack(torch.from_numpy(blocks).to(dev))
+    pq = nat.pack_weights(qs, dsc, cin=128, cout=128, ntaps=8)
+    yw, ys, yq = _all(nat, lambda: nat.sparse_conv(
+        x, pq, b, d.stride2_taps, ntaps=8, n_out=d.nc,
+        plan=nat.conv_plan(d.stride2_taps, ntaps=8, n_out=d.nc, n_in=nf)))
+    assert torch.equal(yw, ys) and torch.equal(yw, yq)
+    wq = orc.q8_0_dequant(blocks, oracle.BF16)
+    ref = orc.sparse_conv(xh, wq, bh, d.stride2_taps.cpu().numpy(), ntaps=8, n_out=d.nc,
+                          idx_layout=1, out_dtype=oracle.F32, x_dtype=oracle.BF16,
+                          w_dtype=oracle.BF16, b_dtype=oracle.BF16, nthreads=oracle_threads(),
+                          blocked=True)
+    check_16bit("stride-2 Q8_0 by-shape tiles", from_dev(yq), ref)
 
 
 def test_q8_0_wide_equals_small(spc, orc, dev, geo):
