@@ -76,6 +76,7 @@ struct ConvArgs {
     int32_t cout;
     int32_t packed;
     int32_t tiles_n;
+    int32_t col_major;        // full row tiles' tiles taken column tile by column tile
     int64_t total_tiles;
     int64_t heavy_tiles;      // tiles of full row tiles (mapped XCD-major)
     int64_t class_rows;       // > 0: rows [c * class_rows, (c + 1) * class_rows) use weight
@@ -659,9 +660,14 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
 
-    // Tile mapping: the full row tiles XCD-major (workgroup b runs on XCD
-    // b % 8, each XCD gets a contiguous range), then the tiles of a partial
-    // last row tile, which run last and cost little.
+    // Tile mapping: the tiles of the full row tiles XCD-major (workgroup b
+    // runs on XCD b % 8, each XCD gets a contiguous range of them), then the
+    // tiles of a partial last row tile, which run last and cost little.
+    // Within the range, row tile by row tile (the column tiles of a row
+    // tile share its gathered rows in the XCD's L2), or, with weights larger
+    // than half an L2 (col_major), column tile by column tile: the tiles an
+    // XCD runs at once then share their weight panels (SubM 128 -> 1024 and
+    // 1024 -> 1024 over 11,774 rows, Q8_0 C = 768: 3-4 % faster).
     int64_t tile;
     const int64_t hb = a.tiles_per_xcd * 8;  // workgroups of the XCD-major part
     if ((int64_t)blockIdx.x < hb) {
@@ -673,8 +679,16 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
         tile = a.heavy_tiles + ((int64_t)blockIdx.x - hb);
         if (tile >= a.total_tiles) return;
     }
-    const int64_t tm = tile / a.tiles_n;
-    const int tn = (int)(tile % a.tiles_n);
+    int64_t tm;
+    int tn;
+    if (tile < a.heavy_tiles && a.col_major) {
+        const int64_t mfull = a.heavy_tiles / a.tiles_n;  // full row tiles
+        tm = tile % mfull;
+        tn = (int)(tile / mfull);
+    } else {
+        tm = tile / a.tiles_n;
+        tn = (int)(tile % a.tiles_n);
+    }
     const int64_t r0 = tm * TM;
     const int co0 = tn * TN;
 
@@ -1574,6 +1588,8 @@ hipError_t launch_conv(hipStream_t s, ConvArgs a) {
     a.total_tiles = tiles_m * a.tiles_n;
     a.heavy_tiles = (a.n_out % TM ? tiles_m - 1 : tiles_m) * a.tiles_n;
     a.tiles_per_xcd = ceil_div(a.heavy_tiles, 8);
+    const int64_t wbytes = (int64_t)NTAPS * max(1, a.n_classes) * a.cin * a.cout * (Q8 ? 1 : (int)sizeof(T));
+    a.col_major = a.tiles_n > 1 && wbytes > (2 << 20);
     const int64_t grid = a.tiles_per_xcd * 8 + (a.total_tiles - a.heavy_tiles);
     if (grid == 0) return hipSuccess;
     // the plan buffer holds the wide plans, then the small ones
