@@ -185,6 +185,39 @@ def test_stride2_ragged_and_tiny(spc, orc, dev, geo, n):
     check_16bit(f"stride-2 ragged nf={nf}", from_dev(yq), ref)
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_stride2_random(spc, orc, dev, geo, seed):
+    """Seeded random stride-2 convs (voxel count, grid, batches, 1-4 channel
+    chunks, output width): the four-buffer tiles the shape picks (whole-chunk
+    weight ring, each chunk staged one ahead) equal the wide and small tiles
+    bit for bit and the oracle."""
+    import oracle
+    import torch
+
+    nat = geo
+    rng = np.random.default_rng(1000 + seed)
+    n = int(rng.integers(500, 12000))
+    res = int(rng.choice([24, 32, 48]))
+    batches = int(rng.integers(1, 4))
+    cin = int(rng.choice([32, 64, 96, 128]))
+    cout = int(rng.choice([32, 64, 128]))
+    coords = spc.workloads.random_voxels(n, res, batches=batches, seed=seed + 40)
+    nf = coords.shape[0]
+    d = nat.downsample_map(torch.from_numpy(coords).to(dev), batches, res)
+    _case(f"stride-2 random seed={seed} nf={nf} nc={d.nc} res={res} B={batches} {cin}->{cout}")
+    (xh, wh, bh), (x, w, b) = _inputs(spc, orc, nf, cin, cout, 8, seed=seed + 60)
+    pw = nat.pack_weights(w)
+    yw, ys, yq = _all(nat, lambda: nat.sparse_conv(
+        x, pw, b, d.stride2_taps, ntaps=8, n_out=d.nc,
+        plan=nat.conv_plan(d.stride2_taps, ntaps=8, n_out=d.nc, n_in=nf)))
+    assert torch.equal(yw, ys) and torch.equal(yw, yq)
+    ref = orc.sparse_conv(xh, wh, bh, d.stride2_taps.cpu().numpy(), ntaps=8, n_out=d.nc,
+                          idx_layout=1, out_dtype=oracle.F32, x_dtype=oracle.BF16,
+                          w_dtype=oracle.BF16, b_dtype=oracle.BF16, nthreads=oracle_threads(),
+                          blocked=True)
+    check_16bit(f"stride-2 random seed={seed}", from_dev(yq), ref)
+
+
 def test_stride2_q8_0(spc, orc, dev, geo):
     """Stride-2 128 -> 128 with Q8_0 weights on the config-2 coords: the
     four-buffer tiles the shape picks (their weight ring holds the block
