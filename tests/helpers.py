@@ -33,7 +33,8 @@ def max_rel(a: np.ndarray, b: np.ndarray) -> float:
 
 
 def oracle_threads() -> int:
-    """Host threads for the oracle's checks (the CPU share of one GPU box)."""
+    """Host threads for the oracle's checks: the process's CPU affinity, at
+    most 16 (the host cores a one-GPU machine gives a process)."""
     import oracle
 
     return max(1, min(oracle.cpu_threads(), 16))
