@@ -89,15 +89,18 @@ __global__ __launch_bounds__(256) void dense_insert_kernel(const int4* __restric
     atomicMin(&grid[(((int64_t)c.x * res + c.y) * res + c.z) * res + c.w], (int32_t)i);
 }
 
-constexpr int kNbrTokens = 64;
-
 // Row lookups of the 27-offset query: the hash table, or a dense grid
 // [n_batch][R][R][R] of row ids when the caller bounds the coordinates.
+// kTokens: rows per 256-thread block of the query.  Hash probes chain
+// dependent loads, so more, smaller blocks hide them better (4 ellipsoid
+// shells, 62,710 rows: 64 -> 16 rows per block, hash build 101 -> 86 us);
+// the dense grid's single loads favour 32 (dense build 53.5 -> 53.0 us).
 // A lookup runs in three steps so that a thread's lookups can have their
 // memory loads in flight together: start (the key and its first slot, or
 // dead), first (the one load most lookups need) and finish (the value;
 // the hash table's rare continued probe).
 struct HashLookup {
+    static constexpr int kTokens = 16;
     const unsigned long long* hkeys;
     const int32_t* hvals;
     uint32_t cap_mask;
@@ -133,6 +136,7 @@ struct HashLookup {
 };
 
 struct DenseLookup {
+    static constexpr int kTokens = 32;
     const int32_t* grid;
     int32_t n_batch;
     int32_t res;
@@ -154,21 +158,21 @@ template <bool MESH, typename Lookup>
 __global__ __launch_bounds__(256) void neighbor_kernel(
     const int4* __restrict__ coords, int64_t n, Lookup find, int32_t* __restrict__ token_major,
     int32_t* __restrict__ offset_major, int32_t* __restrict__ mask_nat, int32_t* status) {
-    __shared__ int32_t nb[27][kNbrTokens + 1];
-    __shared__ int32_t owner[kNbrTokens];
+    __shared__ int32_t nb[27][Lookup::kTokens + 1];
+    __shared__ int32_t owner[Lookup::kTokens];
     const int tid = threadIdx.x;
-    const int64_t t0 = (int64_t)blockIdx.x * kNbrTokens;
+    const int64_t t0 = (int64_t)blockIdx.x * Lookup::kTokens;
     // the thread's (offset, token) pairs e = tid + 256 i: every lookup's
     // first load issued before any result is needed
-    constexpr int PER = (27 * kNbrTokens + 255) / 256;
+    constexpr int PER = (27 * Lookup::kTokens + 255) / 256;
     typename Lookup::Probe pr[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
         const int e = tid + 256 * i;
-        const int o = e / kNbrTokens;
-        const int tl = e % kNbrTokens;
+        const int o = e / Lookup::kTokens;
+        const int tl = e % Lookup::kTokens;
         const int64_t t = t0 + tl;
-        if (e < 27 * kNbrTokens && t < n) {
+        if (e < 27 * Lookup::kTokens && t < n) {
             const int4 c = coords[t];
             pr[i] = find.start(c.x, c.y + (o / 9 - 1), c.z + ((o / 3) % 3 - 1), c.w + (o % 3 - 1));
         } else {
@@ -181,10 +185,10 @@ __global__ __launch_bounds__(256) void neighbor_kernel(
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
         const int e = tid + 256 * i;
-        if (e < 27 * kNbrTokens) nb[e / kNbrTokens][e % kNbrTokens] = find.finish(pr[i], fk[i]);
+        if (e < 27 * Lookup::kTokens) nb[e / Lookup::kTokens][e % Lookup::kTokens] = find.finish(pr[i], fk[i]);
     }
     __syncthreads();
-    if (tid < kNbrTokens) {
+    if (tid < Lookup::kTokens) {
         const int64_t t = t0 + tid;
         int own = 0;
         if (t < n) {
@@ -194,7 +198,7 @@ __global__ __launch_bounds__(256) void neighbor_kernel(
         owner[tid] = own;
     }
     __syncthreads();
-    const int64_t valid_tokens = n - t0 < kNbrTokens ? n - t0 : kNbrTokens;
+    const int64_t valid_tokens = n - t0 < Lookup::kTokens ? n - t0 : Lookup::kTokens;
     if (token_major) {
         for (int e = tid; e < 27 * valid_tokens; e += 256) {
             const int tl = e / 27;
@@ -204,9 +208,9 @@ __global__ __launch_bounds__(256) void neighbor_kernel(
         }
     }
     if (offset_major) {
-        for (int e = tid; e < 27 * kNbrTokens; e += 256) {
-            const int o = e / kNbrTokens;
-            const int tl = e % kNbrTokens;
+        for (int e = tid; e < 27 * Lookup::kTokens; e += 256) {
+            const int o = e / Lookup::kTokens;
+            const int tl = e % Lookup::kTokens;
             if (tl < valid_tokens) {
                 const int32_t v = owner[tl] ? nb[o][tl] : -1;
                 offset_major[(int64_t)o * n + t0 + tl] = v;
@@ -292,7 +296,7 @@ int finish_map(hipStream_t s, const int4* c4, int64_t n, bool mesh, Lookup find,
                int32_t* token_major, int32_t* offset_major, int32_t* mask_sorted, int32_t* argsort,
                int32_t* mask_natural, const MapWs& w) {
     int32_t* mnat = mask_natural ? mask_natural : w.mask_nat;
-    const unsigned nb = (unsigned)((n + kNbrTokens - 1) / kNbrTokens);
+    const unsigned nb = (unsigned)((n + Lookup::kTokens - 1) / Lookup::kTokens);
     if (mesh)
         neighbor_kernel<true, Lookup><<<nb, 256, 0, s>>>(c4, n, find, token_major, offset_major,
                                                          mnat, w.status);
