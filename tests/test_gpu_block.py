@@ -26,7 +26,7 @@ def _dev_feats(orc, a, dt, dev):
 
 @pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
 @pytest.mark.parametrize("c,affine,silu", [(128, True, True), (96, False, True), (1024, True, True),
-                                            (32, True, False), (2048, False, False)])
+                                            (512, True, True), (32, True, False), (2048, False, False)])
 def test_layernorm_silu(spc, orc, dev, dt, c, affine, silu):
     import oracle
 
