@@ -52,8 +52,8 @@ def parse():
                     help="row processing order of the conv kernel")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--headline-only", action="store_true",
-                    help="config 2: time the conv only (no single-shell, bridge or library-GEMM "
-                         "lines), for counter runs")
+                    help="configs 0, 1, 2, 5: time the conv only (no single-shell, bridge, "
+                         "f16-operand or library-GEMM lines), for counter runs")
     ap.add_argument("--fused-only", action="store_true",
                     help="configs 6 / 7: time the fused block only (no unfused comparison)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
@@ -230,6 +230,40 @@ def cpu_baseline(orc, x_bits, w_bits, b_bits, tm, coords, n, cin, cout, target_s
                                  "sample": f"std::map 27-offset table + stable mask argsort, "
                                            f"all {n} voxels, median of 5"},
     }
+
+
+def bench_q8_f16_operands(nat, x, pq8, bias, idx, plan, n, flops, steps=50, warmup=10):
+    """Config 5 with the reference's GEMM operands (the sparse module's
+    default for Q8_0 under bf16 features): bf16 features cast to f16, the
+    packed quants expanded to f16(f32(d) * q), the f16 conv, the output cast
+    back to bf16 -- all four launches timed per step."""
+    import torch
+
+    L = nat.lib()
+    s = torch.cuda.current_stream().cuda_stream
+    cout = pq8.cout
+    x16 = torch.empty(x.shape, dtype=torch.float16, device=x.device)
+    b16 = nat.convert(bias, torch.float16)
+    w16 = nat.expand_q8_0(pq8, dtype=torch.float16)
+    y16 = torch.empty((n, cout), dtype=torch.float16, device=x.device)
+    y = torch.empty((n, cout), dtype=torch.bfloat16, device=x.device)
+    conv = ConvCall(nat, x16, w16, b16, y16, idx, ntaps=27, n_out=n, layout=nat.IDX_TOKEN_MAJOR,
+                    plan=plan)
+
+    def step():
+        st = L.spc_convert(s, nat.BF16, x.data_ptr(), nat.F16, x16.data_ptr(), x.numel())
+        st |= L.spc_conv_expand_q8_0_to(s, pq8.data.data_ptr(), 27, pq8.cin, cout, nat.F16,
+                                        w16.data.data_ptr())
+        conv()
+        st |= L.spc_convert(s, nat.F16, y16.data_ptr(), nat.BF16, y.data_ptr(), y.numel())
+        if st != 0:
+            raise RuntimeError("f16-operand Q8_0 step failed")
+
+    ms, _ = time_gpu(step, steps, warmup)
+    ms_conv, _ = time_gpu(conv, steps, warmup)
+    return {"ms_per_step": ms, "tflops": flops / (ms / 1e3) / 1e12,
+            "conv_only_ms": ms_conv,
+            "path": "cast bf16->f16 + expand Q8_0 to f16(d*q) + f16 conv + cast f16->bf16"}
 
 
 def copy_calibration(steps: int):
@@ -462,6 +496,9 @@ def main():
         if cfg == 5 and not args.bf16_weights:
             result["config"]["q8_path"] = ("dequant in registers" if args.q8_in_registers else
                                            "expand to packed bf16 + bf16 conv, both timed")
+            if not args.headline_only:
+                result["f16_operands"] = bench_q8_f16_operands(
+                    nat, x, nat.pack_weights(qs, dsc, cin=cin, cout=cout), b, idx, plan, n, flops)
         if cfg == 2 and not args.headline_only:
             result["single_shell"] = bench_single_shell(nat, wl, orc, dev, args)
             result["bridge"] = bench_bridge(nat, wl, c_dev, dev, args)

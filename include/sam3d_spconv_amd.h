@@ -15,10 +15,11 @@
  *     library allocates nothing at run time; scratch space comes from a
  *     caller-owned workspace whose size the *_workspace_bytes queries
  *     return.  The exceptions, one per device for the life of the process:
- *     the spconv bridge's 64 MiB weight-pack buffer and its tile-plan cache
- *     (sam3d_spconv_f16_forward, whose signature has no workspace; the
- *     cache is the one run-time hipMalloc) and the 56 MiB map scratch of
- *     spc_map_build_noalloc -- documented at their entry points.
+ *     the spconv bridge's packed weights, padded rows and tile-plan cache
+ *     (sam3d_spconv_f16_forward, whose signature has no workspace: grown
+ *     with hipMalloc by the calls that need them) and the 56 MiB static map
+ *     scratch of spc_map_build_noalloc (reserved on every device the library
+ *     runs on) -- documented at their entry points.
  *   - Calls are asynchronous on `stream` (a hipStream_t; 0 = null stream)
  *     unless documented as synchronising.  Calls on one stream are ordered;
  *     separate workspaces make calls on different streams independent.
@@ -342,6 +343,22 @@ int spc_conv_pack_weights(spc_stream_t stream, int w_dtype, int w_layout, const 
 int spc_conv_expand_q8_0(spc_stream_t stream, const void* packed_q8, int64_t ntaps, int64_t cin,
                          int64_t cout, void* packed_bf16);
 
+/* spc_conv_expand_q8_0 with the operand type chosen: out_dtype SPC_BF16
+ * (bf16(f32(d) * q), as above) or SPC_F16 (f16(f32(d) * q): exactly the
+ * weights the reference's Q8_0 convs feed their f16 GEMM, as_f16 in
+ * SRC/slat_flow_graph.cpp:24-27).  With f16 features (spc_convert turns
+ * bf16 features into f16 exactly, inside f16's range) the f16 conv over
+ * these panels takes the reference's GEMM operands. */
+int spc_conv_expand_q8_0_to(spc_stream_t stream, const void* packed_q8, int64_t ntaps,
+                            int64_t cin, int64_t cout, int out_dtype, void* packed_out);
+
+/* Element conversion of n values between SPC_F32, SPC_F16 and SPC_BF16
+ * (round to nearest even; bf16 -> f16 is exact for magnitudes in
+ * [2^-17, 65504]).  No reference counterpart: the feature casts around
+ * the f16-operand Q8_0 conv (the reference graph's ggml_cast nodes). */
+int spc_convert(spc_stream_t stream, int src_dtype, const void* src, int dst_dtype, void* dst,
+                int64_t n);
+
 /* Drop-in for the reference's spconv bridge (same name, arguments and
  * layouts as cpp_ggml/third_party/sam3d-spconv/include/
  * sam3d_spconv_bridge.cuh:10-21, called from PATCH:2033-2038): f16
@@ -352,20 +369,25 @@ int spc_conv_expand_q8_0(spc_stream_t stream, const void* packed_q8, int64_t nta
  * natural order, which keeps each tile's gathered rows spatially coherent
  * (the output is the same in any order).  Accumulates in F32 (the
  * reference kernel accumulates in f16).  channels and output_channels must
- * be multiples of 32.  The KRSC weights are packed on every call into a
- * library-owned 64 MiB device buffer (one per device, held until the
- * process ends) and the packed conv runs on them.  The tile setup comes
- * from a library-owned tile plan per device with a copy of the indices it
- * was built from (device memory of about 160 bytes per token, hipMalloc'd
- * when a call needs more, held until the process ends): each call checks
- * its indices against the copy in the same launch as the weight pack, and
- * tiles whose entries changed set themselves up and refresh their plan, so
- * repeated calls over one index table skip the setup.  Bridge calls on one
- * device share these buffers, so calls on different streams of one device
- * must not overlap (the reference's bridge, too, assumes one stream).
- * Weights larger than the buffer run unpacked (same results, slower).  Returns
- * nothing, like the reference: spc_last_error() is cleared on entry and
- * is non-empty after the call exactly when it failed (output unwritten). */
+ * be multiples of 8, as the reference's spconv iterators take them
+ * (.../inpitera/ForwardDgradSparseIOIterator.h:58-61); widths that are not
+ * multiples of 32 run zero-padded to the next multiple of 32 (the input
+ * rows copied in, the output rows copied out; input and output 16-byte
+ * aligned).  The KRSC weights are packed on every call into a
+ * library-owned device buffer and the packed conv runs on them.  The tile
+ * setup comes from library-owned tile plans, up to four per device keyed
+ * by (tokens, tile geometry) with the least recently used replaced, each
+ * with a copy of the indices it was built from (about 160 bytes per token):
+ * each call checks its indices against the copy in the same launch as the
+ * weight pack, and tiles whose entries changed set themselves up and
+ * refresh their plan, so repeated calls over one index table skip the
+ * setup, also when calls alternate between token counts.  These buffers
+ * (one set per device) are grown with hipMalloc when a call needs more and
+ * held until the process ends; bridge calls on one device share them, so
+ * calls on different streams of one device must not overlap (the
+ * reference's bridge, too, assumes one stream).  Returns nothing, like the
+ * reference: spc_last_error() is cleared on entry and is non-empty after
+ * the call exactly when it failed (output unwritten). */
 void sam3d_spconv_f16_forward(spc_stream_t stream, const void* input, const void* weight,
                               const void* bias, void* output, const int32_t* indices,
                               const uint32_t* mask, const int32_t* mask_argsort, int64_t tokens,

@@ -449,7 +449,8 @@ def group_norm_items(a: np.ndarray, offsets: np.ndarray, groups: int, gamma=None
 
 
 def subdivide_block(o: "_Oracle", x: np.ndarray, coords: np.ndarray, p: dict, groups: int,
-                    dtype: int = BF16):
+                    dtype: int = BF16, nthreads: int = 1, blocked: bool = False,
+                    rows: np.ndarray | None = None):
     """SparseSubdivideBlock3d.forward (decoder_mesh.py:69-83): h =
     dt(silu(dt(GN(x)))) gathered to the children (SparseSubdivide order,
     spatial.py:108-130), conv1, dt(silu(dt(GN))), conv2, + skip(subdivide(x))
@@ -457,30 +458,37 @@ def subdivide_block(o: "_Oracle", x: np.ndarray, coords: np.ndarray, p: dict, gr
     co], SRC/mesh_decoder_graph.cpp:349-384) or the identity.  p: float32
     gn0_w, gn0_b, conv1_w [Co,27,Ci], conv1_b, gn1_w, gn1_b, conv2_w,
     conv2_b, optional skip_w (the [Co,1,1,1,Ci] buffer) and skip_b.
-    Returns (child coords, features)."""
+    nthreads / blocked select the conv's threads and its vectorised form
+    (same values).  rows: output rows to return (conv1 and both GroupNorms
+    still run over every child; conv2 and the skip only at these rows).
+    Returns (child coords, features) -- features of `rows` when given."""
     r = lambda a: round_to(o, a, dtype)  # noqa: E731
     bits = {F32: lambda a: np.ascontiguousarray(a, np.float32), BF16: o.f32_to_bf16,
             F16: o.f32_to_f16}[dtype]
 
-    def conv(h, w, b, table, ntaps):
-        y = o.sparse_conv(bits(h), bits(w), bits(b), table, ntaps=ntaps, n_out=h.shape[0],
-                          idx_layout=1, out_dtype=F32, x_dtype=dtype, w_dtype=dtype, b_dtype=dtype)
+    def conv(h, w, b, table, ntaps, n_out):
+        y = o.sparse_conv(bits(h), bits(w), bits(b), table, ntaps=ntaps, n_out=n_out,
+                          idx_layout=1, out_dtype=F32, x_dtype=dtype, w_dtype=dtype, b_dtype=dtype,
+                          nthreads=nthreads, blocked=blocked)
         return r(y)
 
     child, parent = o.subdivide(coords)
+    nc = child.shape[0]
     offs_p = batch_offsets(coords[:, 0])
     h = r(silu(r(group_norm_items(x, offs_p, groups, p["gn0_w"], p["gn0_b"]))))[parent]
     table = o.conv_table_slat(child)
-    h = conv(h, p["conv1_w"], p["conv1_b"], table, 27)
+    h = conv(h, p["conv1_w"], p["conv1_b"], table, 27, nc)
     offs_c = batch_offsets(child[:, 0])
     h = r(silu(r(group_norm_items(h, offs_c, groups, p["gn1_w"], p["gn1_b"]))))
-    h = conv(h, p["conv2_w"], p["conv2_b"], table, 27)
-    xs = x[parent]
+    out_rows = np.arange(nc) if rows is None else np.asarray(rows)
+    sub = np.ascontiguousarray(table.reshape(nc, 27)[out_rows]).reshape(-1)
+    h = conv(h, p["conv2_w"], p["conv2_b"], sub, 27, out_rows.shape[0])
+    xs = x[parent[out_rows]]
     if "skip_w" in p:
         co, ci = p["conv2_w"].shape[0], x.shape[1]
         w_eff = p["skip_w"].reshape(-1).reshape(ci, co).T.reshape(co, 1, ci)
         ident = np.arange(xs.shape[0], dtype=np.int32)
-        skip = conv(xs, w_eff, p["skip_b"], ident, 1)
+        skip = conv(xs, w_eff, p["skip_b"], ident, 1, xs.shape[0])
     else:
         skip = xs
     return child, r(h + skip)

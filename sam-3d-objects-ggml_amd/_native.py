@@ -89,6 +89,8 @@ def lib() -> ctypes.CDLL:
     L.sam3d_spconv_f16_forward.argtypes = [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64]
     L.sam3d_spconv_f16_forward.restype = None
     L.spc_q8_0_repack.argtypes = [_P, _P, _I64, _P, _P]
+    L.spc_conv_expand_q8_0_to.argtypes = [_P, _P, _I64, _I64, _I64, _INT, _P]
+    L.spc_convert.argtypes = [_P, _INT, _P, _INT, _P, _I64]
     L.spc_q8_0_quantize.argtypes = [_P, _P, _I64, _P]
     L.spc_q8_0_dequant.argtypes = [_P, _P, _I64, _INT, _P]
     L.spc_scatter_mean_workspace_bytes.restype = _SZ
@@ -406,25 +408,45 @@ def pack_weights(weight: torch.Tensor, w_scale: torch.Tensor | None = None, *,
     return PackedWeights(out, wdt, ntaps, cin, cout)
 
 
-def expand_q8_0(packed: PackedWeights, out: torch.Tensor | None = None) -> PackedWeights:
-    """Packed Q8_0 weights -> packed bf16 weights of bf16(f32(d) * q)
-    (spc_conv_expand_q8_0): a bf16 conv on them is bit-identical to the Q8_0
-    conv, and faster over many row tiles (each weight dequantised once
-    instead of once per tile).  `out` (uint8, the packed bf16 size) is
-    reused when given."""
+def expand_q8_0(packed: PackedWeights, out: torch.Tensor | None = None,
+                dtype: torch.dtype = torch.bfloat16) -> PackedWeights:
+    """Packed Q8_0 weights -> packed 16-bit weights (spc_conv_expand_q8_0_to):
+    bf16(f32(d) * q) for dtype bfloat16 -- a bf16 conv on them is
+    bit-identical to the Q8_0 conv, and faster over many row tiles (each
+    weight dequantised once instead of once per tile) -- or f16(f32(d) * q)
+    for float16, the reference's f16 GEMM operand.  `out` (uint8, the
+    packed 16-bit size) is reused when given."""
     if packed.w_dtype != Q8_0:
         raise ValueError("expand_q8_0 takes packed Q8_0 weights")
+    if dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError("expand_q8_0 expands to bfloat16 or float16")
     _need_gpu(packed.data, out)
     L = lib()
-    nbytes = L.spc_conv_packed_bytes(BF16, packed.ntaps, packed.cin, packed.cout)
+    dt = dtype_code(dtype)
+    nbytes = L.spc_conv_packed_bytes(dt, packed.ntaps, packed.cin, packed.cout)
     if out is None:
         out = torch.empty(nbytes, dtype=torch.uint8, device=packed.data.device)
     elif out.dtype != torch.uint8 or out.numel() < nbytes or not out.is_contiguous():
         raise ValueError(f"out must be a contiguous uint8 tensor of >= {nbytes} bytes")
-    st = L.spc_conv_expand_q8_0(_stream(out.device), _ptr(packed.data), packed.ntaps,
-                                packed.cin, packed.cout, _ptr(out))
-    _check("spc_conv_expand_q8_0", st)
-    return PackedWeights(out, BF16, packed.ntaps, packed.cin, packed.cout)
+    st = L.spc_conv_expand_q8_0_to(_stream(out.device), _ptr(packed.data), packed.ntaps,
+                                   packed.cin, packed.cout, dt, _ptr(out))
+    _check("spc_conv_expand_q8_0_to", st)
+    return PackedWeights(out, dt, packed.ntaps, packed.cin, packed.cout)
+
+
+def convert(x: torch.Tensor, dtype: torch.dtype, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Element conversion between float32 / float16 / bfloat16 (spc_convert,
+    round to nearest even)."""
+    _need_gpu(x, out)
+    x = x.contiguous()
+    if out is None:
+        out = torch.empty(x.shape, dtype=dtype, device=x.device)
+    elif out.dtype != dtype or out.shape != x.shape or not out.is_contiguous():
+        raise ValueError("out must be a contiguous tensor of x's shape and the target dtype")
+    st = lib().spc_convert(_stream(x.device), dtype_code(x.dtype), _ptr(x), dtype_code(dtype),
+                           _ptr(out), x.numel())
+    _check("spc_convert", st)
+    return out
 
 
 TILES_AUTO, TILES_WIDE, TILES_SMALL, TILES_TALL = 0, 1, 2, 3

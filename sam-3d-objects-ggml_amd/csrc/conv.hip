@@ -31,7 +31,7 @@ size_t packed_quant_bytes(int64_t ntaps, int64_t cin, int64_t cout) {
 struct WStride {
     int64_t co, o, ci;
 };
-WStride weight_strides(int layout, int64_t ntaps, int64_t cin, int64_t cout) {
+__host__ __device__ WStride weight_strides(int layout, int64_t ntaps, int64_t cin, int64_t cout) {
     if (layout == SPC_W_TCK) return {cin, cout * cin, 1};
     if (layout == SPC_W_TKC) return {1, cin * cout, cout};
     return {ntaps * cin, cin, 1};  // SPC_W_KRSC
@@ -115,6 +115,9 @@ __global__ void pack_scales_kernel(const uint16_t* __restrict__ d, float* __rest
 // the chunk), a bf16 panel two (one per k-step); the f32 scale of lane l
 // is that of output channel 32 c32 + l % 32.  One thread per panel lane:
 // 16 quant bytes and a scale in, 32 bytes out, all coalesced.
+// F16: the same panels of f16(f32(d) * q) (bf16 and f16 panels share the
+// packed layout).
+template <bool F16>
 __global__ void expand_q8_0_kernel(const u32x4* __restrict__ q, const float* __restrict__ sc,
                                    u32x4* __restrict__ out, int64_t panels, int ncol32,
                                    int cout) {
@@ -126,8 +129,34 @@ __global__ void expand_q8_0_kernel(const u32x4* __restrict__ q, const float* __r
     const int c32 = (int)(p - tk * ncol32);
     const float d = sc[tk * cout + c32 * 32 + (lane & 31)];
     const u32x4 w = q[id];
-    out[p * 128 + lane] = __builtin_bit_cast(u32x4, q8_dequant8(w.x, w.y, d));
-    out[p * 128 + 64 + lane] = __builtin_bit_cast(u32x4, q8_dequant8(w.z, w.w, d));
+    if constexpr (F16) {
+        out[p * 128 + lane] = __builtin_bit_cast(u32x4, q8_dequant8_f16(w.x, w.y, d));
+        out[p * 128 + 64 + lane] = __builtin_bit_cast(u32x4, q8_dequant8_f16(w.z, w.w, d));
+    } else {
+        out[p * 128 + lane] = __builtin_bit_cast(u32x4, q8_dequant8(w.x, w.y, d));
+        out[p * 128 + 64 + lane] = __builtin_bit_cast(u32x4, q8_dequant8(w.z, w.w, d));
+    }
+}
+
+// Element conversion between f32 / f16 / bf16 (round to nearest even), four
+// elements per thread.
+__device__ __forceinline__ float load_elem(const void* p, int dt, int64_t i) {
+    if (dt == SPC_F32) return static_cast<const float*>(p)[i];
+    const uint16_t b = static_cast<const uint16_t*>(p)[i];
+    return dt == SPC_F16 ? f16_bits_to_f32(b) : bf16_bits_to_f32(b);
+}
+__global__ void convert_kernel(const void* __restrict__ src, int sdt, void* __restrict__ dst,
+                               int ddt, int64_t n) {
+    const int64_t i0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int64_t i = i0 + k;
+        if (i >= n) return;
+        const float v = load_elem(src, sdt, i);
+        if (ddt == SPC_F32) static_cast<float*>(dst)[i] = v;
+        else if (ddt == SPC_F16) static_cast<uint16_t*>(dst)[i] = f32_to_f16_bits(v);
+        else static_cast<uint16_t*>(dst)[i] = f32_to_bf16_bits(v);
+    }
 }
 
 __global__ void q8_0_repack_kernel(const uint8_t* __restrict__ blocks, int64_t nblocks,
@@ -216,40 +245,30 @@ int device_cu_count() {
     return n;
 }
 
-// Packed f16 weights of the spconv bridge: the largest pack it holds is
-// 64 MiB (27 x 1024 x 1184 f16 weights; the SLAT IO convs need 27 x 1024 x
-// 1024).  One buffer per device, held until the process ends; bridge calls
-// on one device share it, so they must not overlap (one stream, as the
-// reference's bridge assumes).
-constexpr size_t kBridgePackBytes = (size_t)64 << 20;
-__device__ __attribute__((aligned(256))) uint8_t bridge_pack[kBridgePackBytes];
-
-// Device address of bridge_pack on the current device, looked up once per
-// device with that device current (the host-side symbol is a stand-in, not
-// a device address); null when the lookup fails.
-void* bridge_pack_addr() {
-    static std::atomic<void*> cache[64];
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-    void* p = cache[dev].load(std::memory_order_acquire);
-    if (p == nullptr) {
-        if (hipGetSymbolAddress(&p, HIP_SYMBOL(bridge_pack)) != hipSuccess || p == nullptr) {
-            (void)hipGetLastError();
-            return nullptr;
-        }
-        cache[dev].store(p, std::memory_order_release);
-    }
-    return p;
+__global__ void fill_i32_kernel(int32_t* p, int64_t n, int32_t v) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
 }
 
-// The bridge's self-refreshing tile plan, one per device: a plan buffer
-// for `n` tokens, a copy of the index table its tiles were built from and
-// one flag per (128 rows, tap).  Each call first flags the rows whose entries
-// differ from the copy (bridge_dirty_kernel); the conv runs flagged tiles
-// unplanned and writes their plan tiles and entries back, so repeated
-// calls over one index table (every conv of a coordinate set) skip the
-// tile setup.  Grown with hipMalloc when a call needs more rows, held until
-// the process ends; shared like bridge_pack.
+// The spconv bridge's device state, one per device, grown with hipMalloc
+// when a call needs more and held until the process ends (the bridge's
+// signature has no workspace):
+//   pack    the KRSC f16 weights packed into MFMA fragment order (every call)
+//   pad     channels that are multiples of 8 but not of 32: zero-padded
+//           copies of input, bias and output (widths rounded up to 32)
+//   plans   self-refreshing tile plans, four entries keyed by (tokens, tile
+//           geometry), least recently used replaced: a plan buffer for n
+//           tokens, a copy of the index table its tiles were built from and
+//           one flag per (128 rows, tap).  Each call first flags the rows
+//           whose entries differ from the copy (bridge_prep_kernel); the conv
+//           runs flagged tiles unplanned and writes their plan tiles and
+//           entries back, so repeated calls over one index table (every conv
+//           of a coordinate set) skip the tile setup, and calls that
+//           alternate between token counts (the fine and coarse levels of
+//           the SLAT IO blocks) keep one plan per level.
+// Bridge calls on one device share it, so calls on different streams of
+// one device must not overlap (one stream, as the reference's bridge
+// assumes).
 struct BridgePlan {
     int32_t* idx = nullptr;
     int32_t* dirty = nullptr;
@@ -258,27 +277,85 @@ struct BridgePlan {
     size_t plan_cap = 0;
     int64_t n = -1;
     int geometry = -1;  // the tile geometry whose plan section the entries describe
+    uint64_t used = 0;  // last use (LRU clock)
+};
+constexpr int kBridgePlans = 4;
+struct BridgeDev {
+    void* pack = nullptr;
+    size_t pack_cap = 0;
+    void* pad = nullptr;
+    size_t pad_cap = 0;
+    BridgePlan plans[kBridgePlans];
+    uint64_t clock = 0;
 };
 
-__global__ void fill_i32_kernel(int32_t* p, int64_t n, int32_t v) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) p[i] = v;
+std::mutex g_bridge_mu;
+BridgeDev g_bridge[64];
+
+// Grows a held device buffer to `need` bytes (the old contents are not
+// kept); false when the allocation fails.
+bool bridge_grow(void*& p, size_t& cap, size_t need) {
+    if (cap >= need) return true;
+    // hipFree waits for the work that may still read the old buffer
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    cap = 0;
+    if (hipMalloc(&p, need) != hipSuccess) {
+        p = nullptr;
+        (void)hipGetLastError();
+        return false;
+    }
+    cap = need;
+    return true;
 }
 
 // The bridge's per-call preparation in one launch: blocks [0, npack) pack
-// the KRSC f16 weights (one thread per panel word), the rest flag changed
-// index entries: dirty[27 f + o] = whether any offset-major entry (o, r) of
-// [27, n] with r in [128 f, 128 f + 128) differs from the cached copy.  A
-// flag block covers 256 rows, each thread one row across the 27 taps (all
-// 54 loads in flight at once).
+// the KRSC f16 weights (one thread per panel word, zeros for the padded
+// channels: input channels >= cin_real or output channels >= cout_real),
+// the rest flag changed index entries: dirty[27 f + o] = whether any
+// offset-major entry (o, r) of [27, n] with r in [128 f, 128 f + 128)
+// differs from the cached copy.  A flag block covers 256 rows, each thread
+// one row across the 27 taps (all 54 loads in flight at once).
 __global__ __launch_bounds__(256) void bridge_prep_kernel(
-    const uint8_t* __restrict__ w, u32x4* __restrict__ packed, int cin, int cout, WStride st,
-    int64_t npack, const int32_t* __restrict__ idx, const int32_t* __restrict__ cache, int64_t n,
-    int32_t* __restrict__ dirty) {
+    const uint8_t* __restrict__ w, u32x4* __restrict__ packed, int cin, int cout, int cin_real,
+    int cout_real, int64_t npack, const int32_t* __restrict__ idx,
+    const int32_t* __restrict__ cache, int64_t n, int32_t* __restrict__ dirty) {
     const int64_t b = blockIdx.x;
     const int t = threadIdx.x;
     if (b < npack) {
-        pack_word<__bf16, false>(w, packed, 27, cin, cout, st, b * 256 + t);
+        const int64_t id = b * 256 + t;
+        if (cin == cin_real && cout == cout_real) {
+            pack_word<__bf16, false>(w, packed, 27, cin, cout,
+                                     weight_strides(SPC_W_KRSC, 27, cin, cout), id);
+            return;
+        }
+        // padded panels: word id holds 8 consecutive input channels of one
+        // output channel (all real or all padding: both widths are
+        // multiples of 8)
+        using P = Panel<__bf16, false>;
+        const int kch = cin / P::KC;
+        const int ncol32 = cout / 32;
+        if (id >= (int64_t)27 * kch * ncol32 * P::NG * 64) return;
+        const int lane = (int)(id % 64);
+        const int64_t rest = id / 64;
+        const int g = (int)(rest % P::NG);
+        const int64_t panel = rest / P::NG;
+        const int c32 = (int)(panel % ncol32);
+        const int64_t tk = panel / ncol32;
+        const int kc = (int)(tk % kch);
+        const int o = (int)(tk / kch);
+        const int co = c32 * 32 + (lane & 31);
+        const int ci0 = kc * P::KC + g * P::KSUB + (lane >> 5) * P::EPL;
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (co < cout_real && ci0 < cin_real) {
+            const uint16_t* src = reinterpret_cast<const uint16_t*>(w) +
+                                  ((int64_t)co * 27 + o) * cin_real + ci0;
+            uint32_t h[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) h[e] = (uint32_t)src[2 * e] | ((uint32_t)src[2 * e + 1] << 16);
+            v = u32x4{h[0], h[1], h[2], h[3]};
+        }
+        packed[id] = v;
         return;
     }
     if (!cache) return;
@@ -304,41 +381,61 @@ __global__ __launch_bounds__(256) void bridge_prep_kernel(
     }
 }
 
-// The current device's plan cache sized for n tokens (27 taps) and reset
-// when n or the tile geometry changes (the copy then describes no plan
-// tile), or null when it cannot be had (the call then runs without a plan).
-BridgePlan* bridge_plan(hipStream_t s, int64_t n, int geometry) {
-    static std::mutex mu;
-    static BridgePlan cache[64];
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
-        (void)hipGetLastError();
-        return nullptr;
+// Row copies between widths (16-bit elements, both widths multiples of 8):
+// dst[r, c] = src[r, c] for c < min(cs, cd), zeros up to cd.  One thread
+// per 16-byte piece of a destination row.
+__global__ void bridge_copy_rows_kernel(const uint16_t* __restrict__ src, int64_t cs,
+                                        uint16_t* __restrict__ dst, int64_t cd, int64_t rows) {
+    const int64_t pr = cd / 8;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * pr) return;
+    const int64_t r = i / pr;
+    const int64_t c = (i - r * pr) * 8;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (c < cs) {
+        const uint16_t* p = src + r * cs + c;
+        uint32_t h[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) h[e] = (uint32_t)p[2 * e] | ((uint32_t)p[2 * e + 1] << 16);
+        v = u32x4{h[0], h[1], h[2], h[3]};
     }
-    std::lock_guard<std::mutex> lock(mu);
-    BridgePlan& bp = cache[dev];
-    if (bp.n == n && bp.geometry == geometry) return &bp;
+    uint32_t* q = reinterpret_cast<uint32_t*>(dst + r * cd + c);
+    q[0] = v.x;
+    q[1] = v.y;
+    q[2] = v.z;
+    q[3] = v.w;
+}
+
+// The plan cache entry for n tokens (27 taps) and the tile geometry, from
+// the device's four entries (the least recently used one replaced and
+// reset: its copy then describes no plan tile), or null when it cannot be
+// had (the call then runs without a plan).  Called with g_bridge_mu held.
+BridgePlan* bridge_plan(BridgeDev& bd, hipStream_t s, int64_t n, int geometry) {
+    BridgePlan* hit = nullptr;
+    BridgePlan* lru = &bd.plans[0];
+    for (BridgePlan& e : bd.plans) {
+        if (e.n == n && e.geometry == geometry) hit = &e;
+        if (e.used < lru->used) lru = &e;
+    }
+    ++bd.clock;
+    if (hit) {
+        hit->used = bd.clock;
+        return hit;
+    }
+    BridgePlan& bp = *lru;
+    bp.n = -1;
+    bp.geometry = -1;
+    bp.used = 0;
     const size_t need_idx = (size_t)(n + (n + 127) / 128) * 27 * sizeof(int32_t);
     const size_t need_plan = spc_conv_plan_bytes(n, 27);
     if (need_plan == 0) return nullptr;
-    if (bp.idx_cap < need_idx || bp.plan_cap < need_plan) {
-        // hipFree waits for the work that may still read the old buffers
-        if (bp.idx) (void)hipFree(bp.idx);
-        if (bp.plan) (void)hipFree(bp.plan);
-        bp = BridgePlan{};
-        void* pi = nullptr;
-        void* pp = nullptr;
-        if (hipMalloc(&pi, need_idx) != hipSuccess || hipMalloc(&pp, need_plan) != hipSuccess) {
-            if (pi) (void)hipFree(pi);
-            (void)hipGetLastError();
-            return nullptr;
-        }
-        bp.idx = static_cast<int32_t*>(pi);
-        bp.plan = pp;
-        bp.dirty = bp.idx + n * 27;
-        bp.idx_cap = need_idx;
-        bp.plan_cap = need_plan;
+    void* pi = bp.idx;
+    if (!bridge_grow(pi, bp.idx_cap, need_idx)) {
+        bp.idx = nullptr;
+        return nullptr;
     }
+    bp.idx = static_cast<int32_t*>(pi);
+    if (!bridge_grow(bp.plan, bp.plan_cap, need_plan)) return nullptr;
     // entries no index equals: every tile of the first call sets itself up
     const int64_t ne = n * 27;
     fill_i32_kernel<<<(unsigned)ceil_div(ne, 256), 256, 0, s>>>(bp.idx, ne, INT_MIN);
@@ -346,6 +443,7 @@ BridgePlan* bridge_plan(hipStream_t s, int64_t n, int geometry) {
     bp.dirty = bp.idx + n * 27;
     bp.n = n;
     bp.geometry = geometry;
+    bp.used = bd.clock;
     return &bp;
 }
 
@@ -451,20 +549,48 @@ int spc_conv_pack_weights(spc_stream_t stream, int w_dtype, int w_layout, const 
 
 int spc_conv_expand_q8_0(spc_stream_t stream, const void* packed_q8, int64_t ntaps, int64_t cin,
                          int64_t cout, void* packed_bf16) {
+    return spc_conv_expand_q8_0_to(stream, packed_q8, ntaps, cin, cout, SPC_BF16, packed_bf16);
+}
+
+int spc_conv_expand_q8_0_to(spc_stream_t stream, const void* packed_q8, int64_t ntaps,
+                            int64_t cin, int64_t cout, int out_dtype, void* packed_out) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int st = check_shape("spc_conv_expand_q8_0", ntaps, cin, cout, true);
     if (st != SPC_OK) return st;
-    if (!packed_q8 || !packed_bf16 || !aligned16(packed_q8) || !aligned16(packed_bf16)) {
-        set_last_error("spc_conv_expand_q8_0: null / misaligned pointer");
+    if (!packed_q8 || !packed_out || !aligned16(packed_q8) || !aligned16(packed_out) ||
+        (out_dtype != SPC_BF16 && out_dtype != SPC_F16)) {
+        set_last_error("spc_conv_expand_q8_0: null / misaligned pointer or out_dtype not "
+                       "SPC_BF16 / SPC_F16");
         return SPC_BAD_ARG;
     }
     const size_t qbytes = packed_quant_bytes<__bf16, true>(ntaps, cin, cout);
     const int64_t panels = (int64_t)qbytes / 1024;
     const float* sc =
         reinterpret_cast<const float*>(static_cast<const char*>(packed_q8) + align_up(qbytes, 256));
-    expand_q8_0_kernel<<<(unsigned)ceil_div(panels * 64, 256), 256, 0, s>>>(
-        static_cast<const u32x4*>(packed_q8), sc, static_cast<u32x4*>(packed_bf16), panels,
-        (int)(cout / 32), (int)cout);
+    const unsigned grid = (unsigned)ceil_div(panels * 64, 256);
+    if (out_dtype == SPC_F16)
+        expand_q8_0_kernel<true><<<grid, 256, 0, s>>>(static_cast<const u32x4*>(packed_q8), sc,
+                                                       static_cast<u32x4*>(packed_out), panels,
+                                                       (int)(cout / 32), (int)cout);
+    else
+        expand_q8_0_kernel<false><<<grid, 256, 0, s>>>(static_cast<const u32x4*>(packed_q8), sc,
+                                                        static_cast<u32x4*>(packed_out), panels,
+                                                        (int)(cout / 32), (int)cout);
+    SPC_HIP(hipGetLastError());
+    return SPC_OK;
+}
+
+int spc_convert(spc_stream_t stream, int src_dtype, const void* src, int dst_dtype, void* dst,
+                int64_t n) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    auto ok = [](int d) { return d == SPC_F32 || d == SPC_F16 || d == SPC_BF16; };
+    if (n < 0 || !ok(src_dtype) || !ok(dst_dtype) || (n > 0 && (!src || !dst))) {
+        set_last_error("spc_convert: bad arguments");
+        return SPC_BAD_ARG;
+    }
+    if (n == 0) return SPC_OK;
+    convert_kernel<<<(unsigned)ceil_div(ceil_div(n, 4), 256), 256, 0, s>>>(src, src_dtype, dst,
+                                                                          dst_dtype, n);
     SPC_HIP(hipGetLastError());
     return SPC_OK;
 }
@@ -767,53 +893,109 @@ void sam3d_spconv_f16_forward(spc_stream_t stream, const void* input, const void
     (void)mask;
     (void)mask_argsort;
     clear_last_error();  // spc_last_error() reports this call only
-    if (check_shape("sam3d_spconv_f16_forward", 27, channels, output_channels) != SPC_OK) return;
+    // channel widths in multiples of 8, as the reference's spconv iterators
+    // take them (ForwardDgradSparseIOIterator.h:58-61); widths that are not
+    // multiples of 32 run zero-padded to the next multiple of 32
+    if (channels <= 0 || output_channels <= 0 || channels % 8 != 0 || output_channels % 8 != 0 ||
+        channels > (1 << 16) || output_channels > (1 << 16) || tokens < 0 || tokens > INT32_MAX) {
+        set_last_error("sam3d_spconv_f16_forward: unsupported shape tokens=%lld channels=%lld "
+                       "output_channels=%lld (channel widths multiples of 8, at most 65536)",
+                       (long long)tokens, (long long)channels, (long long)output_channels);
+        return;
+    }
+    const int64_t cin = (channels + 31) / 32 * 32;
+    const int64_t cout = (output_channels + 31) / 32 * 32;
+    if (check_shape("sam3d_spconv_f16_forward", 27, cin, cout) != SPC_OK) return;
+    if (tokens == 0) return;
+    if (!input || !weight || !output || !indices || !aligned16(input) || !aligned16(output)) {
+        set_last_error("sam3d_spconv_f16_forward: null or misaligned (16 bytes) pointer");
+        return;
+    }
+    const bool padded = cin != channels || cout != output_channels;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        (void)hipGetLastError();
+        set_last_error("sam3d_spconv_f16_forward: no current device");
+        return;
+    }
+    std::lock_guard<std::mutex> lock(g_bridge_mu);
+    BridgeDev& bd = g_bridge[dev];
     // The weights arrive in KRSC order on every call (the ggml shim passes
     // its weight tensor).  Packed into the MFMA fragment order first, each
     // B operand is one contiguous 1 KB load instead of 32 strided 32-byte
     // pieces: one pack kernel (weight bytes read and written once) buys the
-    // packed conv.  Weights beyond the pack buffer run unpacked.
-    const size_t wbytes = spc_conv_packed_bytes(SPC_F16, 27, channels, output_channels);
-    void* pk = wbytes <= kBridgePackBytes ? bridge_pack_addr() : nullptr;
+    // packed conv.
+    const size_t wbytes = spc_conv_packed_bytes(SPC_F16, 27, cin, cout);
+    if (!bridge_grow(bd.pack, bd.pack_cap, wbytes)) {
+        set_last_error("sam3d_spconv_f16_forward: cannot allocate %zu bytes for the packed "
+                       "weights", wbytes);
+        return;
+    }
+    // padded widths: input, bias and output copies in one held buffer
+    const void* xin = input;
+    const void* bin = bias;
+    void* yout = output;
+    if (padded) {
+        const size_t xb = cin != channels ? align_up((size_t)tokens * cin * 2, 256) : 0;
+        const size_t yb = cout != output_channels ? align_up((size_t)tokens * cout * 2, 256) : 0;
+        const size_t bb = align_up((size_t)cout * 2, 256);
+        if (!bridge_grow(bd.pad, bd.pad_cap, xb + yb + bb)) {
+            set_last_error("sam3d_spconv_f16_forward: cannot allocate %zu bytes for the padded "
+                           "rows", xb + yb + bb);
+            return;
+        }
+        char* pb = static_cast<char*>(bd.pad);
+        uint16_t* bpad = reinterpret_cast<uint16_t*>(pb + xb + yb);
+        if (cin != channels) {
+            bridge_copy_rows_kernel<<<(unsigned)ceil_div(tokens * cin / 8, 256), 256, 0, s>>>(
+                static_cast<const uint16_t*>(input), channels, reinterpret_cast<uint16_t*>(pb), cin,
+                tokens);
+            xin = pb;
+        }
+        if (cout != output_channels) yout = pb + xb;
+        if (bias && cout != output_channels) {
+            bridge_copy_rows_kernel<<<1, 256, 0, s>>>(static_cast<const uint16_t*>(bias),
+                                                      output_channels, bpad, cout, 1);
+            bin = bpad;
+        }
+        if (hipGetLastError() != hipSuccess) {
+            set_last_error("sam3d_spconv_f16_forward: padding launch failed");
+            return;
+        }
+    }
     // The tile setup (the deduplicated gather of each tile) comes from the
-    // device's self-refreshing plan: built by the first call over an index
+    // device's self-refreshing plans: built by the first call over an index
     // table, reused by every later call over the same one.
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    const int geometry = pk ? spc_conv_tile_geometry(SPC_F16, SPC_F16, 27, tokens, channels,
-                                                     output_channels, 0, SPC_EPI_NONE)
-                            : SPC_TILES_WIDE;
-    BridgePlan* bp = tokens > 0 && tokens <= INT32_MAX && input && indices
-                         ? bridge_plan(s, tokens, geometry)
-                         : nullptr;
+    const int geometry = spc_conv_tile_geometry(SPC_F16, SPC_F16, 27, tokens, cin, cout, 0,
+                                                SPC_EPI_NONE);
+    BridgePlan* bp = bridge_plan(bd, s, tokens, geometry);
     const void* plan = bp ? bp->plan : nullptr;
     int32_t* cache = bp ? bp->idx : nullptr;
     const int32_t* dirty = bp ? bp->dirty : nullptr;
     // one launch packs the weights and flags the changed index entries
-    const int64_t npack = pk && weight ? (int64_t)(wbytes / 16 + 255) / 256 : 0;
+    const int64_t npack = (int64_t)(wbytes / 16 + 255) / 256;
     const int64_t nflag = bp ? (tokens + 255) / 256 : 0;
-    bool packed = false;
-    if (npack + nflag > 0) {
-        bridge_prep_kernel<<<(unsigned)(npack + nflag), 256, 0, s>>>(
-            static_cast<const uint8_t*>(weight), static_cast<u32x4*>(pk), (int)channels,
-            (int)output_channels, weight_strides(SPC_W_KRSC, 27, channels, output_channels), npack,
-            indices, cache, tokens, bp ? bp->dirty : nullptr);
-        if (hipGetLastError() != hipSuccess) {
-            set_last_error("sam3d_spconv_f16_forward: preparation launch failed");
-            return;
-        }
-        packed = npack > 0;
-    }
-    if (packed) {
-        conv_entry(stream, SPC_F16, input, SPC_F16, SPC_W_PACKED, pk, nullptr, bias, output,
-                   indices, SPC_IDX_OFFSET_MAJOR, nullptr, plan, 27, tokens, tokens, channels,
-                   output_channels, 0, 1, nullptr, cache, dirty);
+    bridge_prep_kernel<<<(unsigned)(npack + nflag), 256, 0, s>>>(
+        static_cast<const uint8_t*>(weight), static_cast<u32x4*>(bd.pack), (int)cin, (int)cout,
+        (int)channels, (int)output_channels, npack, indices, cache, tokens,
+        bp ? bp->dirty : nullptr);
+    if (hipGetLastError() != hipSuccess) {
+        set_last_error("sam3d_spconv_f16_forward: preparation launch failed");
         return;
     }
-    // unpacked: weights beyond the pack buffer (wide tiles, the geometry
-    // the cache was set up for)
-    conv_entry(stream, SPC_F16, input, SPC_F16, SPC_W_KRSC, weight, nullptr, bias, output,
-               indices, SPC_IDX_OFFSET_MAJOR, nullptr, plan, 27, tokens, tokens, channels,
-               output_channels, 0, 1, nullptr, cache, dirty);
+    if (conv_entry(stream, SPC_F16, xin, SPC_F16, SPC_W_PACKED, bd.pack, nullptr, bin, yout,
+                   indices, SPC_IDX_OFFSET_MAJOR, nullptr, plan, 27, tokens, tokens, cin, cout, 0,
+                   1, nullptr, cache, dirty) != SPC_OK)
+        return;
+    if (yout != output) {
+        // padded output width: the first output_channels columns
+        bridge_copy_rows_kernel<<<(unsigned)ceil_div(tokens * output_channels / 8, 256), 256, 0, s>>>(
+            static_cast<const uint16_t*>(yout), cout, static_cast<uint16_t*>(output), output_channels,
+            tokens);
+        if (hipGetLastError() != hipSuccess)
+            set_last_error("sam3d_spconv_f16_forward: output copy launch failed");
+    }
 }
 
 int spc_q8_0_repack(spc_stream_t stream, const uint8_t* blocks, int64_t nblocks, int8_t* qs,

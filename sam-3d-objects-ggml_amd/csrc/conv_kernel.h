@@ -193,6 +193,23 @@ __device__ __forceinline__ bf16x8 q8_dequant8(uint32_t lo, uint32_t hi, float d)
     return f;
 }
 
+// The same dequantisation rounded to f16: f16(f32(d) * q), the operand the
+// reference's Q8_0 convs feed their f16 GEMM (as_f16, SRC/slat_flow_graph.
+// cpp:24-27; as_f32 then the F16 weight view, SRC/mesh_decoder_graph.cpp:
+// 309-312).  d * q is exact in F32; one round-to-nearest-even to f16.
+__device__ __forceinline__ f16x8 q8_dequant8_f16(uint32_t lo, uint32_t hi, float d) {
+    lo ^= 0x80808080u;
+    hi ^= 0x80808080u;
+    const float nb = -128.0f * d;
+    f16x8 f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint32_t word = e < 4 ? lo : hi;
+        f[e] = (_Float16)__builtin_fmaf(d, (float)((word >> (8 * (e & 3))) & 0xffu), nb);
+    }
+    return f;
+}
+
 constexpr int kWinWords = 1024; // dedupe bitmap: 32768 source rows
 constexpr int kHashBits = 11;    // wider spans: LDS hash of the tile's source rows
 constexpr int kHashSlots = 1 << kHashBits;  // 64-bit slots: row | rank << 32
@@ -609,6 +626,15 @@ __global__ __launch_bounds__(512) void conv_plan_kernel(ConvArgs a, char* plan) 
 // need ~226 registers.
 template <typename GEO, int TN>
 constexpr int geo_blocks_per_cu() { return GEO::NBUF == 1 ? (TN >= 128 ? 2 : 3) : 1; }
+
+// Whether a tile of TN columns can run the LayerNorm -> modulation -> SiLU
+// epilogue: whole rows of at most 128 channels, and half the tile's rows in
+// F32 inside the A area.  launch_conv refuses the norm epilogue where this
+// is false, so no instantiation stores un-normalised rows.
+template <typename GEO, int TN>
+constexpr bool norm_epilogue_fits() {
+    return TN <= 128 && GEO::TM / 2 * (TN + 4) * 4 <= GEO::NBUF * GEO::STAGE * 16;
+}
 
 template <typename T, bool Q8, bool PACKED, int NTAPS, int TN, int WM, int WN, int PD, typename GEO>
 __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void conv_kernel(ConvArgs a) {
@@ -1315,7 +1341,7 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
     // take one row each (four channels per lane, four rows in flight per
     // lane group), with group-local shuffles for the mean and the biased
     // variance.
-    if constexpr (TN <= 128 && TM / 2 * (TN + 4) * 4 <= ABYTES) if (a.epi_mode == SPC_EPI_NORM_MOD_SILU) {
+    if constexpr (norm_epilogue_fits<GEO, TN>()) if (a.epi_mode == SPC_EPI_NORM_MOD_SILU) {
         constexpr int FP = TN + 4;           // f32 row pitch (16-byte multiple)
         constexpr int NPN = TM * FP * 4 <= ABYTES ? 1 : 2;  // passes
         constexpr int RPN = TM / NPN;        // tile rows per pass
@@ -1592,6 +1618,8 @@ hipError_t launch_conv(hipStream_t s, ConvArgs a) {
     a.col_major = a.tiles_n > 1 && wbytes > (2 << 20);
     const int64_t grid = a.tiles_per_xcd * 8 + (a.total_tiles - a.heavy_tiles);
     if (grid == 0) return hipSuccess;
+    if (a.epi_mode == SPC_EPI_NORM_MOD_SILU && !norm_epilogue_fits<GEO, TN>())
+        return hipErrorInvalidValue;  // the tile cannot hold the epilogue's rows
     // the plan buffer holds the wide plans, then the small ones
     if (a.plan && !GEO::WIDE_PLAN)
         a.plan = static_cast<const char*>(a.plan) + plan_wide_bytes(a.n_out, NTAPS);
@@ -1655,9 +1683,9 @@ hipError_t dispatch_small(hipStream_t s, const ConvArgs& a) {
 //     beyond the wide stage: 29.8 -> 11.6 us for 128 -> 128 over 62,710
 //     fine rows);
 //   - one or two channel chunks per tile (C_in <= 64 in 16-bit, <= 32 in
-//     f32), where a wide tile is mostly setup and staging latency (the
-//     mesh levels: 31.8 -> 23.3 us at 128^3 C=64, 50.8 -> 38.7 us at 256^3
-//     C=32);
+//     f32) into at most 64 output channels, where a wide tile is mostly
+//     setup and staging latency (the mesh levels: 31.8 -> 23.3 us at 128^3
+//     C=64, 50.8 -> 38.7 us at 256^3 C=32);
 //   - 128-column tiles that need more than one round of the CUs, so the
 //     workgroups sharing a CU drift apart (SubM 1024 -> 1024 over 11,774
 //     rows: 627 -> 572 us; 128 -> 1024: 105 -> 89 us).
@@ -1678,7 +1706,10 @@ bool use_small_tiles(const ConvArgs& a) {
         if (a.class_rows > 0) return false;
         if (NTAPS == 8) return true;
         const int64_t kch = (int64_t)a.cin * (int64_t)sizeof(T) / 64;
-        if (kch <= 2) return true;
+        // short rows into narrow outputs only: with 128 output columns the
+        // wide tiles' double-buffered stage wins (C_in 64 -> C_out 128 over
+        // 62,710 rows: 53.7 us small, 29.8 us wide; C_in 32: 29.4 / 19.6 us)
+        if (kch <= 2) return a.cout <= 64;
         const int64_t tiles_m = ceil_div(a.n_out, GeoWide::TM);
         return a.cout % 128 == 0 && tiles_m * (a.cout / 128) > a.num_cu;
     }

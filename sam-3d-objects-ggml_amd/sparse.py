@@ -472,7 +472,8 @@ class _ConvParams(nn.Module):
 # Q8_0 convs over at least this many output rows expand the packed quants
 # to packed bf16 once per forward (one HBM pass over the weights) and run
 # the bf16 kernel; smaller ones dequantise in registers, once per row tile.
-# Both give the same bits.
+# Both give the same bits.  (With q8_operands = "f16", the default, bf16
+# features take the f16-operand path instead, at every size.)
 Q8_EXPAND_MIN_ROWS = 2048
 
 
@@ -486,6 +487,14 @@ class _ConvCore:
         self._packed = None
         self._packed_key = None
         self._q8 = None            # (blocks uint8 tensor, layout) or None
+        # Q8_0 weights under bf16 features: "f16" runs the reference's GEMM
+        # operands -- features cast to f16 (exact inside f16's range) and
+        # f16(f32(d) * q) weights (as_f16, SRC/slat_flow_graph.cpp:24-27) --
+        # through the f16 kernel, the output cast back to bf16; "bf16" feeds
+        # bf16(f32(d) * q) to the bf16 kernel (no feature casts, weights
+        # rounded to 8 significant bits instead of 11).  Fused epilogues
+        # always take "bf16", whose rounding steps they are defined in.
+        self.q8_operands = "f16"
 
     # ---- Q8_0 -------------------------------------------------------------
     def load_q8_0(self, blocks: torch.Tensor, layout: str = "slat") -> None:
@@ -582,6 +591,19 @@ class _ConvCore:
             if cin_p != c.in_channels:
                 x = torch.nn.functional.pad(x, (0, cin_p - c.in_channels))
             w = self._weight_operand(x.dtype, x.device)
+            if (w.w_dtype == nat.Q8_0 and self.q8_operands == "f16" and residual is None
+                    and norm_mod is None):
+                # the reference's operands: f16 features, f16(f32(d) * q)
+                # weights (the per-forward dequant cast before the GEMM,
+                # SRC/slat_flow_graph.cpp:24-27, as one HBM pass), f16 conv
+                w16 = nat.expand_q8_0(w, dtype=torch.float16)
+                y16 = nat.sparse_conv(nat.convert(x, torch.float16), w16,
+                                      self._bias_operand(torch.float16, x.device), idx,
+                                      ntaps=self._ntaps, n_out=n_out, plan=plan)
+                y = nat.convert(y16, x.dtype)
+                if y.shape[1] != c.out_channels:
+                    y = y[:, : c.out_channels].contiguous()
+                return y
             if w.w_dtype == nat.Q8_0 and n_out >= Q8_EXPAND_MIN_ROWS:
                 # the per-forward dequant cast before the GEMM
                 # (SRC/slat_flow_graph.cpp:24-27) as one HBM pass

@@ -478,3 +478,68 @@ def test_subdivide_block_192_channels(spc, orc, dev):
         want = blk.out_layers[3](h) + blk.skip_connection(xs)
     assert torch.equal(y27.feats, want.feats)
     assert max_rel(from_dev(ym.feats), from_dev(y27.feats)) <= 1e-2
+
+
+@pytest.mark.parametrize("case", ["768to192", "192to96"])
+def test_subdivide_block_decoder_widths(spc, orc, dev, case):
+    """The mesh decoder's own SparseSubdivideBlock3d widths against the
+    oracle's block (decoder_mesh.py:69-83; SRC/mesh_decoder_graph.cpp:
+    399-437): 768 -> 192 from the 64^3 sphere shell's 21,766 voxels to their
+    174,128 children (every output row), and 192 -> 96 from those 174,128
+    voxels to their 1,393,024 children (20,000 sampled output rows; the
+    oracle's conv1 and both GroupNorms still run over every child).  Both
+    conv1 forms: merged taps (the default, summed weights rounded once to
+    bf16) and the reference's 27 taps."""
+    import oracle
+    import torch
+    from helpers import oracle_threads
+
+    blocks, sp = spc.blocks, spc.sparse
+    cin, cout, res = {"768to192": (768, 192, 64), "192to96": (192, 96, 128)}[case]
+    coords = spc.workloads.sphere_shell()
+    if res == 128:
+        coords, _ = orc.subdivide(coords)
+    n = coords.shape[0]
+    _case(f"SparseSubdivideBlock3d bf16 decoder widths {cin}->{cout}, {n} parents -> {8 * n} "
+          "children")
+    torch.manual_seed(cin + cout)
+    blk = blocks.SparseSubdivideBlock3d(cin, res, cout).to(dev)
+    with torch.no_grad():
+        for prm in blk.out_layers[3].parameters():  # the reference zero-initialises it
+            prm.normal_(0, 0.02)
+        for gn in (blk.act_layers[0], blk.out_layers[1]):
+            gn.weight.normal_(1, 0.1)
+            gn.bias.normal_(0, 0.1)
+    blk = blk.to(torch.bfloat16)
+    blk.act_layers[0].float()
+    blk.out_layers[1].float()
+    x = spc.workloads.normal((n, cin), 1.0, seed=cin + 7)
+    xt = sp.SparseTensor(_dev_feats(orc, x, "bf16", dev), torch.from_numpy(coords).to(dev))
+    f = lambda t: t.detach().float().cpu().numpy()  # noqa: E731
+    p = {"gn0_w": f(blk.act_layers[0].weight), "gn0_b": f(blk.act_layers[0].bias),
+         "conv1_w": f(blk.out_layers[0].conv.weight).reshape(cout, 27, cin),
+         "conv1_b": f(blk.out_layers[0].conv.bias),
+         "gn1_w": f(blk.out_layers[1].weight), "gn1_b": f(blk.out_layers[1].bias),
+         "conv2_w": f(blk.out_layers[3].conv.weight).reshape(cout, 27, cout),
+         "conv2_b": f(blk.out_layers[3].conv.bias),
+         "skip_w": f(blk.skip_connection.conv.weight), "skip_b": f(blk.skip_connection.conv.bias)}
+    rows = None
+    if case == "192to96":
+        rows = np.sort(np.random.default_rng(97).choice(8 * n, 20000, replace=False))
+    child, ref = oracle.subdivide_block(orc, oracle.round_to(orc, x, oracle.BF16), coords, p, 32,
+                                        oracle.BF16, nthreads=oracle_threads(), blocked=True,
+                                        rows=rows)
+    for merged in (True, False):
+        blk.merged_taps = merged
+        with torch.no_grad():
+            y = blk(xt)
+        torch.cuda.synchronize()
+        got = from_dev(y.feats)
+        if rows is not None:
+            got = got[rows]
+        mr = max_rel(got, ref)
+        print(f"[parity] SparseSubdivideBlock3d {cin}->{cout} merged_taps={merged}: "
+              f"rows={ref.shape[0]} max_rel={mr:.3e}", flush=True)
+        assert np.array_equal(y.coords.cpu().numpy(), child)
+        assert mr <= MAXREL, (merged, mr)
+    blk.merged_taps = True

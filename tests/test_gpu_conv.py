@@ -179,9 +179,9 @@ def test_f16_spconv_bridge(spc, orc, dev):
     b = wl.normal((128,), 0.01, seed=44).astype(np.float16)
     m = nat.map_build(torch.from_numpy(coords).to(dev))
     xd, wd, bd = (torch.from_numpy(a).to(dev) for a in (x, w, b))
-    # a failing call (cin 48 is not a multiple of 32): reported, output untouched
+    # a failing call (cin 44 is not a multiple of 8): reported, output untouched
     bad_out = torch.full((n, 128), 7.0, dtype=torch.float16, device=dev)
-    _, bad = nat.spconv_f16_forward(xd[:, :48].contiguous(), wd[:, :, :48].contiguous(), bd,
+    _, bad = nat.spconv_f16_forward(xd[:, :44].contiguous(), wd[:, :, :44].contiguous(), bd,
                                     m.offset_major, m.mask_sorted, m.argsort, out=bad_out)
     torch.cuda.synchronize()
     assert "unsupported shape" in bad and bool((bad_out == 7.0).all())
@@ -253,6 +253,65 @@ def test_f16_spconv_bridge(spc, orc, dev):
         assert msg == "" and torch.equal(yt, yt_krsc)
 
 
+def test_f16_spconv_bridge_widths_of_8(spc, orc, dev):
+    """sam3d_spconv_f16_forward at channel widths that are multiples of 8 but
+    not of 32 (the reference's spconv iterators take vectors of 8 channels,
+    ForwardDgradSparseIOIterator.h:58-61): zero-padded to 32 inside the
+    bridge, checked against the oracle at the caller's widths and bit for
+    bit against the conv of explicitly zero-padded operands."""
+    import oracle
+    import torch
+
+    nat = spc._native
+    wl = spc.workloads
+    coords = wl.random_voxels(3000, 22, batches=2, seed=51)
+    n = coords.shape[0]
+    m = nat.map_build(torch.from_numpy(coords).to(dev))
+    om = m.offset_major.cpu().numpy()
+    for cin, cout in ((48, 40), (40, 64), (64, 56), (8, 8), (200, 136)):
+        _case(f"f16 bridge widths {cin}->{cout} N={n}")
+        x = wl.normal((n, cin), 1.0, seed=cin).astype(np.float16)
+        w = wl.normal((cout, 27, cin), 0.02, seed=cin + cout).astype(np.float16)
+        b = wl.normal((cout,), 0.01, seed=cout).astype(np.float16)
+        xd, wd, bd = (torch.from_numpy(a).to(dev) for a in (x, w, b))
+        y, msg = nat.spconv_f16_forward(xd, wd, bd, m.offset_major, m.mask_sorted, m.argsort)
+        torch.cuda.synchronize()
+        assert msg == "", msg
+        assert y.shape == (n, cout)
+        ref = orc.sparse_conv(x, w, b, om, ntaps=27, n_out=n, idx_layout=0, out_dtype=oracle.F32)
+        check_16bit(f"f16 bridge {cin}->{cout}", y.float().cpu().numpy(), ref)
+        # the same conv over operands padded to multiples of 32 by hand
+        cp, cq = (cin + 31) // 32 * 32, (cout + 31) // 32 * 32
+        xp = torch.zeros(n, cp, dtype=torch.float16, device=dev)
+        xp[:, :cin] = xd
+        wp = torch.zeros(cq, 27, cp, dtype=torch.float16, device=dev)
+        wp[:cout, :, :cin] = wd
+        bp = torch.zeros(cq, dtype=torch.float16, device=dev)
+        bp[:cout] = bd
+        yp = nat.sparse_conv(xp, wp, bp, m.offset_major, ntaps=27, n_out=n,
+                             idx_layout=nat.IDX_OFFSET_MAJOR)
+        torch.cuda.synchronize()
+        assert torch.equal(y, yp[:, :cout])
+    # the plan cache keeps one entry per token count: calls alternating
+    # between two coordinate sets stay equal to unplanned launches
+    c2 = wl.random_voxels(1800, 18, batches=1, seed=52)
+    m2 = nat.map_build(torch.from_numpy(c2).to(dev))
+    n2 = c2.shape[0]
+    x1 = torch.from_numpy(wl.normal((n, 64), 1.0, seed=53).astype(np.float16)).to(dev)
+    x2 = torch.from_numpy(wl.normal((n2, 64), 1.0, seed=54).astype(np.float16)).to(dev)
+    w = torch.from_numpy(wl.normal((64, 27, 64), 0.02, seed=55).astype(np.float16)).to(dev)
+    b = torch.from_numpy(wl.normal((64,), 0.01, seed=56).astype(np.float16)).to(dev)
+    r1 = nat.sparse_conv(x1, w, b, m.offset_major, ntaps=27, n_out=n, idx_layout=nat.IDX_OFFSET_MAJOR)
+    r2 = nat.sparse_conv(x2, w, b, m2.offset_major, ntaps=27, n_out=n2, idx_layout=nat.IDX_OFFSET_MAJOR)
+    for k in range(3):
+        _case(f"f16 bridge alternating token counts call {k}")
+        y1, msg1 = nat.spconv_f16_forward(x1, w, b, m.offset_major, m.mask_sorted, m.argsort)
+        y2, msg2 = nat.spconv_f16_forward(x2, w, b, m2.offset_major, m2.mask_sorted, m2.argsort)
+        torch.cuda.synchronize()
+        assert msg1 == "" and msg2 == ""
+        assert torch.equal(y1, r1) and torch.equal(y2, r2)
+
+
 def test_q8_0_config5_sphere(spc, orc, dev):
     """Sphere shell, Q8_0 weights (C=768) dequantised inside the GEMM,
     against the reference's f16(f32(d)*q) GEMM input."""
@@ -299,6 +358,28 @@ def test_q8_0_config5_sphere(spc, orc, dev):
     ref_b = orc.sparse_conv(x, orc.q8_0_dequant(blocks, oracle.BF16), b, tm,
                             w_dtype=oracle.BF16, **kw)
     check_16bit("config5 Q8_0 C=768 vs bf16(d*q) weights", got, ref_b)
+    # the reference's operands: features cast to f16 (exact but for the
+    # few below f16's full-precision range), the expansion to f16(f32(d) *
+    # q), the f16 conv, the output cast back to bf16 -- per element within
+    # one rounding of the f16(d*q) reference
+    px16 = nat.expand_q8_0(pw, dtype=torch.float16)
+    wq_h = orc.q8_0_dequant(blocks, oracle.F16).reshape(c, 27, c)
+    assert torch.equal(px16.data, nat.pack_weights(torch.from_numpy(wq_h).to(dev)).data)
+    xd = to_dev_bf16(x, dev)
+    x16 = nat.convert(xd, torch.float16)
+    inexact = x16.float() != xd.float()
+    assert bool((xd.float().abs()[inexact] < 2.0 ** -17).all())
+    print(f"[parity] bf16 -> f16 feature cast: {int(inexact.sum())} of {xd.numel()} values "
+          "below 2^-17 rounded", flush=True)
+    y16 = nat.sparse_conv(x16, px16, nat.convert(to_dev_bf16(b, dev), torch.float16),
+                          m.token_major, ntaps=27, n_out=n)
+    yb16 = nat.convert(y16, torch.bfloat16)
+    torch.cuda.synchronize()
+    check_16bit("config5 Q8_0 C=768 f16 operands vs f16(d*q) weights", from_dev(y16), ref16)
+    # the cast back to bf16: round to nearest even, as torch casts
+    assert torch.equal(yb16, y16.to(torch.bfloat16))
+    check_16bit("config5 Q8_0 C=768 f16 operands, bf16 output", from_dev(yb16), ref16,
+                roundings=2)
 
 
 @pytest.mark.parametrize("ntaps,cin,cout,layout", [(27, 32, 32, "krsc"), (8, 64, 160, "krsc"),

@@ -5,7 +5,7 @@ dense torch brute force.  Bars: maps / coords / scatter-mean bit-exact; f32
 import numpy as np
 import pytest
 
-from helpers import bf16_bits, from_dev, max_rel
+from helpers import bf16_bits, check_16bit, from_dev, max_rel
 
 pytestmark = pytest.mark.gpu
 
@@ -208,9 +208,17 @@ def test_q8_0_module(spc, orc, dev):
     ref = orc.sparse_conv(xb, wq, bb, orc.conv_table_slat(coords), ntaps=27, n_out=n,
                           idx_layout=1, out_dtype=oracle.F32, x_dtype=oracle.BF16,
                           w_dtype=oracle.F16, b_dtype=oracle.BF16)
-    assert max_rel(from_dev(y.feats), ref) <= MAXREL
-    # in-register dequant (n below the expansion threshold) and the
-    # per-forward expansion to packed bf16 give the same bits
+    # the default f16 operands are the reference's GEMM operands: within
+    # the output's two roundings (f16, then bf16) of the oracle per element
+    assert conv.q8_operands == "f16"
+    check_16bit("SparseConv3d Q8_0 f16 operands", from_dev(y.feats), ref, roundings=2)
+    # bf16 operands: in-register dequant (n below the expansion threshold)
+    # and the per-forward expansion to packed bf16 give the same bits, the
+    # 2e-2 bar against the reference's operands
+    conv.q8_operands = "bf16"
+    with torch.no_grad():
+        yb = conv(xt.replace(xt.feats))
+    assert max_rel(from_dev(yb.feats), ref) <= MAXREL
     assert n < sp.Q8_EXPAND_MIN_ROWS
     saved = sp.Q8_EXPAND_MIN_ROWS
     sp.Q8_EXPAND_MIN_ROWS = 0
@@ -219,7 +227,8 @@ def test_q8_0_module(spc, orc, dev):
             yx = conv(xt.replace(xt.feats))
     finally:
         sp.Q8_EXPAND_MIN_ROWS = saved
-    assert torch.equal(yx.feats, y.feats)
+    assert torch.equal(yx.feats, yb.feats)
+    conv.q8_operands = "f16"
     # the mesh GGUF layout of the same quants gives the identical result
     conv_m = sp.SparseConv3d(64, 64, 3).to(dev)
     conv_m.load_state_dict(conv.state_dict())

@@ -158,3 +158,33 @@ def test_io_res_block_sampling_closed_forms(orc, spc):
     want2 = oracle.res_block(orc, xu[inv], orc.conv_table_slat(fine), p, scale, shift,
                              fine[:, 0].astype(np.int64), oracle.F32)
     assert np.array_equal(got2, want2)
+
+
+def test_subdivide_block_row_sampling_and_blocked_conv(orc, spc):
+    """oracle.subdivide_block's `rows` option returns exactly those rows of
+    the whole block, and its threaded, vectorised convs give the scalar
+    loop's values -- so the large-width GPU checks that sample rows with the
+    fast convs compare against the same block."""
+    import oracle
+
+    co = spc.workloads.random_voxels(300, 10, batches=2, seed=3)
+    n = co.shape[0]
+    rng = np.random.default_rng(0)
+    cin, cout = 64, 32
+
+    def nrm(mu, sd, shape):
+        return rng.normal(mu, sd, shape).astype(np.float32)
+
+    p = {"gn0_w": nrm(1, .1, cin), "gn0_b": nrm(0, .1, cin),
+         "conv1_w": nrm(0, .02, (cout, 27, cin)), "conv1_b": nrm(0, .01, cout),
+         "gn1_w": nrm(1, .1, cout), "gn1_b": nrm(0, .1, cout),
+         "conv2_w": nrm(0, .02, (cout, 27, cout)), "conv2_b": nrm(0, .01, cout),
+         "skip_w": nrm(0, .02, (cout, 1, 1, 1, cin)), "skip_b": nrm(0, .01, cout)}
+    x = oracle.round_to(orc, nrm(0, 1, (n, cin)), oracle.BF16)
+    c1, full = oracle.subdivide_block(orc, x, co, p, 32, oracle.BF16)
+    rows = np.sort(rng.choice(8 * n, 100, replace=False))
+    c2, part = oracle.subdivide_block(orc, x, co, p, 32, oracle.BF16, nthreads=4, blocked=True,
+                                      rows=rows)
+    assert np.array_equal(c1, c2)
+    assert np.array_equal(full[rows], part)
+    assert full.shape == (8 * n, cout)
