@@ -398,6 +398,11 @@ def main():
             raise RuntimeError("dense and hash map builds differ")
         map_ms, _ = time_gpu(lambda: nat.map_build(c_dev, sync=False, workspace=wsd, dense=ext),
                              50, 5)
+    # the token-major table alone (no spconv mask / argsort tables): what the
+    # sparse module builds for its convs
+    map_token_ms, _ = time_gpu(lambda: nat.map_build(c_dev, sync=False, outputs="token",
+                                                     workspace=wsd if ext is not None else ws,
+                                                     dense=ext), 50, 5)
     tm_host = m.token_major.cpu().numpy()
     pairs = int((tm_host < n).sum())
     map_bytes = 16 * n + 108 * n + 8 * n
@@ -484,6 +489,7 @@ def main():
             "tflops": tflops, "pct_peak": 100.0 * tflops / peak,
             "dense_equiv_tflops": 2.0 * 27 * n * cin * cout / t / 1e12,
             "wall_s": wall, "map_build_ms": map_ms, "map_build_hash_ms": map_hash_ms,
+            "map_build_token_only_ms": map_token_ms,
             "map_build_kind": "dense grid" if ext is not None else "hash table",
             "map_build_gbs": map_bytes / (map_ms / 1e3) / 1e9,
             "conv_plan_ms": plan_ms,

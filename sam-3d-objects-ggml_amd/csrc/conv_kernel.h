@@ -210,12 +210,20 @@ __device__ __forceinline__ f16x8 q8_dequant8_f16(uint32_t lo, uint32_t hi, float
     return f;
 }
 
-constexpr int kWinWords = 1024; // dedupe bitmap: 32768 source rows
+constexpr int kWinWords = 1024;  // dedupe bitmap: 32768 source rows
+// Tiles whose sources span more take a bitmap over 65536 rows, and only
+// tiles beyond that the LDS hash: the sources of a 256-row tile of the
+// 1,393,024-row 256^3 subdivided shell (children in parent-major order)
+// span up to 64,532 rows, and 5,273 of its 5,442 tiles exceed 32768 (that
+// level's tile plan: 314 us through the hash, 215 us with a 65536-row
+// bitmap for every tile -- which costs the tiles that fit 32768 rows 14 ->
+// 16 us a plan, so the window is chosen per tile from the span).
+constexpr int kWinWordsWide = 2048;
 constexpr int kHashBits = 11;    // wider spans: LDS hash of the tile's source rows
 constexpr int kHashSlots = 1 << kHashBits;  // 64-bit slots: row | rank << 32
 constexpr int kSortCap = 1024;   // distinct rows collected after hashing (> any stage's UMAX)
-constexpr int kSetupScratchWords = 2 * kWinWords > 2 * kHashSlots + 2 * kSortCap
-                                       ? 2 * kWinWords
+constexpr int kSetupScratchWords = 2 * kWinWordsWide > 2 * kHashSlots + 2 * kSortCap
+                                       ? 2 * kWinWordsWide
                                        : 2 * kHashSlots + 2 * kSortCap;
 constexpr int kSegs = 4;        // 16-byte segments per staged 64-byte row chunk
 
@@ -315,14 +323,14 @@ constexpr int32_t kPlanMagic = 0x314e4c50;  // header word 3 of every built plan
 
 // Shared-memory arrays of one tile's setup.
 struct TileLds {
-    uint32_t* scratch;  // 2 * kWinWords words: dedupe bitmap + word ranks
+    uint32_t* scratch;  // kSetupScratchWords words: dedupe bitmap + word ranks, or the hash
     uint16_t* sidx;     // (NTAPS + 1) x TM slot keys; row NTAPS = the zero slot
     uint32_t* tlw;      // kTapWords
     int32_t* urow;      // UMAX source rows of the union slots
     int32_t* srow;      // TM output rows of the tile rows
     int32_t* wsum;      // one per wave
-    int32_t* misc;      // [0] tap mask [1] min source row [2] wide span [3] U [4] fast
-                        // [5] distinct rows (hash path)
+    int32_t* misc;      // [0] tap mask [1] min source row [2] unused [3] U [4] fast
+                        // [5] distinct rows (hash path) [6] max source row
 };
 
 // Tile setup: the tile's NTAPS x 256 neighbour indices are loaded
@@ -330,7 +338,8 @@ struct TileLds {
 // of the valid taps is formed (taps no row uses are skipped -- the per-tile
 // offset set of the reference's spconv kernel, cpp_ggml/third_party/
 // sam3d-spconv/src/.../ConvKernel_conv_kernel.cu:62-80); the referenced
-// source rows are deduplicated with a bitmap over a 32768-row window: a
+// source rows are deduplicated with a bitmap over a 32768-row window (then a
+// 65536-row one, then an LDS hash, for tiles whose sources span more): a
 // spatially coherent tile references ~3.2 x 256 distinct rows instead of
 // ~21 x 256, and ranks by popcount number them in ascending row order.
 // Ends with a barrier; results in L (misc[0], misc[3], misc[4]).
@@ -341,19 +350,18 @@ __device__ __forceinline__ void tile_setup(const ConvArgs& a, int64_t r0, const 
     constexpr int NW = NT / 64;
     constexpr int NQ = NTAPS * TM;
     constexpr int EPT = (NQ + NT - 1) / NT;
-    constexpr int WPT = kWinWords / NT;
-    static_assert(kWinWords % NT == 0, "setup geometry");
+    static_assert(kWinWords % NT == 0 && kWinWordsWide % NT == 0, "setup geometry");
     static_assert((NTAPS + PD - 1) / PD < kTapWords, "tap words");
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     uint32_t* bm = L.scratch;
-    int32_t* wbase = reinterpret_cast<int32_t*>(L.scratch) + kWinWords;
 
     if (tid == 0) {
         L.misc[0] = 0;
         L.misc[1] = INT_MAX;
         L.misc[2] = 0;
+        L.misc[6] = INT_MIN;
     }
     for (int r = tid; r < TM; r += NT) {
         const int64_t rr = r0 + r;
@@ -362,7 +370,7 @@ __device__ __forceinline__ void tile_setup(const ConvArgs& a, int64_t r0, const 
         if (t >= a.n_out) t = -1;  // a bad permutation entry writes nothing
         L.srow[r] = t;
     }
-    for (int i = tid; i < kWinWords; i += NT) bm[i] = 0u;
+    for (int i = tid; i < kWinWordsWide; i += NT) bm[i] = 0u;  // either window
     lds_barrier();
 
     const bool contiguous = a.idx_layout == SPC_IDX_TOKEN_MAJOR && a.row_perm == nullptr;
@@ -389,41 +397,47 @@ __device__ __forceinline__ void tile_setup(const ConvArgs& a, int64_t r0, const 
         ent[k] = src;
     }
     uint32_t my_mask = 0;
-    int32_t my_min = INT_MAX;
+    int32_t my_min = INT_MAX, my_max = INT_MIN;
 #pragma unroll
     for (int k = 0; k < EPT; ++k) {
         const int e = tid + k * NT;
         if (ent[k] >= 0) {
             my_mask |= 1u << (e % NTAPS);
             my_min = min(my_min, ent[k]);
+            my_max = max(my_max, ent[k]);
         }
     }
     for (int off = 32; off > 0; off >>= 1) {
         my_mask |= __shfl_xor(my_mask, off);
         my_min = min(my_min, __shfl_xor(my_min, off));
+        my_max = max(my_max, __shfl_xor(my_max, off));
     }
     if (lane == 0) {
         if (my_mask) atomicOr(reinterpret_cast<uint32_t*>(&L.misc[0]), my_mask);
         atomicMin(&L.misc[1], my_min);
+        atomicMax(&L.misc[6], my_max);
     }
     lds_barrier();
 
-    // ---- dedupe: bitmap over [lo, lo + 32768) ----
+    // ---- dedupe: a bitmap over [lo, lo + 32768), or [lo, lo + 65536) when
+    // the sources span more, or the LDS hash beyond that ----
     const int32_t lo = L.misc[1];
-    bool fail = false;
+    const int64_t span = (int64_t)L.misc[6] - lo + 1;  // <= 0 without sources
+    const bool wide = span > kWinWords * 32;
+    const bool hashed = span > kWinWordsWide * 32;
+    if (!hashed) {
 #pragma unroll
-    for (int k = 0; k < EPT; ++k) {
-        if (ent[k] >= 0) {
-            const int32_t off = ent[k] - lo;
-            if (off >= kWinWords * 32) fail = true;
-            else atomicOr(&bm[off >> 5], 1u << (off & 31));
+        for (int k = 0; k < EPT; ++k) {
+            if (ent[k] >= 0) {
+                const int32_t off = ent[k] - lo;  // < span by the reduction
+                atomicOr(&bm[off >> 5], 1u << (off & 31));
+            }
         }
+        lds_barrier();
     }
-    if (fail) L.misc[2] = 1;
-    lds_barrier();
     int U;
     bool fast;
-    if (L.misc[2]) {
+    if (hashed) {
         // ---- the sources span more than the window (large tensors whose
         // neighbour slabs lie far apart in row order): insert them into an
         // LDS hash table (64-bit slots, linear probing), collect the distinct
@@ -508,7 +522,11 @@ __device__ __forceinline__ void tile_setup(const ConvArgs& a, int64_t r0, const 
             for (int r = tid; r < TM; r += NT) L.sidx[NTAPS * TM + r] = (uint16_t)GEO::key(U);
         }
     } else {
-        // ranks: thread tid owns words WPT*tid .. WPT*tid + WPT - 1
+      // ranks of a W-word bitmap: thread tid owns words WPT*tid .. WPT*tid + WPT - 1
+      auto bitmap_union = [&](auto words_const) __attribute__((always_inline)) {
+        constexpr int W = decltype(words_const)::value;
+        constexpr int WPT = W / NT;
+        int32_t* wbase = reinterpret_cast<int32_t*>(L.scratch) + W;
         uint32_t wv[WPT];
         int cnt = 0;
 #pragma unroll
@@ -567,6 +585,9 @@ __device__ __forceinline__ void tile_setup(const ConvArgs& a, int64_t r0, const 
             }
             for (int r = tid; r < TM; r += NT) L.sidx[NTAPS * TM + r] = (uint16_t)GEO::key(U);
         }
+      };
+      if (wide) bitmap_union(std::integral_constant<int, kWinWordsWide>{});
+      else bitmap_union(std::integral_constant<int, kWinWords>{});
     }
     if (tid == 0) {
         // the active taps in ascending order, four per word; padding 0xff

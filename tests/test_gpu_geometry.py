@@ -384,7 +384,9 @@ def test_plan_sections(spc, orc, dev, geo):
     tg = nat.tile_geometry(torch.bfloat16, ntaps=27, n_out=n, cin=32, cout=32)
     assert tg == nat.TILES_TALL
     assert nat.plan_section(torch.bfloat16, ntaps=27, n_out=n, cin=32, cout=64) == nat.PLAN_WIDE
-    assert nat.tile_geometry(torch.bfloat16, ntaps=27, n_out=n, cin=32, cout=128) == nat.TILES_SMALL
+    # short rows into 128 output columns: the wide tiles' double-buffered stage
+    assert nat.tile_geometry(torch.bfloat16, ntaps=27, n_out=n, cin=32, cout=128) == nat.TILES_WIDE
+    assert nat.tile_geometry(torch.bfloat16, ntaps=27, n_out=n, cin=64, cout=128) == nat.TILES_WIDE
     assert nat.tile_geometry(torch.bfloat16, ntaps=27, n_out=n, cin=64, cout=64) == nat.TILES_SMALL
 
 
