@@ -83,6 +83,10 @@ class SparseResBlock3d(nn.Module):
             self.updown = SparseDownsample(2)
         elif self.upsample:
             self.updown = SparseUpsample(2)
+        # upsample: norm1 / SiLU and the skip on the coarse rows (see
+        # _forward_upsample); False runs the reference's order over the
+        # upsampled copies
+        self.coarse_rows = True
 
     def _updown(self, x: SparseTensor) -> SparseTensor:
         if self.updown is not None:
@@ -92,6 +96,8 @@ class SparseResBlock3d(nn.Module):
     def forward(self, x: SparseTensor, emb: torch.Tensor) -> SparseTensor:
         emb_out = self.emb_layers(emb).type(x.dtype)
         scale, shift = torch.chunk(emb_out, 2, dim=1)
+        if self.upsample and self.coarse_rows:
+            return self._forward_upsample(x, scale, shift)
         x = self._updown(x)
         h = x.replace(nat.layernorm_silu(x.feats, self.norm1.weight, self.norm1.bias,
                                          eps=self.norm1.eps))
@@ -109,6 +115,46 @@ class SparseResBlock3d(nn.Module):
         if self.out_channels % 32 == 0:
             return self.conv2.forward_fused(h, residual=skip.feats)
         return self.conv2(h) + skip
+
+
+    def _forward_upsample(self, x: SparseTensor, scale: torch.Tensor,
+                          shift: torch.Tensor) -> SparseTensor:
+        """forward() with upsampling.  The reference upsamples first (fine
+        row f is a copy of coarse row up[f]) and normalises the copies; norm1,
+        SiLU and the skip Linear are row-wise, so they run on the coarse rows
+        (2048 channels over 11,774 instead of 62,710 rows in the SLAT output
+        block), conv1 reads them through the fine neighbour table composed
+        with up[] (the same values per row and tap, so the same sums, without
+        writing the copies), and conv2 adds the skip from row up[f] in its
+        epilogue."""
+        up = self.updown
+        rows = up.fine_rows(x)
+        n_f, n_c = rows.shape[0], x.feats.shape[0]
+        h_c = nat.layernorm_silu(x.feats, self.norm1.weight, self.norm1.bias, eps=self.norm1.eps)
+        # the fine level (coordinates, layout and cached maps of the paired
+        # downsample's input); its features are conv1's output
+        fine = up.fine_tensor(x, h_c.new_empty((n_f, 0)))
+        m = _subm_map(fine)
+        c1 = self.conv1.conv
+        comp = fine.data.cached("subm3_from_coarse", lambda c: nat.compose_rows(m.token_major, rows))
+        plan = fine.data.cached(("plan", "subm3_from_coarse"), lambda c: nat.conv_plan(
+            comp, ntaps=27, n_out=n_f, n_in=n_c, device=c.device, sections=nat.plan_section(
+                h_c.dtype, ntaps=27, n_out=n_f, cin=_pad32(c1.in_channels),
+                cout=_pad32(c1.out_channels),
+                epi_mode=nat.EPI_NORM_MOD_SILU if self.out_channels in (32, 64, 128) else 0)))
+        if self.out_channels in (32, 64, 128):
+            y1 = self.conv1._conv(h_c, comp, n_f, plan,
+                                  norm_mod=(scale.float(), shift.float(), fine.coords,
+                                            self.norm2.eps))
+        else:
+            y1 = self.conv1._conv(h_c, comp, n_f, plan)
+            y1 = nat.layernorm_mod_silu(y1, scale.float(), shift.float(), fine.coords,
+                                        eps=self.norm2.eps)
+        h = fine.replace(y1)
+        skip = self.skip_connection(x).feats
+        if self.out_channels % 32 == 0:
+            return self.conv2.forward_fused(h, residual=skip, residual_rows=rows)
+        return self.conv2(h) + h.replace(nat.gather_rows(skip, rows))
 
 
 class SparseSubdivideBlock3d(nn.Module):

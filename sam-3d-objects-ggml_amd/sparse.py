@@ -836,14 +836,25 @@ class SparseUpsample(nn.Module):
         self.factor = tuple(factor) if isinstance(factor, (list, tuple)) else factor
 
     def forward(self, input: SparseTensor) -> SparseTensor:
+        return self.fine_tensor(input, nat.gather_rows(input.feats, self.fine_rows(input)))
+
+    def fine_rows(self, input: SparseTensor) -> torch.Tensor:
+        """int32 [N_fine]: the coarse row each fine row copies."""
+        idx = input.get_spatial_cache(f"upsample_{_factor3(self.factor)}_idx")
+        if idx is None:
+            raise ValueError("Upsample cache not found. SparseUpsample must be paired with "
+                             "SparseDownsample.")
+        return idx
+
+    def fine_tensor(self, input: SparseTensor, feats: torch.Tensor) -> SparseTensor:
+        """The fine-level tensor (coordinates, layout, scale and kernel maps
+        of the paired downsample's input) carrying `feats` [N_fine, C]."""
         factor = _factor3(self.factor)
         coords = input.get_spatial_cache(f"upsample_{factor}_coords")
         layout = input.get_spatial_cache(f"upsample_{factor}_layout")
-        idx = input.get_spatial_cache(f"upsample_{factor}_idx")
-        if any(v is None for v in (coords, layout, idx)):
+        if coords is None or layout is None:
             raise ValueError("Upsample cache not found. SparseUpsample must be paired with "
                              "SparseDownsample.")
-        feats = nat.gather_rows(input.feats, idx)
         # the fine level's maps and extent, kept by the paired downsample
         # (the maps' entries check that they were built from these
         # coordinates); without them the extent is read from the coordinates
