@@ -645,12 +645,38 @@ def bench_bridge(nat, wl, c_dev, dev, args) -> dict:
         raise RuntimeError(f"sam3d_spconv_f16_forward: {err}")
     ms_packed, _ = time_gpu(packed, args.steps, args.warmup)
     ms_plan, _ = time_gpu(planned, args.steps, args.warmup)
+    # calls alternating between the fine rows and their stride-2 coarse rows
+    # (the SLAT IO blocks' two levels): each level keeps its own tile plan
+    d = nat.downsample_map(c_dev, int(c_dev[:, 0].max().item()) + 1, 64)
+    mc = nat.map_build(d.coarse_coords)
+    nc = d.nc
+    xc = torch.from_numpy(wl.normal((nc, 128), 1.0, seed=124)).to(dev).half()
+    yc = torch.empty((nc, 128), dtype=torch.float16, device=dev)
+    cargs = (s, xc.data_ptr(), w.data_ptr(), b.data_ptr(), yc.data_ptr(),
+             mc.offset_major.data_ptr(), mc.mask_sorted.data_ptr(), mc.argsort.data_ptr(), nc,
+             128, 128)
+
+    def coarse():
+        L.sam3d_spconv_f16_forward(*cargs)
+
+    def alternate():
+        L.sam3d_spconv_f16_forward(*bargs)
+        L.sam3d_spconv_f16_forward(*cargs)
+
+    ms_coarse, _ = time_gpu(coarse, args.steps, args.warmup)
+    ms_alt, _ = time_gpu(alternate, args.steps, args.warmup)
+    err = L.spc_last_error().decode(errors="replace")
+    if err:
+        raise RuntimeError(f"sam3d_spconv_f16_forward: {err}")
     torch.cuda.synchronize()
     return {"workload": "sam3d_spconv_f16_forward, f16 C=128 -> 128 on the headline rows",
             "bridge_ms": ms_bridge, "packed_ms": ms_packed, "packed_plan_ms": ms_plan,
             "bridge_over_packed": ms_bridge / ms_packed,
             "bit_identical": bool(torch.equal(y_bridge, y_packed) and
-                                  torch.equal(y_bridge, y_plan))}
+                                  torch.equal(y_bridge, y_plan)),
+            "coarse_rows": nc, "bridge_coarse_ms": ms_coarse,
+            "alternating_fine_coarse_ms": ms_alt,
+            "alternating_over_separate": ms_alt / (ms_bridge + ms_coarse)}
 
 
 def bench_feature_ops(spc, nat, wl, orc, coords, c_dev, dev, args, workload) -> dict:

@@ -433,3 +433,50 @@ def test_partial_tile_live_blocks(spc, orc, dev, geo, r):
                            x_dtype=oracle.BF16, w_dtype=oracle.BF16, b_dtype=oracle.BF16,
                            nthreads=oracle_threads(), blocked=True)
     check_16bit(f"partial tile Q8_0 wide N={n}", from_dev(yq), refq)
+
+
+def _slab_block(nx, ny, nz):
+    """Dense block of voxels, lexicographic rows: a tile's x +- 1 neighbours
+    lie ny * nz rows away."""
+    g = np.stack(np.meshgrid(np.arange(nx), np.arange(ny), np.arange(nz), indexing="ij"),
+                 -1).reshape(-1, 3)
+    c = np.zeros((g.shape[0], 4), np.int32)
+    c[:, 1:] = g
+    return c
+
+
+@pytest.mark.parametrize("dims,path", [((2, 256, 60), "32768-row bitmap"),
+                                       ((2, 768, 60), "65536-row bitmap"),
+                                       ((2, 1120, 60), "LDS hash")])
+def test_dedupe_paths(spc, orc, dev, geo, dims, path):
+    """The tile setup's three deduplication paths, chosen per tile from the
+    span of its source rows: dense 2 x ny x 60 blocks whose x-slabs hold
+    15,360 / 46,080 / 67,200 rows put every tile's sources within 32,768,
+    within 65,536 and beyond 65,536 rows (tests/test_oracle_maps.py checks the
+    spans on the CPU), each union within the stage.  All paths give the same
+    ascending union, so the wide, small and tall tiles, with and without a
+    plan, agree bit for bit, and with the oracle."""
+    import oracle
+    import torch
+
+    nat = geo
+    coords = _slab_block(*dims)
+    n = coords.shape[0]
+    _case(f"dedupe via the {path}: N={n} bf16 32->32")
+    (xh, wh, bh), (x, w, b) = _inputs(spc, orc, n, 32, 32, 27, seed=dims[1])
+    m = nat.map_build(torch.from_numpy(coords).to(dev))
+    pw = nat.pack_weights(w)
+
+    def run():
+        plan = nat.conv_plan(m.token_major, ntaps=27, n_out=n)
+        return (nat.sparse_conv(x, pw, b, m.token_major, ntaps=27, n_out=n, plan=plan),
+                nat.sparse_conv(x, pw, b, m.token_major, ntaps=27, n_out=n))
+
+    (wp, wn), (sp_, sn), (tp, tn_) = _all(nat, run)
+    for y in (wn, sp_, sn, tp, tn_):
+        assert torch.equal(y, wp)
+    ref = orc.sparse_conv(xh, wh, bh, m.token_major.cpu().numpy(), ntaps=27, n_out=n,
+                          idx_layout=1, out_dtype=oracle.F32, x_dtype=oracle.BF16,
+                          w_dtype=oracle.BF16, b_dtype=oracle.BF16, nthreads=oracle_threads(),
+                          blocked=True)
+    check_16bit(f"dedupe via the {path}", from_dev(wp), ref)

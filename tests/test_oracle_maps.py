@@ -258,3 +258,26 @@ def test_subdivide_keep_closed_form(spc, orc):
         assert np.array_equal(got_c, full[sel]) and np.array_equal(got_p, sel // 8)
         lvl = got_c
     assert lvl.shape[0] == 347860
+
+
+@pytest.mark.parametrize("dims,lo,hi", [((2, 256, 60), 0, 32768), ((2, 768, 60), 32768, 65536),
+                                        ((2, 1120, 60), 65536, 1 << 30)])
+def test_dedupe_path_spans(orc, dims, lo, hi):
+    """The premise of tests/test_gpu_geometry.py::test_dedupe_paths: in a
+    dense 2 x ny x 60 block every 256-row (and 128-row) tile's source rows
+    span more than `lo` and at most `hi` rows, and their union fits the
+    895-row (511-row) stage."""
+    nx, ny, nz = dims
+    g = np.stack(np.meshgrid(np.arange(nx), np.arange(ny), np.arange(nz), indexing="ij"),
+                 -1).reshape(-1, 3)
+    c = np.zeros((g.shape[0], 4), np.int32)
+    c[:, 1:] = g
+    n = c.shape[0]
+    tm = orc.conv_table_slat(c).reshape(n, 27)
+    for tile, umax in ((256, 895), (128, 511)):
+        for t0 in range(0, n, tile):
+            v = tm[t0:t0 + tile]
+            v = v[v < n]
+            span = int(v.max() - v.min() + 1)
+            assert lo < span <= hi, (tile, t0, span)
+            assert len(np.unique(v)) <= umax, (tile, t0)
