@@ -619,11 +619,14 @@ def bench_single_shell(nat, wl, orc, dev, args) -> dict:
     y = torch.empty((n, 128), dtype=torch.bfloat16, device=dev)
     call = ConvCall(nat, x, nat.pack_weights(w), b, y, m.token_major, ntaps=27, n_out=n,
                     layout=nat.IDX_TOKEN_MAJOR, plan=m.plan())
-    ms, _ = time_gpu(call, args.steps, args.warmup)
+    # its own warm-up: with 84 CUs idle the clock climbs higher (2.15 GHz in
+    # the loop) and takes longer to get there than the full-chip conv's
+    warm = max(args.warmup, 500)
+    ms, _ = time_gpu(call, args.steps, warm)
     tf = 2.0 * pairs * 128 * 128 / (ms / 1e3) / 1e12
     return {"workload": "subm3x3x3 bf16 C=128, one sphere shell r=24 in 64^3", "n_voxels": n,
             "pairs": pairs, "ms": ms, "mvoxel_s": n / (ms / 1e3) / 1e6, "tflops": tf,
-            "pct_peak": 100.0 * tf / PEAK_BF16_TFLOPS}
+            "pct_peak": 100.0 * tf / PEAK_BF16_TFLOPS, "steps": args.steps, "warmup": warm}
 
 
 def bench_bridge(nat, wl, c_dev, dev, args) -> dict:
