@@ -38,7 +38,8 @@ __host__ __device__ WStride weight_strides(int layout, int64_t ntaps, int64_t ci
 }
 
 // Panel word `id` (panel (tap, chunk, c32), word g, lane) of the packed
-// weights.
+// weights: fragments g G .. g G + G - 1, each EPL elements of one output
+// channel (Panel::co_of / ci_of).
 template <typename T, bool Q8>
 __device__ __forceinline__ void pack_word(const uint8_t* __restrict__ w, u32x4* __restrict__ out,
                                           int ntaps, int cin, int cout, WStride st, int64_t id) {
@@ -55,13 +56,12 @@ __device__ __forceinline__ void pack_word(const uint8_t* __restrict__ w, u32x4* 
     const int64_t tk = panel / ncol32;
     const int kc = (int)(tk % kch);
     const int o = (int)(tk / kch);
-    const int co = c32 * 32 + (lane & 31);
     if constexpr (!Q8 && sizeof(T) == 2) {
         if (st.ci == 1 && ((uintptr_t)w & 15u) == 0) {
             // the word's 8 channels are contiguous: one 16-byte load
             // (16-byte aligned: cin and the chunk offsets are multiples of 8)
-            const int64_t el = co * st.co + o * st.o + (int64_t)kc * P::KC + g * P::KSUB +
-                               (lane >> 5) * P::EPL;
+            const int64_t co = c32 * 32 + P::co_of(g, lane);
+            const int64_t el = co * st.co + o * st.o + (int64_t)kc * P::KC + P::ci_of(g, lane);
             out[id] = *reinterpret_cast<const u32x4*>(w + el * 2);
             return;
         }
@@ -69,8 +69,9 @@ __device__ __forceinline__ void pack_word(const uint8_t* __restrict__ w, u32x4* 
     uint8_t bytes[16];
 #pragma unroll
     for (int i = 0; i < P::G; ++i) {
-        const int ks = g * P::G + i;
-        const int64_t ci0 = (int64_t)kc * P::KC + ks * P::KSUB + (lane >> 5) * P::EPL;
+        const int f = g * P::G + i;
+        const int64_t co = c32 * 32 + P::co_of(f, lane);
+        const int64_t ci0 = (int64_t)kc * P::KC + P::ci_of(f, lane);
 #pragma unroll
         for (int e = 0; e < P::EPL; ++e) {
             const int64_t el = co * st.co + o * st.o + (ci0 + e) * st.ci;
@@ -111,30 +112,35 @@ __global__ void pack_scales_kernel(const uint16_t* __restrict__ d, float* __rest
 }
 
 // Packed Q8_0 panels -> packed bf16 panels of the same (tap, chunk, c32)
-// order.  A Q8_0 panel holds one 16-byte word per lane (both k-steps of
-// the chunk), a bf16 panel two (one per k-step); the f32 scale of lane l
-// is that of output channel 32 c32 + l % 32.  One thread per panel lane:
-// 16 quant bytes and a scale in, 32 bytes out, all coalesced.
+// order.  A Q8_0 panel holds one 16-byte word per lane (the 8 quants of
+// both 16-channel blocks), a bf16 panel two (one per block); lane l's
+// quants in block h belong to output channel 32 c32 + 16 h + l % 16, whose
+// f32 scale they take.  One thread per panel lane: 16 quant bytes and two
+// scales in, 32 bytes out, all coalesced.
 // F16: the same panels of f16(f32(d) * q) (bf16 and f16 panels share the
 // packed layout).
 template <bool F16>
 __global__ void expand_q8_0_kernel(const u32x4* __restrict__ q, const float* __restrict__ sc,
                                    u32x4* __restrict__ out, int64_t panels, int ncol32,
                                    int cout) {
+    using PQ = Panel<__bf16, true>;
+    using PB = Panel<__bf16, false>;
+    static_assert(PQ::NG == 1 && PQ::G == 2 && PB::NG == 2 && PB::NH == 2, "Q8_0 and 16-bit panel words");
     const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (id >= panels * 64) return;
     const int lane = (int)(id & 63);
     const int64_t p = id >> 6;
     const int64_t tk = p / ncol32;  // tap * chunks + chunk
     const int c32 = (int)(p - tk * ncol32);
-    const float d = sc[tk * cout + c32 * 32 + (lane & 31)];
+    const float d0 = sc[tk * cout + c32 * 32 + PQ::co_of(0, lane)];
+    const float d1 = sc[tk * cout + c32 * 32 + PQ::co_of(1, lane)];
     const u32x4 w = q[id];
     if constexpr (F16) {
-        out[p * 128 + lane] = __builtin_bit_cast(u32x4, q8_dequant8_f16(w.x, w.y, d));
-        out[p * 128 + 64 + lane] = __builtin_bit_cast(u32x4, q8_dequant8_f16(w.z, w.w, d));
+        out[p * 128 + lane] = __builtin_bit_cast(u32x4, q8_dequant8_f16(w.x, w.y, d0));
+        out[p * 128 + 64 + lane] = __builtin_bit_cast(u32x4, q8_dequant8_f16(w.z, w.w, d1));
     } else {
-        out[p * 128 + lane] = __builtin_bit_cast(u32x4, q8_dequant8(w.x, w.y, d));
-        out[p * 128 + 64 + lane] = __builtin_bit_cast(u32x4, q8_dequant8(w.z, w.w, d));
+        out[p * 128 + lane] = __builtin_bit_cast(u32x4, q8_dequant8(w.x, w.y, d0));
+        out[p * 128 + 64 + lane] = __builtin_bit_cast(u32x4, q8_dequant8(w.z, w.w, d1));
     }
 }
 
@@ -333,6 +339,7 @@ __global__ __launch_bounds__(256) void bridge_prep_kernel(
         // output channel (all real or all padding: both widths are
         // multiples of 8)
         using P = Panel<__bf16, false>;
+        static_assert(P::G == 1, "one fragment per word");
         const int kch = cin / P::KC;
         const int ncol32 = cout / 32;
         if (id >= (int64_t)27 * kch * ncol32 * P::NG * 64) return;
@@ -344,8 +351,8 @@ __global__ __launch_bounds__(256) void bridge_prep_kernel(
         const int64_t tk = panel / ncol32;
         const int kc = (int)(tk % kch);
         const int o = (int)(tk / kch);
-        const int co = c32 * 32 + (lane & 31);
-        const int ci0 = kc * P::KC + g * P::KSUB + (lane >> 5) * P::EPL;
+        const int co = c32 * 32 + P::co_of(g, lane);
+        const int ci0 = kc * P::KC + P::ci_of(g, lane);
         u32x4 v = {0u, 0u, 0u, 0u};
         if (co < cout_real && ci0 < cin_real) {
             const uint16_t* src = reinterpret_cast<const uint16_t*>(w) +

@@ -105,18 +105,36 @@ struct ConvArgs {
     int32_t geometry;         // tile geometry: 0 by shape, 1 wide, 2 small
 };
 
-// MFMA operand traits per activation type.
+// MFMA operand traits per activation type.  The conv computes transposed
+// blocks: the weights are the MFMA's row operand (BC output channels) and the
+// gathered features its column operand (BR output rows), so a lane's
+// accumulators hold runs of consecutive channels of one output row.
+//   16-bit  v_mfma_f32_16x16x32_{bf16,f16}: 16 rows x 16 channels per block,
+//           the 32 channels of a 64-byte chunk in one instruction; lane l
+//           supplies 8 consecutive channels 8 (l / 16) .. of row / output
+//           channel l % 16 and holds channels 4 (l / 16) .. + 3 of row l % 16.
+//           (Under full-chip load with real data this shape sustains ~2.0
+//           PFLOP/s against ~1.75 for 32x32x16: at equal work it draws less
+//           power, and the chip holds a higher clock.)
+//   f32     v_mfma_f32_32x32x2f32: 32 x 32 blocks, two channels per k-step;
+//           lane l holds channels 8 g + 4 (l / 32) .. + 3 (g < 4) of row l % 32.
 template <typename T>
 struct Mfma;
 
 template <>
 struct Mfma<__bf16> {
-    static constexpr int KSUB = 16;  // K per instruction
+    static constexpr int KSUB = 32;  // K per instruction
     static constexpr int EPL = 8;    // elements per lane per operand
+    static constexpr int BR = 16;    // output rows per block
+    static constexpr int BC = 16;    // output channels per block
+    static constexpr int NRUN = 1;   // runs of four channels per lane per block
     typedef bf16x8 frag;
-    __device__ static floatx16 mma(frag a, frag b, floatx16 c) {
-        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    typedef floatx4 acc_t;
+    __device__ static acc_t mma(frag a, frag b, acc_t c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
     }
+    // first channel (within the block) of a lane's run g
+    __host__ __device__ static constexpr int run(int lane, int) { return 4 * (lane >> 4); }
     __device__ static uint16_t cvt(float v) { return f32_to_bf16_bits(v); }
     __device__ static float ld(const void* p, int64_t i) {
         return bf16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
@@ -127,12 +145,17 @@ struct Mfma<__bf16> {
 
 template <>
 struct Mfma<_Float16> {
-    static constexpr int KSUB = 16;
+    static constexpr int KSUB = 32;
     static constexpr int EPL = 8;
+    static constexpr int BR = 16;
+    static constexpr int BC = 16;
+    static constexpr int NRUN = 1;
     typedef f16x8 frag;
-    __device__ static floatx16 mma(frag a, frag b, floatx16 c) {
-        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    typedef floatx4 acc_t;
+    __device__ static acc_t mma(frag a, frag b, acc_t c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
     }
+    __host__ __device__ static constexpr int run(int lane, int) { return 4 * (lane >> 4); }
     __device__ static uint16_t cvt(float v) { return f32_to_f16_bits(v); }
     __device__ static float ld(const void* p, int64_t i) {
         return f16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
@@ -145,10 +168,15 @@ template <>
 struct Mfma<float> {
     static constexpr int KSUB = 2;
     static constexpr int EPL = 1;
+    static constexpr int BR = 32;
+    static constexpr int BC = 32;
+    static constexpr int NRUN = 4;
     typedef float frag;
-    __device__ static floatx16 mma(frag a, frag b, floatx16 c) {
+    typedef floatx16 acc_t;
+    __device__ static acc_t mma(frag a, frag b, acc_t c) {
         return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
     }
+    __host__ __device__ static constexpr int run(int lane, int g) { return 8 * g + 4 * (lane >> 5); }
     __device__ static float cvt(float v) { return v; }
     __device__ static float ld(const void* p, int64_t i) {
         return static_cast<const float*>(p)[i];
@@ -156,21 +184,31 @@ struct Mfma<float> {
     __device__ static float round(float v) { return v; }
 };
 
-// Weight-panel geometry shared by the packer and the kernel.  One panel =
-// the B operands of (tap, channel chunk, 32 output channels) for all KS
-// MFMA k-steps of the chunk, stored lane-major as NG 16-byte words per lane:
-// word g of lane l holds k-steps g*G .. g*G+G-1, each EPL elements of
-// W[co = 32*c32 + l%32][tap][ci = chunk*KC + ks*KSUB + (l/32)*EPL + e].
+// Weight-panel geometry shared by the packers and the kernel.  One panel =
+// the row operands of (tap, channel chunk, 32 output channels): NF = KS x NH
+// MFMA fragments (KS k-steps of the chunk, NH = 32 / BC channel blocks),
+// fragment f = ks NH + h holding, for lane l, EPL elements of
+// W[co = 32 c32 + h BC + l % BC][tap][ci = chunk KC + ks KSUB + (l / BC) EPL + e].
+// Stored lane-major as NG 16-byte words per lane, G fragments per word
+// (16-bit: two words, one per 16-channel block; Q8_0: one word, both blocks'
+// 8 quants; f32: two words of four k-steps each).
 template <typename T, bool Q8>
 struct Panel {
     static constexpr int KC = 64 / sizeof(T);  // channels per chunk (64-byte rows)
     static constexpr int KSUB = Mfma<T>::KSUB;
     static constexpr int EPL = Mfma<T>::EPL;
+    static constexpr int BC = Mfma<T>::BC;
     static constexpr int KS = KC / KSUB;                  // MFMA k-steps per chunk
+    static constexpr int NH = 32 / BC;                    // channel blocks per panel
+    static constexpr int NF = KS * NH;                    // fragments per panel
     static constexpr int WB = Q8 ? 1 : (int)sizeof(T);    // stored bytes per weight
-    static constexpr int G = 16 / (EPL * WB);             // k-steps per 16-byte word
-    static constexpr int NG = KS / G;                     // words per lane per panel
-    static_assert(KS % G == 0, "panel geometry");
+    static constexpr int G = 16 / (EPL * WB);             // fragments per 16-byte word
+    static constexpr int NG = NF / G;                     // words per lane per panel
+    static_assert(NF % G == 0 && KS * KSUB == KC && NH * BC == 32, "panel geometry");
+    // output channel (within the panel) and first input channel (within the
+    // chunk) of lane l's elements of fragment f
+    __host__ __device__ static constexpr int co_of(int f, int lane) { return (f % NH) * BC + lane % BC; }
+    __host__ __device__ static constexpr int ci_of(int f, int lane) { return (f / NH) * KSUB + (lane / BC) * EPL; }
 };
 
 // Q8_0 dequantisation of one k-step's 8 quants (byte e of lo, hi = quant
@@ -256,16 +294,21 @@ constexpr int kSegs = 4;        // 16-byte segments per staged 64-byte row chunk
 //             128 channels waits for one staging instead of one per chunk --
 //             for the stride-2 convs whose tiles fit the device in one round.
 // Staged row layouts (one 64-byte chunk of a union row = four 16-byte
-// segments; a wave's A-fragment read takes one segment of 32 slots, which
-// the LDS serves 16 lanes at a time):
-//   SW = false  row r at an 80-byte pitch: segment s at unit 5r + s; 16
-//               consecutive slots reading one segment hit 16 distinct
-//               bank groups (5 is odd).
-//   SW = true   row r at a 64-byte pitch, segment s at unit 4r + (s ^ ((r >> 2)
-//               & 3)): the XOR spreads 16 consecutive slots over the 16 bank
-//               groups as well, without the 16 bytes of padding per row.
+// segments; a 16-bit wave's feature-fragment read takes all four segments
+// of 16 slots, lane l segment l / 16 of slot l % 16):
+//   SW = false  row r at an 80-byte pitch: segment s at unit 5r + s.
+//   SW = true   row r at a 64-byte pitch, segment s at unit 4r + (s ^ ((r >> 1)
+//               & 3)): 16 consecutive slots read that way are served at the
+//               LDS's full 198 B/clk per CU (an LDS probe, 8 waves per CU:
+//               swizzling on row bits 2-3 instead -- conflict-free for the
+//               32-row reads of a 32x32 MFMA operand -- gives 128 B/clk for
+//               this pattern, no swizzle 128 B/clk; the f32 kernels' 4-byte
+//               reads take the same time either way).
 // A slot key is the unit of segment 0's position base: unit(s) = key + s
 // (padded) or key ^ s (swizzled: the key's low two bits carry the swizzle).
+// A tap's slot keys sit in 64-row groups, row r of a group at position
+// 4 (r % 16) + r / 16, so the 16-bit kernels' four keys of lane l (rows
+// l % 16 + 16 i of a 64-row wave tile) are one 8-byte LDS read.
 template <int TM_, int UMAX_, int NBUF_, bool SW_, int PUMAX_ = UMAX_>
 struct Geo {
     static constexpr int TM = TM_;
@@ -281,7 +324,8 @@ struct Geo {
     // 16-byte units per A buffer: whole 64-unit blocks (one LDS-DMA
     // instruction each) holding the UMAX union rows and the zero row
     static constexpr int STAGE = ((UMAX + 1) * PITCH + 63) / 64 * 64;
-    __host__ __device__ static constexpr int key(int r) { return SW ? 4 * r + ((r >> 2) & 3) : 5 * r; }
+    __host__ __device__ static constexpr int swz(int r) { return (r >> 1) & 3; }
+    __host__ __device__ static constexpr int key(int r) { return SW ? 4 * r + swz(r) : 5 * r; }
     __host__ __device__ static constexpr int unit(int k, int s) { return SW ? (k ^ s) : k + s; }
     __host__ __device__ static constexpr int seg_pos(int r, int s) { return unit(key(r), s); }
     // One row tile's plan: header (U, tap mask, fast flag, tap words),
@@ -320,6 +364,10 @@ __host__ __device__ constexpr int64_t plan_small_bytes(int64_t n_out, int ntaps)
 
 constexpr int kTapWords = 8;  // step taps, four per word: up to 28 steps per chunk
 constexpr int32_t kPlanMagic = 0x314e4c50;  // header word 3 of every built plan tile
+
+// Position of tile row r among a tap's TM slot keys: 64-row groups, row
+// 16 i + j of a group at 4 j + i.
+__host__ __device__ constexpr int slot_pos(int r) { return (r & ~63) | ((r & 15) << 2) | ((r >> 4) & 3); }
 
 // Shared-memory arrays of one tile's setup.
 struct TileLds {
@@ -516,7 +564,7 @@ __device__ __forceinline__ void tile_setup(const ConvArgs& a, int64_t r0, const 
                         }
                         out = (uint32_t)v == (uint32_t)ent[k] ? (int32_t)(v >> 32) : U;
                     }
-                    L.sidx[o * TM + r] = (uint16_t)GEO::key(out);
+                    L.sidx[o * TM + slot_pos(r)] = (uint16_t)GEO::key(out);
                 }
             }
             for (int r = tid; r < TM; r += NT) L.sidx[NTAPS * TM + r] = (uint16_t)GEO::key(U);
@@ -580,7 +628,7 @@ __device__ __forceinline__ void tile_setup(const ConvArgs& a, int64_t r0, const 
                         const int wi = off >> 5;
                         out = wbase[wi] + __popc(bm[wi] & ((1u << (off & 31)) - 1u));
                     }
-                    L.sidx[o * TM + r] = (uint16_t)GEO::key(out);
+                    L.sidx[o * TM + slot_pos(r)] = (uint16_t)GEO::key(out);
                 }
             }
             for (int r = tid; r < TM; r += NT) L.sidx[NTAPS * TM + r] = (uint16_t)GEO::key(U);
@@ -668,14 +716,19 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
     constexpr int KC = P::KC;
     constexpr int WTM = TM / WM;
     constexpr int WTN = TN / WN;
-    constexpr int FM = WTM / 32;
-    constexpr int FN = WTN / 32;
+    constexpr int BR = M::BR;                   // output rows per MFMA block
+    constexpr int BC = M::BC;                   // output channels per MFMA block
+    constexpr int NH = P::NH;                   // channel blocks per 32-channel panel
+    constexpr int FM = WTM / BR;                // the wave's row blocks
+    constexpr int FN = WTN / 32;                // the wave's 32-channel panels
+    constexpr int FC = FN * NH;                 // the wave's channel blocks
     constexpr int NQ = NTAPS * TM;
     constexpr int STAGE = GEO::STAGE;           // 16-byte units per A buffer
     constexpr int NBUF = GEO::NBUF;             // A buffers
     constexpr int ABYTES = NBUF * STAGE * 16;   // the A area (reused by the setup and epilogue)
     constexpr int NPART = 4;                    // parts of a chunk's staging
-    static_assert(FM >= 1 && FN >= 1 && WTM * WM == TM && WTN * WN == TN, "wave geometry");
+    static_assert(FM >= 1 && FN >= 1 && FM * BR == WTM && FN * 32 == WTN && WTM * WM == TM && WTN * WN == TN,
+                  "wave geometry");
     static_assert(!Q8 || ES == 2, "Q8_0 weights feed 16-bit MFMA operands");
     static_assert(NTAPS <= 32, "tap mask is 32-bit");
     static_assert(kSetupScratchWords * 4 <= ABYTES, "setup scratch aliases the A stage");
@@ -855,18 +908,18 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
     const int wn = wave % WN;
 
     // accumulators start at the bias: element 4g + e of lane l holds output
-    // channel 8g + 4(l/32) + e of its 32-column block
-    floatx16 acc[FM][FN];
+    // channel M::run(l, g) + e of its channel block
+    typename M::acc_t acc[FM][FC];
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-        floatx4 b4[4];
+    for (int c = 0; c < FC; ++c) {
+        floatx4 b4[M::NRUN];
 #pragma unroll
-        for (int g = 0; g < 4; ++g)
-            b4[g] = *reinterpret_cast<const floatx4*>(sbias + wn * WTN + j * 32 + 8 * g + 4 * (lane >> 5));
+        for (int g = 0; g < M::NRUN; ++g)
+            b4[g] = *reinterpret_cast<const floatx4*>(sbias + wn * WTN + c * BC + M::run(lane, g));
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
-            for (int k = 0; k < 16; ++k) acc[i][j][k] = b4[k / 4][k % 4];
+            for (int k = 0; k < 4 * M::NRUN; ++k) acc[i][c][k] = b4[k / 4][k % 4];
     }
 
     const char* xb = static_cast<const char*>(a.x);
@@ -874,7 +927,7 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
 
     struct Slot {
         u32x4 q[FN][P::NG];
-        float d[Q8 ? FN : 1];
+        float d[Q8 ? FC : 1];  // Q8_0: scale of the lane's channel in block j NH + h
     };
 
     // Packed weights through a buffer resource: the panel offset is a scalar,
@@ -886,12 +939,11 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
     const uint32_t wtap0 = a.class_rows > 0 ? (uint32_t)(r0 / a.class_rows) * NTAPS : 0u;
     const __amdgpu_buffer_rsrc_t wrsrc =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a.w), (short)0, (int)wbytes, 0x00020000);
-    // B operands of (tap o, chunk kc) for this wave's FN column blocks
+    // weight operands of (tap o, chunk kc) for this wave's FN panels
     auto load_b = [&](int o, int kc, Slot& sl) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
             const int c32 = (co0 + wn * WTN) / 32 + j;  // wave-uniform
-            const int co = c32 * 32 + (lane & 31);
             if constexpr (PACKED) {
                 const uint32_t panel =
                     ((wtap0 + (uint32_t)o) * (uint32_t)kch + (uint32_t)kc) * (uint32_t)ncol32 + (uint32_t)c32;
@@ -900,78 +952,85 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
                 for (int g = 0; g < P::NG; ++g)
                     sl.q[j][g] = __builtin_bit_cast(
                         u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrsrc, lane * 16 + g * 1024, poff, 0));
-                if constexpr (Q8)
-                    sl.d[j] = static_cast<const float*>(a.wscale)[((int64_t)o * kch + kc) * a.cout + co];
+                if constexpr (Q8) {
+#pragma unroll
+                    for (int h = 0; h < NH; ++h)
+                        sl.d[j * NH + h] = static_cast<const float*>(
+                            a.wscale)[((int64_t)o * kch + kc) * a.cout + c32 * 32 + P::co_of(h, lane)];
+                }
             } else {
-                const int64_t rowbase = ((int64_t)co * NTAPS + o) * a.cin + (int64_t)kc * KC;
+                // [cout, ntaps, cin]: fragment f of word g from its own row
 #pragma unroll
                 for (int g = 0; g < P::NG; ++g) {
-                    if constexpr (P::G == 1) {
-                        const int64_t el = rowbase + g * P::KSUB + (lane >> 5) * P::EPL;
-                        sl.q[j][g] = *reinterpret_cast<const u32x4*>(
+                    uint32_t words[4];
+                    constexpr int WPF = 4 / P::G;  // 32-bit words per fragment
+#pragma unroll
+                    for (int i = 0; i < P::G; ++i) {
+                        const int f = g * P::G + i;
+                        const int64_t co = c32 * 32 + P::co_of(f, lane);
+                        const int64_t el = (co * NTAPS + o) * a.cin + (int64_t)kc * KC + P::ci_of(f, lane);
+                        const uint32_t* wp = reinterpret_cast<const uint32_t*>(
                             static_cast<const char*>(a.w) + el * P::WB);
-                    } else {
-                        uint32_t words[4];
-                        constexpr int WPK = 4 / P::G;  // 32-bit words per k-step
 #pragma unroll
-                        for (int i = 0; i < P::G; ++i) {
-                            const int ks = g * P::G + i;
-                            const int64_t el = rowbase + ks * P::KSUB + (lane >> 5) * P::EPL;
-                            const uint32_t* wp = reinterpret_cast<const uint32_t*>(
-                                static_cast<const char*>(a.w) + el * P::WB);
+                        for (int h = 0; h < WPF; ++h) words[i * WPF + h] = wp[h];
+                    }
+                    sl.q[j][g] = u32x4{words[0], words[1], words[2], words[3]};
+                }
+                if constexpr (Q8) {
 #pragma unroll
-                            for (int h = 0; h < WPK; ++h) words[i * WPK + h] = wp[h];
-                        }
-                        sl.q[j][g] = u32x4{words[0], words[1], words[2], words[3]};
+                    for (int h = 0; h < NH; ++h) {
+                        const int64_t co = c32 * 32 + P::co_of(h, lane);
+                        const int64_t el = (co * NTAPS + o) * a.cin + (int64_t)kc * KC;
+                        sl.d[j * NH + h] = f16_bits_to_f32(static_cast<const uint16_t*>(a.wscale)[el >> 5]);
                     }
                 }
-                if constexpr (Q8)
-                    sl.d[j] = f16_bits_to_f32(static_cast<const uint16_t*>(a.wscale)[rowbase >> 5]);
             }
         }
     };
 
-    // B fragment of k-step ks from a loaded slot
-    auto b_frag = [&](const Slot& sl, int j, int ks) __attribute__((always_inline)) {
-        typename M::frag f;
-        const u32x4 wv4 = sl.q[j][ks / P::G];
+    // weight fragment f (k-step f / NH, channel block f % NH) of panel j from a loaded slot
+    auto b_frag = [&](const Slot& sl, int j, int f) __attribute__((always_inline)) {
+        typename M::frag fr;
+        const u32x4 wv4 = sl.q[j][f / P::G];
         if constexpr (Q8) {
-            // 8 int8 quants of this k-step -> bf16(d * q)
-            f = q8_dequant8((ks % P::G) == 0 ? wv4.x : wv4.z, (ks % P::G) == 0 ? wv4.y : wv4.w,
-                            sl.d[j]);
+            // 8 int8 quants of this fragment -> bf16(d * q)
+            fr = q8_dequant8((f % P::G) == 0 ? wv4.x : wv4.z, (f % P::G) == 0 ? wv4.y : wv4.w,
+                             sl.d[j * NH + f % NH]);
         } else if constexpr (P::G == 1) {
-            f = __builtin_bit_cast(typename M::frag, wv4);
+            fr = __builtin_bit_cast(typename M::frag, wv4);
         } else {
-            // explicit component select: indexing the vector by (ks % G) read
+            // explicit component select: indexing the vector by (f % G) read
             // component 0 for every k-step in generated code
-            const int c = ks % P::G;
+            const int c = f % P::G;
             const uint32_t word = c == 0 ? wv4.x : c == 1 ? wv4.y : c == 2 ? wv4.z : wv4.w;
-            f = __builtin_bit_cast(float, word);
+            fr = __builtin_bit_cast(float, word);
         }
-        return f;
+        return fr;
     };
 
     typedef typename M::frag AFrag[P::KS][FM];
-    // The MFMA computes the transposed block (weights as the 32-row operand,
-    // gathered features as the 32-column one): the accumulator of lane l then
-    // holds output row l%32 and output channels 8*(k/4) + 4*(l/32) + k%4 for
-    // element k -- four runs of four consecutive channels per lane, stored
-    // straight to global memory.
-    // fa_const: the wave's live 32-row blocks (FM, or fewer in a partial
-    // last row tile, whose dead blocks are skipped)
+    // The MFMA computes the transposed block (weights as the row operand,
+    // gathered features as the column one): the accumulator of lane l then
+    // holds output row l % BR and four consecutive output channels from
+    // M::run(l, g) per run g, stored straight to global memory.
+    // fa_const: the wave's live row blocks (FM, or fewer in a partial last
+    // row tile, whose dead blocks are skipped)
     auto mma_step = [&](const AFrag& af, const Slot& bs, auto fa_const) __attribute__((always_inline)) {
         constexpr int FA = decltype(fa_const)::value;
 #pragma unroll
         for (int ks = 0; ks < P::KS; ++ks) {
 #pragma unroll
             for (int j = 0; j < FN; ++j) {
-                const typename M::frag bf = b_frag(bs, j, ks);
 #pragma unroll
-                for (int i = 0; i < FA; ++i) acc[i][j] = M::mma(bf, af[ks][i], acc[i][j]);
+                for (int h = 0; h < NH; ++h) {
+                    const typename M::frag bf = b_frag(bs, j, ks * NH + h);
+#pragma unroll
+                    for (int i = 0; i < FA; ++i) acc[i][j * NH + h] = M::mma(bf, af[ks][i], acc[i][j * NH + h]);
+                }
             }
         }
     };
-    // A fragments of k-slices of 32 rows per FM block.  sl[] holds slot
+    // A fragments of k-slices of BR rows per row block.  sl[] holds slot
     // keys; the byte of each k-step within the 64-byte row is a lane
     // constant, its segment placed by the geometry's row layout.
     auto read_frags = [&](int buf, const int* sl, AFrag& f, auto fa_const) __attribute__((always_inline)) {
@@ -979,18 +1038,36 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
         const char* ab = reinterpret_cast<const char*>(Au + buf * STAGE);
 #pragma unroll
         for (int ks = 0; ks < P::KS; ++ks) {
-            const int byte = (ks * M::KSUB + (lane >> 5) * M::EPL) * ES;  // within the 64-byte row
+            const int byte = (ks * M::KSUB + (lane / BR) * M::EPL) * ES;  // within the 64-byte row
 #pragma unroll
             for (int i = 0; i < FA; ++i)
                 f[ks][i] = *reinterpret_cast<const typename M::frag*>(
                     ab + GEO::unit(sl[i], byte >> 4) * 16 + (byte & 15));
         }
     };
-    // union slots of the wave's rows for sidx row `row` (a tap, or NTAPS = zeros)
+    // union slots of the wave's rows for sidx row `row` (a tap, or NTAPS =
+    // zeros): 16-row blocks read four keys (a 64-row wave tile) or two (32
+    // rows) at once from the interleaved layout
     auto read_slots = [&](int row, int* sl, auto fa_const) __attribute__((always_inline)) {
         constexpr int FA = decltype(fa_const)::value;
+        const uint16_t* st = sidx + row * TM;
+        if constexpr (BR == 16 && WTM % 64 == 0) {
 #pragma unroll
-        for (int i = 0; i < FA; ++i) sl[i] = sidx[row * TM + wm * WTM + i * 32 + (lane & 31)];
+            for (int q = 0; q < (FA + 3) / 4; ++q) {
+                const u32x2 v = *reinterpret_cast<const u32x2*>(st + wm * WTM + 64 * q + 4 * (lane & 15));
+#pragma unroll
+                for (int i = 0; i < 4 && 4 * q + i < FA; ++i)
+                    sl[4 * q + i] = (int)((i & 1) ? v[i >> 1] >> 16 : v[i >> 1] & 0xffffu);
+            }
+        } else if constexpr (BR == 16 && WTM == 32) {
+            const uint32_t v = *reinterpret_cast<const uint32_t*>(
+                st + (wm * WTM & ~63) + 4 * (lane & 15) + ((wm * WTM >> 4) & 3));
+            sl[0] = (int)(v & 0xffffu);
+            if constexpr (FA > 1) sl[1] = (int)(v >> 16);
+        } else {
+#pragma unroll
+            for (int i = 0; i < FA; ++i) sl[i] = st[slot_pos(wm * WTM + i * BR + (lane % BR))];
+        }
     };
     const auto fm_all = std::integral_constant<int, FM>{};
 
@@ -1029,7 +1106,7 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
         for (int j = 0; j < NJ; ++j) {
             const int v = (wave + NW * j) * 64 + lane;
             const int r = v / GEO::PITCH;
-            const int sg = GEO::SW ? (v & 3) ^ ((r >> 2) & 3) : v - r * GEO::PITCH;
+            const int sg = GEO::SW ? (v & 3) ^ GEO::swz(r) : v - r * GEO::PITCH;
             doff[j] = 0x80000000u;  // out of range: zeros
             if (sg < kSegs && r < U)
                 doff[j] = (uint32_t)(urow[r] - row0) * (uint32_t)rowbytes + (uint32_t)(sg * 16);
@@ -1235,7 +1312,7 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
                         // issue order: slot reads, then MFMAs interleaved with the
                         // fragment reads and their address arithmetic, then the
                         // weight loads
-                        constexpr int NMF = P::KS * FA * FN;
+                        constexpr int NMF = P::KS * FA * FC;
                         constexpr int NFR = P::KS * FA;
                         __builtin_amdgcn_sched_group_barrier(0x100, FA, 0);
 #pragma unroll
@@ -1275,12 +1352,12 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
             }
           };
             // A wave of the partial last row tile whose rows end inside its
-            // first 32-row block runs that block's MFMAs only (the same
-            // loads and barriers): a 6-row tile no longer costs a full one.
+            // first row block runs that block's MFMAs only (the same loads
+            // and barriers): a 6-row tile no longer costs a full one.
             uint32_t live_blocks = 0;  // bit i: block i has a row
 #pragma unroll
             for (int i = 0; i < FM; ++i)
-                live_blocks |= (__builtin_amdgcn_ballot_w64(srow[wm * WTM + i * 32 + (lane & 31)] >= 0) != 0)
+                live_blocks |= (__builtin_amdgcn_ballot_w64(srow[wm * WTM + i * BR + (lane % BR)] >= 0) != 0)
                                 << i;
             if constexpr (FM >= 2) {
                 if (live_blocks == 1u) run_tile(std::integral_constant<int, 1>{});
@@ -1346,7 +1423,7 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
                     int sl[FM];
 #pragma unroll
                     for (int i = 0; i < FM; ++i)
-                        sl[i] = GEO::key(g * TM + wm * WTM + i * 32 + (lane & 31));
+                        sl[i] = GEO::key(g * TM + wm * WTM + i * BR + (lane % BR));
                     AFrag af;
                     read_frags(0, sl, af, fm_all);
                     mma_step(af, bs[g & 1], fm_all);
@@ -1380,16 +1457,16 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
         lds_barrier();  // every wave is done with the A stage / the previous pass
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
-            const int rl = wm * WTM + i * 32 + (lane & 31);
-            if (wm * WTM + i * 32 < p * RPN || wm * WTM + i * 32 >= (p + 1) * RPN) continue;
+            const int rl = wm * WTM + i * BR + (lane % BR);
+            if (wm * WTM + i * BR < p * RPN || wm * WTM + i * BR >= (p + 1) * RPN) continue;
 #pragma unroll
-            for (int j = 0; j < FN; ++j)
+            for (int c = 0; c < FC; ++c)
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const int cl = wn * WTN + j * 32 + 8 * g + 4 * (lane >> 5);
+                for (int g = 0; g < M::NRUN; ++g) {
+                    const int cl = wn * WTN + c * BC + M::run(lane, g);
                     *reinterpret_cast<floatx4*>(of + (rl - p * RPN) * FP + cl) =
-                        floatx4{M::round(acc[i][j][4 * g]), M::round(acc[i][j][4 * g + 1]),
-                                M::round(acc[i][j][4 * g + 2]), M::round(acc[i][j][4 * g + 3])};
+                        floatx4{M::round(acc[i][c][4 * g]), M::round(acc[i][c][4 * g + 1]),
+                                M::round(acc[i][c][4 * g + 2]), M::round(acc[i][c][4 * g + 3])};
                 }
         }
         lds_barrier();
@@ -1464,15 +1541,15 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
                         : pw_extra + (wave - PW_IN_STAGE) * PW_BYTES;
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
-            const int rl = i * 32 + (lane & 31);
+            const int rl = i * BR + (lane % BR);
 #pragma unroll
-            for (int j = 0; j < FN; ++j)
+            for (int c = 0; c < FC; ++c)
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const int cl = j * 32 + 8 * g + 4 * (lane >> 5);
+                for (int g = 0; g < M::NRUN; ++g) {
+                    const int cl = c * BC + M::run(lane, g);
                     *reinterpret_cast<u32x2*>(reg + rl * PW_PITCH + cl * ES) =
-                        u32x2{(uint32_t)M::cvt(acc[i][j][4 * g]) | ((uint32_t)M::cvt(acc[i][j][4 * g + 1]) << 16),
-                              (uint32_t)M::cvt(acc[i][j][4 * g + 2]) | ((uint32_t)M::cvt(acc[i][j][4 * g + 3]) << 16)};
+                        u32x2{(uint32_t)M::cvt(acc[i][c][4 * g]) | ((uint32_t)M::cvt(acc[i][c][4 * g + 1]) << 16),
+                              (uint32_t)M::cvt(acc[i][c][4 * g + 2]) | ((uint32_t)M::cvt(acc[i][c][4 * g + 3]) << 16)};
                 }
         }
         // the reads below take other lanes' writes: keep the compiler from
@@ -1540,16 +1617,16 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
         lds_barrier();  // every wave is done with the A stage / the previous pass
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
-            const int rl = wm * WTM + i * 32 + (lane & 31);
-            if (wm * WTM + i * 32 < p * RPP || wm * WTM + i * 32 >= (p + 1) * RPP) continue;
+            const int rl = wm * WTM + i * BR + (lane % BR);
+            if (wm * WTM + i * BR < p * RPP || wm * WTM + i * BR >= (p + 1) * RPP) continue;
 #pragma unroll
-            for (int j = 0; j < FN; ++j) {
+            for (int c = 0; c < FC; ++c) {
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const int cl = wn * WTN + j * 32 + 8 * g + 4 * (lane >> 5);
+                for (int g = 0; g < M::NRUN; ++g) {
+                    const int cl = wn * WTN + c * BC + M::run(lane, g);
                     float v[4];
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * g + e];
+                    for (int e = 0; e < 4; ++e) v[e] = acc[i][c][4 * g + e];
                     char* dst = ob + (rl - p * RPP) * OPITCH + cl * ES;
                     if constexpr (ES == 4) {
                         *reinterpret_cast<float2*>(dst) = float2{v[0], v[1]};

@@ -390,10 +390,11 @@ def test_plan_sections(spc, orc, dev, geo):
     assert nat.tile_geometry(torch.bfloat16, ntaps=27, n_out=n, cin=64, cout=64) == nat.TILES_SMALL
 
 
-@pytest.mark.parametrize("r", [1, 6, 31, 32, 33, 64, 65, 129, 255])
+@pytest.mark.parametrize("r", [1, 6, 15, 16, 17, 31, 32, 33, 64, 65, 129, 255])
 def test_partial_tile_live_blocks(spc, orc, dev, geo, r):
     """A partial last row tile of 2 * 256 + r rows: its waves whose rows end
-    inside their first 32-row block run that block's MFMAs only.  bf16
+    inside their first row block (16 rows in 16-bit) run that block's MFMAs
+    only.  bf16
     128 -> 128 on the wide tiles (64-row waves), the small tiles (64-row
     waves over 128-row tiles), the tall tiles (64-row waves over 256-row
     tiles) and Q8_0 128 -> 128 (128-row waves), every row against the
