@@ -720,14 +720,21 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
     constexpr int BC = M::BC;                   // output channels per MFMA block
     constexpr int NH = P::NH;                   // channel blocks per 32-channel panel
     constexpr int FM = WTM / BR;                // the wave's row blocks
-    constexpr int FN = WTN / 32;                // the wave's 32-channel panels
-    constexpr int FC = FN * NH;                 // the wave's channel blocks
+    constexpr int FC = WTN / BC;                // the wave's channel blocks
+    // Weight loads: packed 16-bit weights per 16-channel block (a panel's
+    // word h is its block h, so a wave's width need only be a multiple of
+    // 16: the 96-column tiles' 48-channel waves), the other layouts per
+    // 32-channel panel of P::NG words.
+    constexpr bool BLK = PACKED && !Q8 && P::G == 1 && P::NG == NH && P::KS == 1;
+    constexpr int LG = BLK ? FC : WTN / 32;     // load groups per step
+    constexpr int LW = BLK ? 1 : P::NG;         // words per load group
     constexpr int NQ = NTAPS * TM;
     constexpr int STAGE = GEO::STAGE;           // 16-byte units per A buffer
     constexpr int NBUF = GEO::NBUF;             // A buffers
     constexpr int ABYTES = NBUF * STAGE * 16;   // the A area (reused by the setup and epilogue)
     constexpr int NPART = 4;                    // parts of a chunk's staging
-    static_assert(FM >= 1 && FN >= 1 && FM * BR == WTM && FN * 32 == WTN && WTM * WM == TM && WTN * WN == TN,
+    static_assert(FM >= 1 && FC >= 1 && FM * BR == WTM && FC * BC == WTN && (BLK || WTN % 32 == 0) &&
+                      WTM * WM == TM && WTN * WN == TN,
                   "wave geometry");
     static_assert(!Q8 || ES == 2, "Q8_0 weights feed 16-bit MFMA operands");
     static_assert(NTAPS <= 32, "tap mask is 32-bit");
@@ -926,7 +933,7 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
     const u32x4 zero4 = {0u, 0u, 0u, 0u};
 
     struct Slot {
-        u32x4 q[FN][P::NG];
+        u32x4 q[LG][LW];
         float d[Q8 ? FC : 1];  // Q8_0: scale of the lane's channel in block j NH + h
     };
 
@@ -939,12 +946,19 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
     const uint32_t wtap0 = a.class_rows > 0 ? (uint32_t)(r0 / a.class_rows) * NTAPS : 0u;
     const __amdgpu_buffer_rsrc_t wrsrc =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a.w), (short)0, (int)wbytes, 0x00020000);
-    // weight operands of (tap o, chunk kc) for this wave's FN panels
+    // weight operands of (tap o, chunk kc) for this wave's LG load groups
     auto load_b = [&](int o, int kc, Slot& sl) __attribute__((always_inline)) {
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-            const int c32 = (co0 + wn * WTN) / 32 + j;  // wave-uniform
-            if constexpr (PACKED) {
+        for (int j = 0; j < LG; ++j) {
+            const int c32 = (co0 + wn * WTN) / 32 + j;  // wave-uniform (panel groups)
+            if constexpr (BLK) {
+                const int cb = (co0 + wn * WTN) / BC + j;  // 16-channel block, wave-uniform
+                const uint32_t panel = ((wtap0 + (uint32_t)o) * (uint32_t)kch + (uint32_t)kc) *
+                                           (uint32_t)ncol32 + (uint32_t)(cb / NH);
+                const int poff = (int)(panel * (uint32_t)(P::NG * 1024) + (uint32_t)(cb % NH) * 1024u);
+                sl.q[j][0] = __builtin_bit_cast(
+                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrsrc, lane * 16, poff, 0));
+            } else if constexpr (PACKED) {
                 const uint32_t panel =
                     ((wtap0 + (uint32_t)o) * (uint32_t)kch + (uint32_t)kc) * (uint32_t)ncol32 + (uint32_t)c32;
                 const int poff = (int)(panel * (uint32_t)(P::NG * 1024));
@@ -1017,15 +1031,25 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
     // row tile, whose dead blocks are skipped)
     auto mma_step = [&](const AFrag& af, const Slot& bs, auto fa_const) __attribute__((always_inline)) {
         constexpr int FA = decltype(fa_const)::value;
+        if constexpr (BLK) {
 #pragma unroll
-        for (int ks = 0; ks < P::KS; ++ks) {
+            for (int c = 0; c < FC; ++c) {
+                const typename M::frag bf = __builtin_bit_cast(typename M::frag, bs.q[c][0]);
 #pragma unroll
-            for (int j = 0; j < FN; ++j) {
+                for (int i = 0; i < FA; ++i) acc[i][c] = M::mma(bf, af[0][i], acc[i][c]);
+            }
+        } else {
 #pragma unroll
-                for (int h = 0; h < NH; ++h) {
-                    const typename M::frag bf = b_frag(bs, j, ks * NH + h);
+            for (int ks = 0; ks < P::KS; ++ks) {
 #pragma unroll
-                    for (int i = 0; i < FA; ++i) acc[i][j * NH + h] = M::mma(bf, af[ks][i], acc[i][j * NH + h]);
+                for (int j = 0; j < LG; ++j) {
+#pragma unroll
+                    for (int h = 0; h < NH; ++h) {
+                        const typename M::frag bf = b_frag(bs, j, ks * NH + h);
+#pragma unroll
+                        for (int i = 0; i < FA; ++i)
+                            acc[i][j * NH + h] = M::mma(bf, af[ks][i], acc[i][j * NH + h]);
+                    }
                 }
             }
         }
@@ -1136,7 +1160,7 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
                 for (int h = 0; h < NPART; ++h) stage_part_rt(c, c % NBUF, h);
         };
         // vector-memory loads per step (weight words, plus Q8_0 scales)
-        constexpr int LPS = PACKED ? FN * P::NG + (Q8 ? FN : 0) : 0;
+        constexpr int LPS = PACKED ? LG * LW + (Q8 ? FC : 0) : 0;
         // Four buffers with at most two step groups per chunk (the stride-2
         // taps): a whole-chunk weight ring.  Every step's weights are loaded
         // one chunk ahead and each chunk is staged at the start of the one
@@ -1322,7 +1346,7 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
                             // Q8_0: room for the in-register dequantisation
                             __builtin_amdgcn_sched_group_barrier(0x002, Q8 ? 6 : 2, 0);
                         }
-                        __builtin_amdgcn_sched_group_barrier(0x020, FN * P::NG, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x020, LG * LW, 0);
                         // nothing crosses a step boundary: without this fence the
                         // scheduler sinks every weight load of the group to its
                         // end, which leaves the next group's first steps waiting
@@ -1875,11 +1899,12 @@ hipError_t dispatch_tn(hipStream_t s, const ConvArgs& a) {
         if (a.cout % 192 == 0 && a.cout % 128 != 0 && a.epi_mode != SPC_EPI_NORM_MOD_SILU &&
             tiles_m * (a.cout / 192) >= a.num_cu)
             return launch_conv<T, Q8, PACKED, NTAPS, 192, 2, 2>(s, a);
-        // 96 (the mesh decoder's 768 / 8): four waves of 64x96 instead of
-        // three 32-column tiles of 32x32 wave tiles
+        // 96 (the mesh decoder's 768 / 8): eight waves of 64x48 (two per
+        // SIMD, weights loaded per 16-channel block) instead of three
+        // 32-column tiles of 32x32 wave tiles
         if (a.cout % 96 == 0 && a.cout % 64 != 0 && a.epi_mode != SPC_EPI_NORM_MOD_SILU &&
             tiles_m * (a.cout / 96) >= a.num_cu)
-            return launch_conv<T, Q8, PACKED, NTAPS, 96, 4, 1>(s, a);
+            return launch_conv<T, Q8, PACKED, NTAPS, 96, 4, 2>(s, a);
     }
     if (tn == 128) {
         if constexpr (Q8) return launch_conv<T, Q8, PACKED, NTAPS, 128, 2, 2>(s, a);
