@@ -58,12 +58,13 @@ def test_bf16_channels(spc, orc, dev, cin, cout):
     assert torch.equal(y, yp)
 
 
-@pytest.mark.parametrize("ntaps,cout", [(27, 192), (8, 192), (27, 96)])
+@pytest.mark.parametrize("ntaps,cout", [(27, 192), (8, 192), (27, 96), (8, 96)])
 def test_bf16_wide_tiles(spc, orc, dev, ntaps, cout):
     """C_out = 192 / 96 with at least 256 row tiles runs the 192-column tile
-    (four waves of 128x96) / the 96-column tile (four waves of 64x96):
-    every row against the oracle, and bit-identical to the unpacked-weight
-    launch, which runs 64- / 32-column tiles."""
+    (four waves of 128x96) / the 96-column tile (eight waves of 64x48,
+    weights loaded per 16-channel block): every row against the oracle, and
+    bit-identical to the unpacked-weight launch, which runs 64- / 32-column
+    tiles."""
     import torch
 
     nat = spc._native
