@@ -62,9 +62,10 @@ def test_bf16_channels(spc, orc, dev, cin, cout):
 def test_bf16_wide_tiles(spc, orc, dev, ntaps, cout):
     """C_out = 192 / 96 with at least 256 row tiles runs the 192-column tile
     (four waves of 128x96) / the 96-column tile (eight waves of 64x48,
-    weights loaded per 16-channel block): every row against the oracle, and
-    bit-identical to the unpacked-weight launch, which runs 64- / 32-column
-    tiles."""
+    weights loaded per 16-channel block; the 8-tap convs take them with the
+    wide geometry forced, as the decoder's merged-tap convs do through their
+    weight classes): every row against the oracle, and bit-identical to the
+    unpacked-weight launch, which runs 64- / 32-column tiles."""
     import torch
 
     nat = spc._native
@@ -83,7 +84,14 @@ def test_bf16_wide_tiles(spc, orc, dev, ntaps, cout):
     wd = to_dev_bf16(w, dev)
     xd, bd = to_dev_bf16(x, dev), to_dev_bf16(b, dev)
     plan = nat.conv_plan(idx, ntaps=ntaps, n_out=n_out, n_in=n_in)
-    yp = nat.sparse_conv(xd, nat.pack_weights(wd), bd, idx, ntaps=ntaps, n_out=n_out, plan=plan)
+    pw = nat.pack_weights(wd)
+    if ntaps == 8:
+        nat.set_tile_geometry(nat.TILES_WIDE)
+        assert nat.tile_geometry(torch.bfloat16, ntaps=8, n_out=n_out, cin=64, cout=cout) == nat.TILES_WIDE
+    try:
+        yp = nat.sparse_conv(xd, pw, bd, idx, ntaps=ntaps, n_out=n_out, plan=plan)
+    finally:
+        nat.set_tile_geometry(nat.TILES_AUTO)
     y = nat.sparse_conv(xd, wd, bd, idx, ntaps=ntaps, n_out=n_out, plan=plan)
     torch.cuda.synchronize()
     ref = _oracle_bf16(orc, x, w, b, idx.cpu().numpy(), np.arange(n_out), ntaps, n_in)
