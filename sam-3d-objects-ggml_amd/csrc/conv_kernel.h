@@ -551,8 +551,6 @@ __device__ __forceinline__ void tile_setup(const ConvArgs& a, int64_t r0, const 
             for (int k = 0; k < EPT; ++k) {
                 const int e = tid + k * NT;
                 if (e < NQ) {
-                    const int r = e / NTAPS;
-                    const int o = e - r * NTAPS;
                     int32_t out = U;  // the zero row
                     if (ent[k] >= 0) {
                         // present: no insert stopped early when U <= kUMax
@@ -564,7 +562,7 @@ __device__ __forceinline__ void tile_setup(const ConvArgs& a, int64_t r0, const 
                         }
                         out = (uint32_t)v == (uint32_t)ent[k] ? (int32_t)(v >> 32) : U;
                     }
-                    L.sidx[o * TM + slot_pos(r)] = (uint16_t)GEO::key(out);
+                    ent[k] = GEO::key(out);  // the entry's slot key (placed below)
                 }
             }
             for (int r = tid; r < TM; r += NT) L.sidx[NTAPS * TM + r] = (uint16_t)GEO::key(U);
@@ -602,16 +600,7 @@ __device__ __forceinline__ void tile_setup(const ConvArgs& a, int64_t r0, const 
 #pragma unroll
             for (int w = 0; w < WPT; ++w) {
                 wbase[WPT * tid + w] = b;
-                if (fast) {
-                    uint32_t m = wv[w];
-                    while (m) {
-                        const int bit = __ffs(m) - 1;
-                        m &= m - 1;
-                        L.urow[b++] = lo + (WPT * tid + w) * 32 + bit;
-                    }
-                } else {
-                    b += __popc(wv[w]);
-                }
+                b += __popc(wv[w]);
             }
         }
         lds_barrier();
@@ -620,15 +609,19 @@ __device__ __forceinline__ void tile_setup(const ConvArgs& a, int64_t r0, const 
             for (int k = 0; k < EPT; ++k) {
                 const int e = tid + k * NT;
                 if (e < NQ) {
-                    const int r = e / NTAPS;
-                    const int o = e - r * NTAPS;
                     int32_t out = U;  // the zero row
                     if (ent[k] >= 0) {
                         const int32_t off = ent[k] - lo;
                         const int wi = off >> 5;
                         out = wbase[wi] + __popc(bm[wi] & ((1u << (off & 31)) - 1u));
+                        // the union row at its rank: every union row is some
+                        // entry's source, and entries sharing a source write
+                        // the same value (a per-word walk of the set bits
+                        // left most lanes idle behind the densest words:
+                        // 6.6 of a 256^3-level tile's 19 us)
+                        L.urow[out] = ent[k];
                     }
-                    L.sidx[o * TM + slot_pos(r)] = (uint16_t)GEO::key(out);
+                    ent[k] = GEO::key(out);  // the entry's slot key (placed below)
                 }
             }
             for (int r = tid; r < TM; r += NT) L.sidx[NTAPS * TM + r] = (uint16_t)GEO::key(U);
@@ -636,6 +629,28 @@ __device__ __forceinline__ void tile_setup(const ConvArgs& a, int64_t r0, const 
       };
       if (wide) bitmap_union(std::integral_constant<int, kWinWordsWide>{});
       else bitmap_union(std::integral_constant<int, kWinWords>{});
+    }
+    if (fast) {
+        // The slot keys go to their rows through a contiguous staging pass:
+        // entry e = r NTAPS + o leaves a thread's registers for stg[e], then
+        // each (tap, row) is read across and placed.  Stored straight from
+        // the entry order, a wave's 64 lanes wrote TM x 2 bytes apart per tap,
+        // into a few LDS banks (the plan of the 1,393,024-row 256^3 level:
+        // 10.8 of a tile's 19 us).
+        static_assert(NQ * 2 <= kSetupScratchWords * 4, "slot-key staging fits the scratch");
+        lds_barrier();  // every thread is done with the bitmap / hash
+        uint16_t* stg = reinterpret_cast<uint16_t*>(L.scratch);
+#pragma unroll
+        for (int k = 0; k < EPT; ++k) {
+            const int e = tid + k * NT;
+            if (e < NQ) stg[e] = (uint16_t)ent[k];
+        }
+        lds_barrier();
+        for (int q = tid; q < NQ; q += NT) {
+            const int o = q / TM;
+            const int r = q - o * TM;
+            L.sidx[o * TM + slot_pos(r)] = stg[r * NTAPS + o];
+        }
     }
     if (tid == 0) {
         // the active taps in ascending order, four per word; padding 0xff
