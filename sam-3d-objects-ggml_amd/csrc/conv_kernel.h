@@ -871,6 +871,26 @@ __global__ __launch_bounds__(WM * WN * 64, (geo_blocks_per_cu<GEO, TN>())) void 
         tile_mask = (uint32_t)misc[1];
         fast = misc[2] != 0;
     }
+    if constexpr (NTAPS == 1) {
+        if (!planned && a.idx == nullptr && a.row_perm == nullptr && a.class_rows == 0) {
+            // the dense 1x1x1 conv (identity map): the tile's union is its own
+            // rows in order, each row's slot its own -- no deduplication (the
+            // general setup cost such a tile more than its one-tap loop)
+            const int nr = (int)min<int64_t>(TM, a.n_out - r0);
+            for (int r = tid; r < TM; r += NT) {
+                srow[r] = r < nr ? (int32_t)(r0 + r) : -1;
+                urow[r] = (int32_t)(r0 + r);
+                sidx[slot_pos(r)] = (uint16_t)GEO::key(r < nr ? r : nr);
+                sidx[TM + r] = (uint16_t)GEO::key(nr);
+            }
+            if (tid < kTapWords) tlw[tid] = tid == 0 ? 0xffffff00u : 0xffffffffu;  // tap 0, then padding
+            lds_barrier();
+            U = nr;
+            tile_mask = 1u;
+            fast = true;
+            planned = true;
+        }
+    }
     if (!planned) {
         // tile_setup writes misc[3] only after its first barriers, once every
         // thread has read the marker above
