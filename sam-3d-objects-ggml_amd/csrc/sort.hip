@@ -11,11 +11,15 @@
 //   upsweep   : per-tile digit histogram (tile = 256 threads x 1-8 keys:
 //               small sorts take fewer keys per thread, up to 64 tiles)
 //   offsets   : up to 128 tiles, every downsweep block derives its own
-//               offsets from the digit-major [512 x tiles] counts; beyond
-//               that one workgroup scans them first
+//               offsets from the block-major [tiles x 512] counts (a wave
+//               reads 512 contiguous bytes per tile, up to 64 tiles in one
+//               batch of loads); beyond that the counts are digit-major and
+//               a multi-block exclusive scan turns them into offsets
 //   downsweep : per tile, stable rank of every key among equal digits via
-//               64-lane ballots (peer mask -> popcount of lower lanes), wave
-//               counts combined in LDS, scattered to offset + rank
+//               64-lane ballots (peer mask -> popcount of lower lanes); the
+//               per-(round, wave) digit counts of up to four rounds are
+//               scanned in one LDS pass (three barriers per 1,024 keys);
+//               scattered to offset + rank
 #include <cstdarg>
 #include <cstdio>
 
@@ -46,12 +50,14 @@ __device__ inline int32_t wave_incl_scan(int32_t v, int lane) {
     return v;
 }
 
-// Per-tile digit histogram, digit-major: counts[d * nblocks + block].
+// Per-tile digit histogram, digit-major (counts[d * nblocks + block], the
+// order a global scan needs) or, with BLOCK_MAJOR, one row of kRsBins per
+// tile (counts[block * kRsBins + d]: the fused downsweep's coalesced reads).
 // A tile is kRsThreads x ITEMS keys.
-template <typename K, int ITEMS>
+template <typename K, int ITEMS, bool BLOCK_MAJOR>
 __global__ __launch_bounds__(kRsThreads) void rs_upsweep(const K* __restrict__ keys, int64_t n,
                                                          int shift, int32_t* __restrict__ counts,
-                                                         int stride) {
+                                                         int nblocks) {
     __shared__ int32_t hist[kRsBins];
 #pragma unroll
     for (int j = 0; j < kRsBinsPerThread; ++j) hist[j * kRsThreads + threadIdx.x] = 0;
@@ -69,55 +75,76 @@ __global__ __launch_bounds__(kRsThreads) void rs_upsweep(const K* __restrict__ k
 #pragma unroll
     for (int j = 0; j < kRsBinsPerThread; ++j) {
         const int d = j * kRsThreads + threadIdx.x;
-        counts[(int64_t)d * stride + blockIdx.x] = hist[d];
+        counts[BLOCK_MAJOR ? (int64_t)blockIdx.x * kRsBins + d : (int64_t)d * nblocks + blockIdx.x] =
+            hist[d];
     }
 }
 
 // Stable scatter of one tile.  `offsets` (digit-major, as the scan leaves
 // them) gives each (digit, block) its first output position; with
-// FUSED the block derives its own offsets from the raw counts instead:
-// offset(d) = (keys of smaller digits) + (keys of digit d in earlier
-// blocks).  Within the tile every key is ranked among equal digits by
-// 64-lane ballots (peer mask -> popcount of lower lanes), wave counts
-// combined in LDS, rounds in input order.
+// FUSED the block derives its own offsets from the raw block-major counts
+// instead: offset(d) = (keys of smaller digits) + (keys of digit d in
+// earlier blocks).  Within the tile every key is ranked among equal digits by
+// 64-lane ballots (peer mask -> popcount of lower lanes); the counts of
+// each (round, wave) become offsets in input order (round, then wave), up
+// to four rounds per group.
 template <typename K, bool FUSED, int ITEMS>
 __global__ __launch_bounds__(kRsThreads) void rs_downsweep(
     const K* __restrict__ keys_in, const int32_t* __restrict__ vals_in, K* __restrict__ keys_out,
     int32_t* __restrict__ vals_out, int64_t n, int shift, const int32_t* __restrict__ offsets,
-    int nblocks, int stride) {
-    __shared__ int32_t wave_off[kRsWaves][kRsBins];
+    int nblocks) {
+    constexpr int R = ITEMS < 4 ? ITEMS : 4;  // rounds per group
+    __shared__ int32_t cnt[R * kRsWaves][kRsBins];
     __shared__ int32_t run[kRsBins];
     __shared__ int32_t wsum[kRsWaves];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
+    const int64_t base = (int64_t)blockIdx.x * (kRsThreads * ITEMS);
+    // FUSED: thread tid owns digits 2 tid and 2 tid + 1, one 8-byte load per
+    // block's row of counts (a wave's load is 512 contiguous bytes).  Up to
+    // 64 loads go out at once (one batch up to 64 blocks), the row index
+    // clamped so every load is in bounds; the first batch before the tile's
+    // keys, so both latencies overlap.
+    static_assert(kRsBinsPerThread == 2, "two digits per thread");
+    constexpr int MAXB = 64;
+    const int2* c = reinterpret_cast<const int2*>(offsets) + tid;
+    int2 v2[FUSED ? MAXB : 1];
     if constexpr (FUSED) {
-        // thread tid owns digits kRsBinsPerThread*tid .. +kRsBinsPerThread-1
-        int32_t tot[kRsBinsPerThread], before[kRsBinsPerThread];
-        int32_t mine = 0;
 #pragma unroll
-        for (int j = 0; j < kRsBinsPerThread; ++j) {
-            // the digit's row of per-block counts, four at a time (stride is a
-            // multiple of four; entries past nblocks are padding)
-            const int4* c = reinterpret_cast<const int4*>(
-                offsets + (int64_t)(kRsBinsPerThread * tid + j) * stride);
-            int32_t t = 0, bsum = 0;
-#pragma unroll 8
-            for (int q = 0; q < stride / 4; ++q) {  // eight 16-byte loads in flight
-                const int4 v4 = c[q];
-                const int32_t v[4] = {v4.x, v4.y, v4.z, v4.w};
+        for (int k = 0; k < MAXB; ++k) v2[k] = c[(int64_t)min(k, nblocks - 1) * (kRsBins / 2)];
+    }
+    K key[ITEMS];
+    int32_t val[ITEMS];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int b = 4 * q + e;
-                    const int32_t vv = b < nblocks ? v[e] : 0;
-                    t += vv;
-                    if (b < (int)blockIdx.x) bsum += vv;
+    for (int r = 0; r < ITEMS; ++r) {
+        const int64_t i = base + r * kRsThreads + tid;
+        const bool valid = i < n;
+        key[r] = valid ? keys_in[i] : (K)0;
+        val[r] = valid ? (vals_in ? vals_in[i] : (int32_t)i) : 0;
+    }
+    if constexpr (FUSED) {
+        int32_t tot[2] = {0, 0}, before[2] = {0, 0};
+        for (int b0 = 0;;) {
+#pragma unroll
+            for (int k = 0; k < MAXB; ++k) {
+                const int b = b0 + k;
+                if (b < nblocks) {
+                    tot[0] += v2[k].x;
+                    tot[1] += v2[k].y;
+                    if (b < (int)blockIdx.x) {
+                        before[0] += v2[k].x;
+                        before[1] += v2[k].y;
+                    }
                 }
             }
-            tot[j] = t;
-            before[j] = bsum;
-            mine += t;
+            b0 += MAXB;
+            if (b0 >= nblocks) break;
+#pragma unroll
+            for (int k = 0; k < MAXB; ++k)
+                v2[k] = c[(int64_t)min(b0 + k, nblocks - 1) * (kRsBins / 2)];
         }
+        const int32_t mine = tot[0] + tot[1];
         const int32_t incl = wave_incl_scan(mine, lane);
         if (lane == 63) wsum[wave] = incl;
         __syncthreads();
@@ -125,63 +152,67 @@ __global__ __launch_bounds__(kRsThreads) void rs_downsweep(
 #pragma unroll
         for (int w = 0; w < kRsWaves; ++w)
             if (w < wave) excl += wsum[w];
-#pragma unroll
-        for (int j = 0; j < kRsBinsPerThread; ++j) {
-            run[kRsBinsPerThread * tid + j] = excl + before[j];
-            excl += tot[j];
-        }
+        run[2 * tid] = excl + before[0];
+        run[2 * tid + 1] = excl + tot[0] + before[1];
     } else {
 #pragma unroll
         for (int j = 0; j < kRsBinsPerThread; ++j) {
             const int d = j * kRsThreads + tid;
-            run[d] = offsets[(int64_t)d * stride + blockIdx.x];
+            run[d] = offsets[(int64_t)d * nblocks + blockIdx.x];
         }
     }
-    const int64_t base = (int64_t)blockIdx.x * (kRsThreads * ITEMS);
     const unsigned long long lower = (1ull << lane) - 1ull;
-    for (int r = 0; r < ITEMS; ++r) {
 #pragma unroll
-        for (int w = 0; w < kRsWaves; ++w)
+    for (int g = 0; g < ITEMS / R; ++g) {
 #pragma unroll
-            for (int j = 0; j < kRsBinsPerThread; ++j) wave_off[w][j * kRsThreads + tid] = 0;
-        __syncthreads();
-        const int64_t i = base + r * kRsThreads + tid;
-        const bool valid = i < n;
-        const K key = valid ? keys_in[i] : (K)0;
-        const int32_t val = valid ? (vals_in ? vals_in[i] : (int32_t)i) : 0;
-        const uint32_t d = (uint32_t)(key >> shift) & (kRsBins - 1);
-        // lanes of this wave holding the same digit
-        unsigned long long peers = __ballot(valid);
+        for (int e = 0; e < R * kRsWaves; ++e)
 #pragma unroll
-        for (int b = 0; b < kRsBits; ++b) {
-            const bool bit = (d >> b) & 1u;
-            const unsigned long long bal = __ballot(bit);
-            peers &= bit ? bal : ~bal;
+            for (int j = 0; j < kRsBinsPerThread; ++j) cnt[e][j * kRsThreads + tid] = 0;
+        __syncthreads();  // also orders run[] (written per owner above) before the scan
+        uint32_t dig[R];
+        int rank[R];
+#pragma unroll
+        for (int q = 0; q < R; ++q) {
+            const int r = g * R + q;
+            const bool valid = base + r * kRsThreads + tid < n;
+            dig[q] = (uint32_t)(key[r] >> shift) & (kRsBins - 1);
+            // lanes of this wave holding the same digit
+            unsigned long long peers = __ballot(valid);
+#pragma unroll
+            for (int b = 0; b < kRsBits; ++b) {
+                const bool bit = (dig[q] >> b) & 1u;
+                const unsigned long long bal = __ballot(bit);
+                peers &= bit ? bal : ~bal;
+            }
+            rank[q] = __popcll(peers & lower);
+            if (valid && rank[q] == 0) cnt[q * kRsWaves + wave][dig[q]] = __popcll(peers);
         }
-        const int rank = __popcll(peers & lower);
-        if (valid && rank == 0) wave_off[wave][d] = __popcll(peers);
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < kRsBinsPerThread; ++j) {
-            // wave counts -> offsets (global base + keys of this digit already
-            // placed by earlier rounds)
+            // (round, wave) counts -> offsets in input order, after the keys
+            // of this digit placed by earlier groups
             const int dd = j * kRsThreads + tid;
             int32_t acc = run[dd];
 #pragma unroll
-            for (int w = 0; w < kRsWaves; ++w) {
-                const int32_t c = wave_off[w][dd];
-                wave_off[w][dd] = acc;
+            for (int e = 0; e < R * kRsWaves; ++e) {
+                const int32_t c = cnt[e][dd];
+                cnt[e][dd] = acc;
                 acc += c;
             }
             run[dd] = acc;
         }
         __syncthreads();
-        if (valid) {
-            const int32_t dst = wave_off[wave][d] + rank;
-            keys_out[dst] = key;
-            vals_out[dst] = val;
+#pragma unroll
+        for (int q = 0; q < R; ++q) {
+            const int r = g * R + q;
+            if (base + r * kRsThreads + tid < n) {
+                const int32_t dst = cnt[q * kRsWaves + wave][dig[q]] + rank[q];
+                keys_out[dst] = key[r];
+                vals_out[dst] = val[r];
+            }
         }
-        __syncthreads();
+        if (g + 1 < ITEMS / R) __syncthreads();  // cnt is cleared by the next group
     }
 }
 
@@ -231,30 +262,39 @@ constexpr int kScanThreads = 256;
 constexpr int kScanItems = 16;
 constexpr int kScanTile = kScanThreads * kScanItems;
 
+// Sum of each tile of kScanTile values: per-thread sums, wave shuffles,
+// one LDS step.
 __global__ __launch_bounds__(kScanThreads) void scan_tile_sums(const int32_t* __restrict__ in,
                                                                int32_t* __restrict__ sums,
                                                                int64_t n) {
-    __shared__ int32_t s[kScanThreads];
+    __shared__ int32_t wsum[kScanThreads / 64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t base = (int64_t)blockIdx.x * kScanTile;
     int32_t acc = 0;
+#pragma unroll
     for (int r = 0; r < kScanItems; ++r) {
         const int64_t i = base + r * kScanThreads + threadIdx.x;
         if (i < n) acc += in[i];
     }
-    s[threadIdx.x] = acc;
+    const int32_t incl = wave_incl_scan(acc, lane);
+    if (lane == 63) wsum[wave] = incl;
     __syncthreads();
-    for (int w = kScanThreads / 2; w > 0; w >>= 1) {
-        if (threadIdx.x < w) s[threadIdx.x] += s[threadIdx.x + w];
-        __syncthreads();
+    if (threadIdx.x == 0) {
+        int32_t t = 0;
+#pragma unroll
+        for (int w = 0; w < kScanThreads / 64; ++w) t += wsum[w];
+        sums[blockIdx.x] = t;
     }
-    if (threadIdx.x == 0) sums[blockIdx.x] = s[0];
 }
 
+// Exclusive scan of each tile (kScanItems contiguous values per thread)
+// from its offset tile_off[tile]: wave shuffles and one LDS step.
 __global__ __launch_bounds__(kScanThreads) void scan_tiles(const int32_t* __restrict__ in,
                                                            int32_t* __restrict__ out,
                                                            const int32_t* __restrict__ tile_off,
                                                            int64_t n) {
-    __shared__ int32_t s[kScanThreads];
+    __shared__ int32_t wsum[kScanThreads / 64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t base = (int64_t)blockIdx.x * kScanTile + (int64_t)threadIdx.x * kScanItems;
     int32_t v[kScanItems];
     int32_t sum = 0;
@@ -264,15 +304,13 @@ __global__ __launch_bounds__(kScanThreads) void scan_tiles(const int32_t* __rest
         v[j] = i < n ? in[i] : 0;
         sum += v[j];
     }
-    s[threadIdx.x] = sum;
+    const int32_t incl = wave_incl_scan(sum, lane);
+    if (lane == 63) wsum[wave] = incl;
     __syncthreads();
-    for (int off = 1; off < kScanThreads; off <<= 1) {
-        const int32_t t = threadIdx.x >= off ? s[threadIdx.x - off] : 0;
-        __syncthreads();
-        s[threadIdx.x] += t;
-        __syncthreads();
-    }
-    int32_t acc = tile_off[blockIdx.x] + s[threadIdx.x] - sum;
+    int32_t acc = tile_off[blockIdx.x] + incl - sum;
+#pragma unroll
+    for (int w = 0; w < kScanThreads / 64; ++w)
+        if (w < wave) acc += wsum[w];
 #pragma unroll
     for (int j = 0; j < kScanItems; ++j) {
         const int64_t i = base + j;
@@ -307,13 +345,12 @@ hipError_t radix_sort_items(hipStream_t s, const K* keys_in, const int32_t* vals
                             int32_t* vals_out, int64_t n, int end_bit, void* ws, size_t ws_bytes) {
     const int nblocks = (int)ceil_div(n, (int64_t)kRsThreads * ITEMS);
     const bool fused = nblocks <= kRsFusedBlocks;
-    // fused: digit rows padded to a multiple of four for 16-byte reads; the
-    // single-block scan walks the counts linearly, so no padding there
-    const int stride = fused ? (nblocks + 3) / 4 * 4 : nblocks;
     Carver c(ws, ws_bytes);
-    int32_t* counts = c.take<int32_t>((size_t)kRsBins * stride);
+    int32_t* counts = c.take<int32_t>((size_t)kRsBins * nblocks);
     K* tk[2] = {c.take<K>(n), c.take<K>(n)};
     int32_t* tv[2] = {c.take<int32_t>(n), c.take<int32_t>(n)};
+    const size_t scan_bytes = fused ? 0 : scan_ws_bytes((int64_t)kRsBins * nblocks);
+    char* scan_ws = c.take<char>(scan_bytes);
     if (!c.ok) return hipErrorInvalidValue;
     int passes = (end_bit + kRsBits - 1) / kRsBits;
     if (passes < 1) passes = 1;
@@ -324,14 +361,17 @@ hipError_t radix_sort_items(hipStream_t s, const K* keys_in, const int32_t* vals
         K* kout = last ? keys_out : tk[p & 1];
         int32_t* vout = last ? vals_out : tv[p & 1];
         const int shift = p * kRsBits;
-        rs_upsweep<K, ITEMS><<<nblocks, kRsThreads, 0, s>>>(kin, n, shift, counts, stride);
         if (fused) {
+            rs_upsweep<K, ITEMS, true><<<nblocks, kRsThreads, 0, s>>>(kin, n, shift, counts, nblocks);
             rs_downsweep<K, true, ITEMS><<<nblocks, kRsThreads, 0, s>>>(
-                kin, vin, kout, vout, n, shift, counts, nblocks, stride);
+                kin, vin, kout, vout, n, shift, counts, nblocks);
         } else {
-            scan_one_block<<<1, 1024, 0, s>>>(counts, counts, nullptr, (int64_t)kRsBins * nblocks);
+            rs_upsweep<K, ITEMS, false><<<nblocks, kRsThreads, 0, s>>>(kin, n, shift, counts, nblocks);
+            const hipError_t e = exclusive_scan_i32(s, counts, counts, nullptr,
+                                                    (int64_t)kRsBins * nblocks, scan_ws, scan_bytes);
+            if (e != hipSuccess) return e;
             rs_downsweep<K, false, ITEMS><<<nblocks, kRsThreads, 0, s>>>(
-                kin, vin, kout, vout, n, shift, counts, nblocks, stride);
+                kin, vin, kout, vout, n, shift, counts, nblocks);
         }
         kin = kout;
         vin = vout;
@@ -389,9 +429,10 @@ size_t radix_sort_ws_bytes(int64_t n, int key_bytes) {
     const int64_t m = n > 0 ? n : 1;
     const int64_t nblocks = ceil_div(m, (int64_t)kRsThreads * rs_items(m));
     Sizer z;
-    z.take<int32_t>((size_t)kRsBins * ((nblocks + 3) / 4 * 4));
+    z.take<int32_t>((size_t)kRsBins * nblocks);
     for (int i = 0; i < 2; ++i) z.take<char>((size_t)n * key_bytes);
     for (int i = 0; i < 2; ++i) z.take<int32_t>(n);
+    z.take<char>(nblocks <= kRsFusedBlocks ? 0 : scan_ws_bytes((int64_t)kRsBins * nblocks));
     return z.used + 256;
 }
 
@@ -414,10 +455,15 @@ size_t scan_ws_bytes(int64_t n) {
     return z.used + 256;
 }
 
+// Up to here one workgroup scans alone (four rounds of 4,096); beyond, the
+// three-launch tile scan is faster, each of the one workgroup's rounds
+// costing a global-memory round trip (62,710 values: 26 us alone).
+constexpr int64_t kScanOneBlockMax = 16384;
+
 hipError_t exclusive_scan_i32(hipStream_t s, const int32_t* in, int32_t* out, int32_t* total,
                               int64_t n, void* ws, size_t ws_bytes) {
     if (n <= 0) return total ? fill_i32(s, total, 0, 1) : hipSuccess;
-    if (n <= 65536) {
+    if (n <= kScanOneBlockMax) {
         scan_one_block<<<1, 1024, 0, s>>>(in, out, total, n);
         return hipGetLastError();
     }
