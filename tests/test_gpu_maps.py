@@ -219,7 +219,12 @@ def test_large_subdivided_shell_maps(spc, dev):
     m = nat.map_build(torch.from_numpy(child).to(dev))
     assert torch.equal(nat.map_build(torch.from_numpy(child).to(dev), outputs="token",
                                      dense=(1, 256)).token_major, m.token_major)
-    pm = nat.map_build(torch.from_numpy(par).to(dev), outputs="token")
+    pm = nat.map_build(torch.from_numpy(par).to(dev))
+    # the parents' mask sort: 86 tiles of 2,048 keys, past the 64 tiles whose
+    # counts each downsweep block reads in one batch
+    pmask = ((pm.token_major.cpu().numpy().reshape(npar, 27) < npar) << np.arange(27)).sum(1)
+    assert np.array_equal(pm.argsort.cpu().numpy(), np.argsort(pmask, kind="stable"))
+    assert np.array_equal(pm.mask_sorted.cpu().numpy(), pmask[np.argsort(pmask, kind="stable")])
     derived = nat.subdivide_neighbors(pm.token_major, npar).token_major
     assert torch.equal(derived, m.token_major)
     tm = m.token_major.cpu().numpy().reshape(n, 27)
