@@ -214,12 +214,19 @@ int spc_compose_rows(spc_stream_t stream, const int32_t* idx, int64_t n, const i
  * Child c = dx*4 + dy*2 + dz of parent p has coords (b, 2x+dx, 2y+dy, 2z+dz)
  * and row p*8+c; with `keep` ([8n] bytes, nonzero = keep) survivors stay in
  * parent-major order.  parent[m] = the parent row of each output row.
- * Outputs sized for 8n rows; synchronises and writes m to *m_out.
+ * Outputs sized for 8n rows; writes the row count m to *m_out.  With
+ * `keep` the call synchronises `stream` (m is read back) and returns the
+ * device-side status (BAD_COORD: a parent coordinate outside [0, 2^14) or
+ * a batch index out of range); without `keep`, m = 8n and the call
+ * synchronises and returns that status only with SPC_MAP_SYNC -- otherwise
+ * it returns once the kernels are queued and the status is read with
+ * spc_read_status on the same workspace (the reference's subdivide,
+ * SP/spatial.py:120-124, checks no range at all).
  * ------------------------------------------------------------------------ */
 size_t spc_subdivide_workspace_bytes(int64_t n);
 int spc_subdivide_map(spc_stream_t stream, const int32_t* coords, int64_t n, const uint8_t* keep,
-                      int32_t* out_coords, int32_t* parent, int64_t* m_out, void* workspace,
-                      size_t workspace_bytes);
+                      uint32_t flags, int32_t* out_coords, int32_t* parent, int64_t* m_out,
+                      void* workspace, size_t workspace_bytes);
 
 /* ------------------------------------------------------------------------
  * Sparse convolution: gather -> implicit GEMM (MFMA) -> store.

@@ -73,7 +73,7 @@ def lib() -> ctypes.CDLL:
                                           _I64, _I64, _I64, _I64, _I64, _P]
     L.spc_subdivide_workspace_bytes.restype = _SZ
     L.spc_subdivide_workspace_bytes.argtypes = [_I64]
-    L.spc_subdivide_map.argtypes = [_P, _P, _I64, _P, _P, _P, _P, _P, _SZ]
+    L.spc_subdivide_map.argtypes = [_P, _P, _I64, _P, _U32, _P, _P, _P, _P, _SZ]
     L.spc_sparse_conv.argtypes = [_P, _INT, _P, _INT, _INT, _P, _P, _P, _P, _P, _INT, _P, _I64,
                                   _I64, _I64, _I64, _I64]
     L.spc_sparse_conv_plan.argtypes = [_P, _INT, _P, _INT, _INT, _P, _P, _P, _P, _P, _INT, _P,
@@ -326,8 +326,12 @@ def stride2_inverse_taps(fine_coords: torch.Tensor, fine_to_coarse: torch.Tensor
     return taps
 
 
-def subdivide_map(coords: torch.Tensor, keep: torch.Tensor | None = None):
-    """Returns (child coords [m,4], parent [m]) in parent-major order."""
+def subdivide_map(coords: torch.Tensor, keep: torch.Tensor | None = None, sync: bool = True):
+    """Returns (child coords [m,4], parent [m]) in parent-major order.  With
+    `keep` the call synchronises (the survivor count comes back) and raises
+    on out-of-range coordinates; without it only when `sync` is set --
+    otherwise it returns once the kernels are queued (m = 8n) and the range
+    check is not reported."""
     _need_gpu(coords, keep)
     coords = coords.contiguous()
     n = coords.shape[0]
@@ -341,8 +345,8 @@ def subdivide_map(coords: torch.Tensor, keep: torch.Tensor | None = None):
         if keep.numel() != 8 * n:
             raise ValueError("keep must have 8*n entries")
     m = ctypes.c_int64(0)
-    st = L.spc_subdivide_map(_stream(dev), _ptr(coords), n, _ptr(keep), _ptr(oc), _ptr(par),
-                             ctypes.byref(m), _ptr(ws), ws.numel())
+    st = L.spc_subdivide_map(_stream(dev), _ptr(coords), n, _ptr(keep), MAP_SYNC if sync else 0,
+                             _ptr(oc), _ptr(par), ctypes.byref(m), _ptr(ws), ws.numel())
     _check("spc_subdivide_map", st)
     return oc[: m.value], par[: m.value]
 

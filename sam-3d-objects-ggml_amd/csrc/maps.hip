@@ -775,8 +775,8 @@ size_t spc_subdivide_workspace_bytes(int64_t n) {
 }
 
 int spc_subdivide_map(spc_stream_t stream, const int32_t* coords, int64_t n, const uint8_t* keep,
-                      int32_t* out_coords, int32_t* parent, int64_t* m_out, void* workspace,
-                      size_t workspace_bytes) {
+                      uint32_t flags, int32_t* out_coords, int32_t* parent, int64_t* m_out,
+                      void* workspace, size_t workspace_bytes) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (n <= 0 || n > INT32_MAX / 8) {
         set_last_error("spc_subdivide_map: n = %lld out of range", (long long)n);
@@ -809,8 +809,14 @@ int spc_subdivide_map(spc_stream_t stream, const int32_t* coords, int64_t n, con
         parent, status);
     SPC_HIP(hipGetLastError());
     int32_t m = (int32_t)m8;
-    if (keep) SPC_HIP(hipMemcpyAsync(&m, total, sizeof(int32_t), hipMemcpyDeviceToHost, s));
-    const int code = read_status_word(s, status);
+    int code = SPC_OK;
+    if (keep) {
+        // the survivor count comes back with the status word (one synchronisation)
+        SPC_HIP(hipMemcpyAsync(&m, total, sizeof(int32_t), hipMemcpyDeviceToHost, s));
+        code = read_status_word(s, status);
+    } else if (flags & SPC_MAP_SYNC) {
+        code = read_status_word(s, status);
+    }
     *m_out = m;
     return code;
 }

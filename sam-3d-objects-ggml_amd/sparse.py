@@ -884,8 +884,11 @@ class SparseSubdivide(nn.Module):
 
     @staticmethod
     def map(input: SparseTensor):
-        """(child coords, parent row of every child)."""
-        return nat.subdivide_map(input.coords.contiguous())
+        """(child coords, parent row of every child).  Queued without a host
+        synchronisation: like the reference's `coords * 2 + offset`
+        (SP/spatial.py:120-124) it reports no out-of-range coordinate here;
+        a map built over the children (spc_map_build, synchronous) does."""
+        return nat.subdivide_map(input.coords.contiguous(), sync=False)
 
     @staticmethod
     def assemble(input: SparseTensor, coords: torch.Tensor, feats: torch.Tensor) -> SparseTensor:

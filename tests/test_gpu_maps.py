@@ -159,6 +159,38 @@ def test_subdivide_unpruned(spc, orc, dev):
     oc, par = spc._native.subdivide_map(torch.from_numpy(c).to(dev))
     assert np.array_equal(oc.cpu().numpy(), ref_c)
     assert np.array_equal(par.cpu().numpy(), ref_p)
+    # queued without the status read-back: the same rows
+    oq, pq = spc._native.subdivide_map(torch.from_numpy(c).to(dev), sync=False)
+    assert np.array_equal(oq.cpu().numpy(), ref_c)
+    assert np.array_equal(pq.cpu().numpy(), ref_p)
+
+
+def test_subdivide_range_status(spc, dev):
+    """A parent coordinate at 2^14 would put children past the 2^15 grid:
+    the synchronising call returns BAD_COORD; the queued one returns OK and
+    leaves BAD_COORD in the workspace's status word for spc_read_status."""
+    import ctypes
+
+    import torch
+
+    nat = spc._native
+    L = nat.lib()
+    _case("subdivide range status")
+    c = torch.tensor([[0, 3, 4, 5], [0, 1 << 14, 2, 2]], dtype=torch.int32, device=dev)
+    with pytest.raises(nat.SparseConvError):
+        nat.subdivide_map(c)
+    oc = torch.empty((16, 4), dtype=torch.int32, device=dev)
+    par = torch.empty(16, dtype=torch.int32, device=dev)
+    ws = torch.empty(L.spc_subdivide_workspace_bytes(2), dtype=torch.uint8, device=dev)
+    m = ctypes.c_int64(0)
+    s = torch.cuda.current_stream(dev).cuda_stream
+    st = L.spc_subdivide_map(ctypes.c_void_p(s), ctypes.c_void_p(c.data_ptr()), 2, None, 0,
+                             ctypes.c_void_p(oc.data_ptr()), ctypes.c_void_p(par.data_ptr()),
+                             ctypes.byref(m), ctypes.c_void_p(ws.data_ptr()), ws.numel())
+    assert st == nat.OK and m.value == 16
+    assert L.spc_read_status(ctypes.c_void_p(s), ctypes.c_void_p(ws.data_ptr())) == nat.BAD_COORD
+    # the in-range parent's children are written all the same
+    assert oc[:8].cpu().tolist() == [[0, 6 + d // 4, 8 + (d // 2) % 2, 10 + d % 2] for d in range(8)]
 
 
 @pytest.mark.parametrize("name", ["sphere64", "ellipsoids4", "ragged_193"])
